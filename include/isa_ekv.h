@@ -1,0 +1,107 @@
+/*
+ * isa_ekv.h - C ABI of the MI355X (gfx950) Flash-EKV LUT CIMLinear library
+ * (libisa_ekv_hip.so).
+ *
+ * Replaces the reference's native boundary for the Transformer FFN hot path:
+ *   - the pybind11 module of src/isa/kernels/transformer_ffn/cuda/binding.cpp:56-62
+ *     (forward, grad_x, grad_x_shared, grad_w, grad_w_shared),
+ *   - the Triton forward launch of src/isa/kernels/transformer_ffn/ekv_lut_triton.py:151-157,
+ *   - the LUT construction of src/isa/approximations/delta_lut.py:12-35.
+ *
+ * Conventions (differences from the reference are deliberate):
+ *   - Plain pointers and sizes; no torch types. All tensors are fp32, row-major,
+ *     contiguous, device memory of the current HIP device; table, gradient and
+ *     workspace pointers must be 16-byte aligned.
+ *   - The caller owns all memory: outputs, tables and workspace are passed in
+ *     (the reference allocated outputs with torch::empty inside the extension).
+ *   - `stream` is a hipStream_t passed as void*; every call only enqueues work on it
+ *     and returns without synchronising.
+ *   - Return value: 0 on success, ISA_EKV_EINVAL (<0) for an invalid argument,
+ *     >0 for a hipError_t. isa_ekv_last_error() returns the calling thread's last
+ *     message (the reference surfaced TORCH_CHECK messages as RuntimeError).
+ *   - Layouts: x [M][K], vth_pos/vth_neg [O][K], grad_out and out [M][O].
+ */
+#ifndef ISA_EKV_H
+#define ISA_EKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ISA_EKV_ABI_VERSION 1
+#define ISA_EKV_EINVAL (-1)
+
+/* LUT layouts produced by isa_ekv_lut_build */
+#define ISA_EKV_LUT_PLAIN_F32 0  /* float table_i[N], then float table_ddelta[N]       */
+#define ISA_EKV_LUT_FWD 1        /* float2 {I, I[i+1]-I[i]} x (N + 2*pad), forward      */
+#define ISA_EKV_LUT_BWD 2        /* float4 {I, dI, D, dD} x (N + 2*pad), backward       */
+#define ISA_EKV_LUT_PLAIN_BF16 3 /* bf16 table_i[N], then bf16 table_ddelta[N]          */
+
+/* ABI version of the loaded library (ISA_EKV_ABI_VERSION). No reference counterpart. */
+int isa_ekv_abi_version(void);
+
+/* Message for the last nonzero return on the calling thread. Stands in for the
+ * TORCH_CHECK messages of ekv_cuda.cu:343-347, :454, :549. */
+const char* isa_ekv_last_error(void);
+
+/* Number of replicated end records on each side of the padded layouts. */
+int isa_ekv_lut_pad(void);
+
+/* Bytes needed by isa_ekv_lut_build for (n_entries, layout); 0 if invalid. */
+size_t isa_ekv_lut_bytes(int n_entries, int layout);
+
+/* Build the Flash-EKV delta-V table on the device.
+ * Replaces delta_lut.py:12-35 (_cpu_lut_cached) and the upload of delta_lut.py:60-62.
+ * params = {n, U_T, I_S, V_D}; entries are evaluated in fp64 on the grid
+ * linspace(delta_min, delta_max, n_entries) and rounded to fp32 (or bf16 RNE for
+ * ISA_EKV_LUT_PLAIN_BF16). V_sat is not part of the table (delta_lut.py:24). */
+int isa_ekv_lut_build(const double params[4], double delta_min, double delta_max, int n_entries, int layout,
+                      void* dst, void* stream);
+
+/* Source dtypes for isa_ekv_lut_pack */
+#define ISA_EKV_DTYPE_F32 0
+#define ISA_EKV_DTYPE_BF16 1
+
+/* Pack plain tables (table_i[N], table_ddelta[N]; fp32, or bf16 widened as the
+ * reference's .float() at cuda_backend.py:68-69) into the padded ISA_EKV_LUT_FWD or
+ * ISA_EKV_LUT_BWD records. Lets cuda_backend.shared_backward accept the reference's
+ * (table_i, table_ddelta) pair (cuda_backend.py:50-62); table_ddelta may be null for FWD. */
+int isa_ekv_lut_pack(const void* table_i, const void* table_ddelta, int n_entries, int src_dtype, int layout,
+                     void* dst, void* stream);
+
+/* Workspace bytes for isa_ekv_forward at this shape. */
+size_t isa_ekv_forward_workspace(int64_t M, int64_t K, int64_t O);
+
+/* out[m,o] = clamp(sum_k (L(x-vth_pos) - L(x-vth_neg)) / (1 + x/v_sat), out_min, out_max)
+ * with L the linear interpolation of table_i (lut_fwd = ISA_EKV_LUT_FWD layout).
+ * Replaces the Triton _forward_kernel launch (ekv_lut_triton.py:37-62, :151-157) and
+ * binding.cpp:57 `forward` (ekv_cuda.cu:351-387). n_entries <= 16384. */
+int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd, int64_t M,
+                    int64_t K, int64_t O, int n_entries, float delta_min, float delta_max, float v_sat,
+                    float out_min, float out_max, float* out, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* Workspace bytes for isa_ekv_backward at this shape and gradient selection. */
+size_t isa_ekv_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x,
+                                  int need_grad_w);
+
+/* grad_x[m,k]   = sum_o G[m,o] ((L_D(d+) - L_D(d-)) r - (L_I(d+) - L_I(d-)) r^2 / v_sat)
+ * grad_vth_pos[o,k] = -sum_m G[m,o] L_D(d+) r,  grad_vth_neg[o,k] = +sum_m G[m,o] L_D(d-) r
+ * with r = 1/(1 + x/v_sat), d+- = x - vth_pos/neg, lut_bwd = ISA_EKV_LUT_BWD layout.
+ * grad_x may be null (no dX); grad_vth_pos and grad_vth_neg are both null or both set.
+ * Replaces binding.cpp:59 `grad_x_shared` (ekv_cuda.cu:193-252, :433-485) and
+ * binding.cpp:61 `grad_w_shared` (ekv_cuda.cu:296-341, :530-574), i.e. the calls made by
+ * cuda_backend.shared_backward (cuda_backend.py:50-99). n_entries <= 8192, as the reference. */
+int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
+                     const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries, float delta_min,
+                     float delta_max, float v_sat, float* grad_x, float* grad_vth_pos, float* grad_vth_neg,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ISA_EKV_H */

@@ -1,0 +1,939 @@
+// Flash-EKV LUT CIMLinear for gfx950 (MI355X): LUT build, forward, backward.
+//
+// The operator (reference: src/isa/kernels/transformer_ffn/ekv_lut_triton.py:25-62
+// and cuda/ekv_cuda.cu:193-341) evaluates, for every (token m, output o, input k),
+//   dV+ = x[m,k] - vth_pos[o,k],  dV- = x[m,k] - vth_neg[o,k]
+//   L(dV) = T[i0] + a * (T[i0+1] - T[i0]),  c = clamp((dV - dmin) * s, 0, N-1),
+//           i0 = trunc(c), a = c - i0,  s = (N-1) / (dmax - dmin)
+//   out[m,o] = clamp(sum_k (L_I(dV+) - L_I(dV-)) * r[m,k], out_min, out_max),
+//           r = 1 / (1 + x / V_sat)
+// and the backward from the derivative table D = dI/ddV:
+//   dX[m,k]   = sum_o G[m,o] * ((L_D(dV+) - L_D(dV-)) * r - (L_I(dV+) - L_I(dV-)) * r^2 / V_sat)
+//   dVth+[o,k] = -sum_m G[m,o] * L_D(dV+) * r
+//   dVth-[o,k] = +sum_m G[m,o] * L_D(dV-) * r
+//
+// MI355X design (one process, one device, caller-owned memory):
+//  * The table lives in LDS as padded, pre-differenced records: forward {I, I[i+1]-I[i]}
+//    (8 B, one ds_read_b64 per branch), backward {I, dI, D, dD} (16 B, one ds_read_b128).
+//    kPad replicated end records on each side reproduce the reference's coordinate clamp
+//    exactly for coordinates within kPad-1 entries of the table range, so a kernel whose
+//    operand ranges fit (checked on device from the prep kernel's range partials) runs a
+//    clamp-free inner loop: sub, cvt_u32, fract, lshl_add, ds_read, fma per branch.
+//  * A prep kernel writes the token-side operands pre-scaled into LUT-index units
+//    (xs = (x - dmin) * s + kPad, r, and -r/V_sat for the backward) and the threshold
+//    operands transposed to [K][O] as {vth_pos * s, vth_neg * s}, padded so the hot loops
+//    carry no bounds tests.
+//  * Lanes run along outputs o: the 64 gathers of one instruction share (m, k), so they
+//    fall inside the narrow window spanned by the thresholds. Token-side operands are
+//    wave-uniform and reach the VALU as SGPR operands (s_load), costing no VGPRs.
+//  * Forward: each wave owns MR tokens x 64*ORR outputs and reduces over K in registers.
+//  * Backward: each wave owns 64*ORR outputs x KR inputs and streams a range of tokens,
+//    keeping dVth accumulators in registers; the per-token dX partial sums over its
+//    outputs are transposed through an LDS buffer and reduced across the wave, then
+//    written as one partial per output block. Two small deterministic reduction kernels
+//    combine the output-block partials (dX) and token-range partials (dVth). No atomics:
+//    every result is bitwise reproducible.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "isa_ekv.h"
+
+namespace {
+
+constexpr int kPad = 16;          // replicated end records on each side of the LDS table
+constexpr int kFwdORR = 4;        // outputs per lane, forward
+constexpr int kBwdORR = 4;        // outputs per lane, backward
+constexpr int kBwdKR = 4;         // inputs per wave, backward
+constexpr int kBwdMB = 4;         // tokens per dX transpose batch, backward
+constexpr int kRedStride = 68;    // floats per slot row in the transpose buffer (64 + pad)
+constexpr int kPrepBlocksX = 128; // prep blocks for the token side
+constexpr int kPrepBlocksW = 128; // prep blocks for the threshold side
+constexpr int kMaxEntriesFwd = 16384;
+constexpr int kMaxEntriesBwd = 8192;
+constexpr int kLdsBytes = 160 * 1024;
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+    return fail(static_cast<int>(err), "%s: %s", what, hipGetErrorString(err));
+}
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// ----------------------------------------------------------------------------------
+// LUT build (reference: src/isa/approximations/delta_lut.py:12-35). Each entry is
+// evaluated in fp64 and rounded once to fp32; slopes are fp32 differences of the
+// rounded entries, so fma(a, T[i+1]-T[i], T[i]) matches ekv_cuda.cu:35 for the fp32 table.
+// ----------------------------------------------------------------------------------
+
+struct DeviceParams {
+    double n, u_t, i_s, v_d;
+    double delta_min, delta_max;
+    int n_entries;
+};
+
+__device__ inline double softplus_ref(double u) {
+    // torch.nn.functional.softplus(beta=1, threshold=20)
+    return u > 20.0 ? u : log1p(exp(u));
+}
+
+__device__ inline double sig_from_sp(double sp) {
+    // flash_transistor.py:27-29: 1 - exp(-sp), or 1 above the softplus threshold
+    return sp > 20.0 ? 1.0 : -expm1(-sp);
+}
+
+__device__ inline void lut_entry(const DeviceParams& p, int j, float* ti, float* td) {
+    const int n = p.n_entries;
+    const double delta =
+        n > 1 ? p.delta_min + (double)j * ((p.delta_max - p.delta_min) / (double)(n - 1))
+              : p.delta_min;
+    const double inv_2nut = 1.0 / (2.0 * p.n * p.u_t);
+    const double sp1 = softplus_ref(delta * inv_2nut);
+    const double sp2 = softplus_ref((delta - p.v_d) * inv_2nut);
+    *ti = (float)(p.i_s * (sp1 * sp1 - sp2 * sp2));
+    *td = (float)(p.i_s * 2.0 * inv_2nut * (sp1 * sig_from_sp(sp1) - sp2 * sig_from_sp(sp2)));
+}
+
+__device__ inline unsigned short f32_to_bf16_rne(float f) {
+    unsigned int u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (unsigned short)(u >> 16);
+}
+
+__global__ void lut_build_kernel(DeviceParams p, int layout, void* dst) {
+    const int n = p.n_entries;
+    const int total = (layout == ISA_EKV_LUT_PLAIN_F32 || layout == ISA_EKV_LUT_PLAIN_BF16)
+                          ? n
+                          : n + 2 * kPad;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    if (layout == ISA_EKV_LUT_PLAIN_F32) {
+        float ti, td;
+        lut_entry(p, idx, &ti, &td);
+        static_cast<float*>(dst)[idx] = ti;
+        static_cast<float*>(dst)[n + idx] = td;
+        return;
+    }
+    if (layout == ISA_EKV_LUT_PLAIN_BF16) {
+        float ti, td;
+        lut_entry(p, idx, &ti, &td);
+        static_cast<unsigned short*>(dst)[idx] = f32_to_bf16_rne(ti);
+        static_cast<unsigned short*>(dst)[n + idx] = f32_to_bf16_rne(td);
+        return;
+    }
+    // padded record idx holds table entry j = idx - kPad, clamped to [0, n-1]; records
+    // outside the interior carry zero slopes so they reproduce the clamped end values
+    const int j = idx - kPad;
+    const int jc = j < 0 ? 0 : (j > n - 1 ? n - 1 : j);
+    float i0, d0;
+    lut_entry(p, jc, &i0, &d0);
+    float si = 0.0f, sd = 0.0f;
+    if (j >= 0 && j < n - 1) {
+        float i1, d1;
+        lut_entry(p, j + 1, &i1, &d1);
+        si = i1 - i0;
+        sd = d1 - d0;
+    }
+    if (layout == ISA_EKV_LUT_FWD) {
+        static_cast<float2*>(dst)[idx] = make_float2(i0, si);
+    } else {
+        static_cast<float4*>(dst)[idx] = make_float4(i0, si, d0, sd);
+    }
+}
+
+// Pack plain tables into the padded records. bf16 sources are widened exactly as the
+// reference's .float() before its CUDA backward (cuda_backend.py:68-69).
+__device__ inline float load_table(const void* t, int i, int bf16) {
+    if (bf16) return __uint_as_float((unsigned int)static_cast<const unsigned short*>(t)[i] << 16);
+    return static_cast<const float*>(t)[i];
+}
+
+__global__ void lut_pack_kernel(const void* ti, const void* td, int n, int src_bf16, int layout, void* dst) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n + 2 * kPad) return;
+    const int j = idx - kPad;
+    const int jc = j < 0 ? 0 : (j > n - 1 ? n - 1 : j);
+    const float i0 = load_table(ti, jc, src_bf16);
+    const float d0 = layout == ISA_EKV_LUT_BWD ? load_table(td, jc, src_bf16) : 0.0f;
+    float si = 0.0f, sd = 0.0f;
+    if (j >= 0 && j < n - 1) {
+        si = load_table(ti, j + 1, src_bf16) - i0;
+        if (layout == ISA_EKV_LUT_BWD) sd = load_table(td, j + 1, src_bf16) - d0;
+    }
+    if (layout == ISA_EKV_LUT_FWD)
+        static_cast<float2*>(dst)[idx] = make_float2(i0, si);
+    else
+        static_cast<float4*>(dst)[idx] = make_float4(i0, si, d0, sd);
+}
+
+// ----------------------------------------------------------------------------------
+// Prep: token side [M][Kp] records and threshold side [Kp][Op] {wp*s, wn*s}, plus
+// per-block (min, max) partials of the pre-scaled coordinates. NaN maps to an
+// infinite partial so the range test fails and the clamping loop runs.
+// ----------------------------------------------------------------------------------
+
+struct PrepArgs {
+    const float* x;
+    const float* wp;
+    const float* wn;
+    int64_t M, K, O, Kp, Op;
+    float delta_min, scale, v_sat;
+    int rec_floats;      // 2: {xs, r}; 4: {xs, r, -r/V_sat, 0}
+    float* xrec;         // [M][Kp][rec_floats]
+    float2* wsT;         // [Kp][Op]
+    float2* partials;    // [kPrepBlocksX + kPrepBlocksW]
+};
+
+__device__ inline void block_minmax(float lo, float hi, float2* out) {
+    __shared__ float s_lo[32], s_hi[32];
+    for (int off = 32; off > 0; off >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, off));
+        hi = fmaxf(hi, __shfl_xor(hi, off));
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) {
+        s_lo[wave] = lo;
+        s_hi[wave] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = blockDim.x >> 6;
+        for (int i = 1; i < nw; ++i) {
+            lo = fminf(lo, s_lo[i]);
+            hi = fmaxf(hi, s_hi[i]);
+        }
+        *out = make_float2(lo, hi);
+    }
+}
+
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
+    float lo = INFINITY, hi = -INFINITY;
+    if (blockIdx.x < kPrepBlocksX) {
+        const int64_t total = a.M * a.Kp;
+        const float pad_coord = (float)kPad + 1.0f;
+        for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+             e += (int64_t)kPrepBlocksX * blockDim.x) {
+            const int64_t m = e / a.Kp;
+            const int64_t k = e - m * a.Kp;
+            float xs, r;
+            if (k < a.K) {
+                const float xv = a.x[m * a.K + k];
+                xs = fmaf(xv - a.delta_min, a.scale, (float)kPad);
+                r = 1.0f / (1.0f + xv / a.v_sat);
+                const bool bad = xs != xs;
+                lo = fminf(lo, bad ? -INFINITY : xs);
+                hi = fmaxf(hi, bad ? INFINITY : xs);
+            } else {
+                xs = pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
+                r = 0.0f;
+            }
+            if (a.rec_floats == 2) {
+                reinterpret_cast<float2*>(a.xrec)[e] = make_float2(xs, r);
+            } else {
+                reinterpret_cast<float4*>(a.xrec)[e] = make_float4(xs, r, -r / a.v_sat, 0.0f);
+            }
+        }
+        block_minmax(lo, hi, &a.partials[blockIdx.x]);
+        return;
+    }
+    // threshold side: 64(o) x 32(k) tiles transposed through LDS
+    __shared__ float2 tile[32][65];
+    const int64_t n_ot = a.Op / 64, n_kt = (a.Kp + 31) / 32;  // Op: multiple of 256; Kp: of 8
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int64_t t = blockIdx.x - kPrepBlocksX; t < n_ot * n_kt; t += kPrepBlocksW) {
+        const int64_t ot = t % n_ot, kt = t / n_ot;
+        // load: rows o (64), cols k (32), coalesced along k
+        for (int rr = ty; rr < 64; rr += 8) {
+            int64_t o = ot * 64 + rr;
+            const int64_t k = kt * 32 + tx;
+            float2 v = make_float2(0.0f, 0.0f);
+            if (k < a.K && a.O > 0) {
+                const bool real = o < a.O;
+                if (!real) o = a.O - 1;  // padded outputs copy a real row; results are dropped
+                const float p = a.wp[o * a.K + k] * a.scale;
+                const float q = a.wn[o * a.K + k] * a.scale;
+                v = make_float2(p, q);
+                if (real) {
+                    const bool bad = (p != p) || (q != q);
+                    lo = fminf(lo, bad ? -INFINITY : fminf(p, q));
+                    hi = fmaxf(hi, bad ? INFINITY : fmaxf(p, q));
+                }
+            }
+            tile[tx][rr] = v;
+        }
+        __syncthreads();
+        // store: rows k (32), cols o (64), coalesced along o
+        for (int rr = ty; rr < 32; rr += 8) {
+            const int64_t k = kt * 32 + rr;
+            if (k < a.Kp) {
+                a.wsT[k * a.Op + ot * 64 + tx] = tile[rr][tx];
+                a.wsT[k * a.Op + ot * 64 + 32 + tx] = tile[rr][32 + tx];
+            }
+        }
+        __syncthreads();
+    }
+    block_minmax(lo, hi, &a.partials[blockIdx.x]);
+}
+
+// Reads the prep partials and decides, identically in every wave, whether every cell
+// coordinate xs - ws lies in [1, NP-2] (then the padded table makes the clamp redundant).
+__device__ inline bool coords_in_padded_range(const float2* __restrict__ partials, int n_pad_entries) {
+    const int lane = threadIdx.x & 63;
+    float xlo = INFINITY, xhi = -INFINITY, wlo = INFINITY, whi = -INFINITY;
+    for (int i = lane; i < kPrepBlocksX; i += 64) {
+        const float2 p = partials[i];
+        xlo = fminf(xlo, p.x);
+        xhi = fmaxf(xhi, p.y);
+    }
+    for (int i = lane; i < kPrepBlocksW; i += 64) {
+        const float2 p = partials[kPrepBlocksX + i];
+        wlo = fminf(wlo, p.x);
+        whi = fmaxf(whi, p.y);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        xlo = fminf(xlo, __shfl_xor(xlo, off));
+        xhi = fmaxf(xhi, __shfl_xor(xhi, off));
+        wlo = fminf(wlo, __shfl_xor(wlo, off));
+        whi = fmaxf(whi, __shfl_xor(whi, off));
+    }
+    const bool ok = (xlo - whi >= 1.0f) && (xhi - wlo <= (float)(n_pad_entries - 2));
+    return __builtin_amdgcn_readfirstlane((int)ok) != 0;
+}
+
+template <bool CLAMP>
+__device__ inline float coord(float xs, float ws, float cmin, float cmax) {
+    float c = xs - ws;
+    if (CLAMP) c = fminf(fmaxf(c, cmin), cmax);  // NaN -> cmin, as fmaxf(NaN, 0) in ekv_cuda.cu:20
+    return c;
+}
+
+// ----------------------------------------------------------------------------------
+// Forward. Block = FWD_WAVES waves sharing one LDS table and one output block of
+// 64*ORR outputs; wave w owns tokens [ (tile_m * FWD_WAVES + w) * MR, +MR ).
+// ----------------------------------------------------------------------------------
+
+struct FwdArgs {
+    const float2* xrec;     // [M][Kp] {xs, r}
+    const float2* wsT;      // [Kp][Op]
+    const float2* lut;      // [NP] {I, dI}
+    const float2* partials;
+    float* out;             // [M][O]
+    int M, O, Kp, Op, NP;
+    int n_mt, n_ot;         // tiles along M (per block) and O
+    float cmin, cmax, out_min, out_max;
+};
+
+template <int MR, int ORR, bool CLAMP>
+__device__ inline void fwd_body(const FwdArgs& a, const float2* lut, int m0, int o_lane) {
+    float acc[MR][ORR];
+#pragma unroll
+    for (int i = 0; i < MR; ++i)
+#pragma unroll
+        for (int j = 0; j < ORR; ++j) acc[i][j] = 0.0f;
+
+    const float2* xrow[MR];
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+        const int m = min(m0 + i, a.M - 1);
+        xrow[i] = a.xrec + (size_t)m * a.Kp;
+    }
+    const float4* wcol = reinterpret_cast<const float4*>(a.wsT + o_lane);
+    const size_t wstride = (size_t)a.Op / 2;  // float4 per k row
+
+    constexpr int KU = 16 / MR;  // 32 SGPRs of token operands per step
+    static_assert(KU >= 1 && 8 % KU == 0, "Kp is a multiple of 8");
+    for (int k0 = 0; k0 < a.Kp; k0 += KU) {
+        float2 w[KU][ORR];
+#pragma unroll
+        for (int kk = 0; kk < KU; ++kk)
+#pragma unroll
+            for (int j = 0; j < ORR / 2; ++j) {
+                const float4 v = wcol[(size_t)(k0 + kk) * wstride + j];
+                w[kk][2 * j] = make_float2(v.x, v.y);
+                w[kk][2 * j + 1] = make_float2(v.z, v.w);
+            }
+#pragma unroll
+        for (int kk = 0; kk < KU; ++kk) {
+#pragma unroll
+            for (int i = 0; i < MR; ++i) {
+                const float2 xv = xrow[i][k0 + kk];
+#pragma unroll
+                for (int j = 0; j < ORR; ++j) {
+                    const float cp = coord<CLAMP>(xv.x, w[kk][j].x, a.cmin, a.cmax);
+                    const float cn = coord<CLAMP>(xv.x, w[kk][j].y, a.cmin, a.cmax);
+                    const float2 ep = lut[(unsigned)cp];
+                    const float2 en = lut[(unsigned)cn];
+                    const float lp = fmaf(__builtin_amdgcn_fractf(cp), ep.y, ep.x);
+                    const float ln = fmaf(__builtin_amdgcn_fractf(cn), en.y, en.x);
+                    acc[i][j] = fmaf(lp - ln, xv.y, acc[i][j]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+        const int m = m0 + i;
+        if (m >= a.M) break;
+        float* orow = a.out + (size_t)m * a.O;
+#pragma unroll
+        for (int j = 0; j < ORR; ++j) {
+            const int o = o_lane + j;
+            if (o < a.O) orow[o] = fminf(fmaxf(acc[i][j], a.out_min), a.out_max);
+        }
+    }
+}
+
+constexpr int kFwdWaves = 8;
+
+template <int MR>
+__global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
+    extern __shared__ float2 s_lut_fwd[];
+    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
+    const bool fast = coords_in_padded_range(a.partials, a.NP);
+    __syncthreads();
+
+    // XCD-aware order: consecutive hardware block ids go round-robin over 8 XCDs; remap so
+    // the blocks of one XCD walk consecutive token tiles of the same output block and share
+    // that output block's threshold columns in their L2.
+    const int nb = gridDim.x;
+    const int bid = blockIdx.x;
+    const int per_xcd = nb / 8;
+    int t = bid;
+    if (per_xcd > 0 && bid < per_xcd * 8) t = (bid % 8) * per_xcd + bid / 8;
+    const int tile_m = t % a.n_mt;
+    const int tile_o = t / a.n_mt;
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int m0 = (tile_m * kFwdWaves + wave) * MR;
+    const int o_lane = tile_o * 64 * kFwdORR + lane * kFwdORR;
+    if (m0 >= a.M) return;
+    if (fast)
+        fwd_body<MR, kFwdORR, false>(a, s_lut_fwd, m0, o_lane);
+    else
+        fwd_body<MR, kFwdORR, true>(a, s_lut_fwd, m0, o_lane);
+}
+
+// ----------------------------------------------------------------------------------
+// Backward. Wave item = (output block ob of 64*ORR outputs, input block kb of KR inputs,
+// token split sp). Each lane keeps dVth accumulators for its ORR x KR (o, k) pairs over
+// the split's tokens; per token, the lane's partial dX over its outputs goes through the
+// transpose buffer and a wave reduction, giving one dX partial per (ob, m, k).
+// ----------------------------------------------------------------------------------
+
+struct BwdArgs {
+    const float4* xrec;     // [M][Kp] {xs, r, -r/V_sat, 0}
+    const float2* wsT;      // [Kp][Op]
+    const float* grad;      // [M][ldg]
+    const float4* lut;      // [NP] {I, dI, D, dD}
+    const float2* partials;
+    float* dx_part;         // [n_ob][M][K]            (need_x)
+    float* dv_part;         // [S][2][Kp][Op]          (need_w)
+    int M, K, O, Kp, Op, ldg, NP;
+    int n_ob, n_kb, n_split, m_chunk;
+    int n_items;
+    float cmin, cmax;
+};
+
+template <bool CLAMP, bool NEED_X, bool NEED_W>
+__device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red, int item) {
+    constexpr int ORR = kBwdORR, KR = kBwdKR, MB = kBwdMB;
+    const int lane = threadIdx.x & 63;
+    const int ob = item % a.n_ob;
+    const int rest = item / a.n_ob;
+    const int kb = rest % a.n_kb;
+    const int sp = rest / a.n_kb;
+    const int o_lane = ob * 64 * ORR + lane * ORR;
+    const int k0 = kb * KR;
+    const int m_begin = sp * a.m_chunk;
+    const int m_end = min(a.M, m_begin + a.m_chunk);
+
+    float2 w[KR][ORR];
+#pragma unroll
+    for (int kk = 0; kk < KR; ++kk) {
+        const float4* src = reinterpret_cast<const float4*>(a.wsT + (size_t)(k0 + kk) * a.Op + o_lane);
+#pragma unroll
+        for (int j = 0; j < ORR / 2; ++j) {
+            const float4 v = src[j];
+            w[kk][2 * j] = make_float2(v.x, v.y);
+            w[kk][2 * j + 1] = make_float2(v.z, v.w);
+        }
+    }
+    float accp[KR][ORR], accn[KR][ORR];
+#pragma unroll
+    for (int kk = 0; kk < KR; ++kk)
+#pragma unroll
+        for (int j = 0; j < ORR; ++j) accp[kk][j] = accn[kk][j] = 0.0f;
+
+    // transpose-buffer reduction role of this lane: slot = lane / 4, quarter = lane % 4
+    const int my_slot = lane >> 2;
+    const int my_quarter = lane & 3;
+
+    for (int mb = m_begin; mb < m_end; mb += MB) {
+#pragma unroll 1
+        for (int s = 0; s < MB; ++s) {
+            const int m = mb + s;
+            float tv[KR];
+            if (m < m_end) {
+                const float4 g4 = *reinterpret_cast<const float4*>(a.grad + (size_t)m * a.ldg + o_lane);
+                const float g[4] = {g4.x, g4.y, g4.z, g4.w};
+                const float4* xr = a.xrec + (size_t)m * a.Kp + k0;
+#pragma unroll
+                for (int kk = 0; kk < KR; ++kk) {
+                    const float4 xv = xr[kk];
+                    float x1 = 0.0f, x2 = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < ORR; ++j) {
+                        const float cp = coord<CLAMP>(xv.x, w[kk][j].x, a.cmin, a.cmax);
+                        const float cn = coord<CLAMP>(xv.x, w[kk][j].y, a.cmin, a.cmax);
+                        const float4 ep = lut[(unsigned)cp];
+                        const float4 en = lut[(unsigned)cn];
+                        const float ap = __builtin_amdgcn_fractf(cp);
+                        const float an = __builtin_amdgcn_fractf(cn);
+                        const float dp = fmaf(ap, ep.w, ep.z);
+                        const float dn = fmaf(an, en.w, en.z);
+                        const float gr = g[j] * xv.y;
+                        if (NEED_X) {
+                            const float lp = fmaf(ap, ep.y, ep.x);
+                            const float ln = fmaf(an, en.y, en.x);
+                            x1 = fmaf(gr, dp - dn, x1);
+                            x2 = fmaf(gr, lp - ln, x2);
+                        }
+                        if (NEED_W) {
+                            accp[kk][j] = fmaf(gr, dp, accp[kk][j]);
+                            accn[kk][j] = fmaf(gr, dn, accn[kk][j]);
+                        }
+                    }
+                    tv[kk] = fmaf(x2, xv.z, x1);  // r*sum(G dL') - r^2/V_sat*sum(G dL)
+                    // keep one input's gathers in flight at a time: bounds register pressure
+                    // to the 128 VGPRs of a 16-wave block; other waves hide the LDS latency
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < KR; ++kk) tv[kk] = 0.0f;
+            }
+            if (NEED_X) {
+#pragma unroll
+                for (int kk = 0; kk < KR; ++kk) red[(s * KR + kk) * kRedStride + lane] = tv[kk];
+            }
+        }
+        if (NEED_X) {
+            // all 64 lanes of this wave wrote MB*KR slots; LDS ops of one wave complete in
+            // order, so only a compiler barrier is needed before reading other lanes' values
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const float4* row = reinterpret_cast<const float4*>(red + my_slot * kRedStride + my_quarter * 16);
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = row[q];
+                sum += (v.x + v.y) + (v.z + v.w);
+            }
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            const int m = mb + my_slot / KR;
+            const int k = k0 + my_slot % KR;
+            if (my_quarter == 0 && m < m_end && k < a.K)
+                a.dx_part[((size_t)ob * a.M + m) * a.K + k] = sum;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+    if (NEED_W) {
+        float* dst_p = a.dv_part + (size_t)sp * 2 * a.Kp * a.Op;
+        float* dst_n = dst_p + (size_t)a.Kp * a.Op;
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) {
+            float4* pp = reinterpret_cast<float4*>(dst_p + (size_t)(k0 + kk) * a.Op + o_lane);
+            float4* pn = reinterpret_cast<float4*>(dst_n + (size_t)(k0 + kk) * a.Op + o_lane);
+            *pp = make_float4(accp[kk][0], accp[kk][1], accp[kk][2], accp[kk][3]);
+            *pn = make_float4(accn[kk][0], accn[kk][1], accn[kk][2], accn[kk][3]);
+        }
+    }
+}
+
+template <bool NEED_X, bool NEED_W>
+__global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
+    extern __shared__ float4 s_lut_bwd[];
+    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_bwd[i] = a.lut[i];
+    const bool fast = coords_in_padded_range(a.partials, a.NP);
+    __syncthreads();
+    const int waves = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* red = reinterpret_cast<float*>(s_lut_bwd + a.NP) + wave * (kBwdMB * kBwdKR * kRedStride);
+    const int item = blockIdx.x * waves + wave;
+    if (item >= a.n_items) return;
+    if (fast)
+        bwd_body<false, NEED_X, NEED_W>(a, s_lut_bwd, red, item);
+    else
+        bwd_body<true, NEED_X, NEED_W>(a, s_lut_bwd, red, item);
+}
+
+// dX[m,k] = sum over output blocks, in block order (deterministic)
+__global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict__ part, int n_ob,
+                                                        int64_t n, float* __restrict__ dx) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        float s = part[e];
+        for (int b = 1; b < n_ob; ++b) s += part[(size_t)b * n + e];
+        dx[e] = s;
+    }
+}
+
+// dVth+[o,k] = -sum_s P[s][0][k][o], dVth-[o,k] = +sum_s P[s][1][k][o]; 32x32 transpose tiles
+__global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict__ part, int n_split,
+                                                        int K, int O, int Kp, int Op,
+                                                        float* __restrict__ dvp, float* __restrict__ dvn) {
+    __shared__ float tile[2][32][33];
+    const int n_ot = (O + 31) / 32, n_kt = (K + 31) / 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    const size_t plane = (size_t)Kp * Op;
+    for (int t = blockIdx.x; t < n_ot * n_kt; t += gridDim.x) {
+        const int ot = t % n_ot, kt = t / n_ot;
+        for (int rr = ty; rr < 32; rr += 8) {
+            const int k = kt * 32 + rr, o = ot * 32 + tx;
+            float sp = 0.0f, sn = 0.0f;
+            if (k < K && o < O) {
+                const size_t e = (size_t)k * Op + o;
+                for (int s = 0; s < n_split; ++s) {
+                    sp += part[(size_t)s * 2 * plane + e];
+                    sn += part[(size_t)s * 2 * plane + plane + e];
+                }
+            }
+            tile[0][rr][tx] = -sp;
+            tile[1][rr][tx] = sn;
+        }
+        __syncthreads();
+        for (int rr = ty; rr < 32; rr += 8) {
+            const int o = ot * 32 + rr, k = kt * 32 + tx;
+            if (o < O && k < K) {
+                dvp[(size_t)o * K + k] = tile[0][tx][rr];
+                dvn[(size_t)o * K + k] = tile[1][tx][rr];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------------------------
+// Host-side planning shared by the workspace queries and the launches.
+// ----------------------------------------------------------------------------------
+
+struct FwdPlan {
+    int64_t Kp, Op;
+    int mr, n_mt, n_ot, blocks;
+    size_t off_xrec, off_wsT, off_part, bytes;
+};
+
+FwdPlan plan_forward(int64_t M, int64_t K, int64_t O) {
+    FwdPlan p{};
+    p.Kp = round_up(K > 0 ? K : 1, 8);
+    p.Op = round_up(O > 0 ? O : 1, 64 * kFwdORR);
+    p.n_ot = (int)(p.Op / (64 * kFwdORR));
+    // choose tokens per wave so the grid covers the chip several times over
+    const int64_t waves_target = 3 * 256 * 16;
+    p.mr = 8;
+    while (p.mr > 2 && ((M + p.mr - 1) / p.mr) * p.n_ot < waves_target) p.mr /= 2;
+    const int64_t tokens_per_block = (int64_t)kFwdWaves * p.mr;
+    p.n_mt = (int)((M + tokens_per_block - 1) / tokens_per_block);
+    p.blocks = p.n_mt * p.n_ot;
+    size_t off = 0;
+    p.off_xrec = off;
+    off += (size_t)round_up((int64_t)M * p.Kp * 8, 256);
+    p.off_wsT = off;
+    off += (size_t)round_up(p.Kp * p.Op * 8, 256);
+    p.off_part = off;
+    off += (size_t)(kPrepBlocksX + kPrepBlocksW) * 8;
+    p.bytes = round_up((int64_t)off, 256);
+    return p;
+}
+
+struct BwdPlan {
+    int64_t Kp, Op;
+    int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
+    bool grad_padded;
+    size_t off_xrec, off_wsT, off_part, off_gpad, off_dx, off_dv, bytes, lds_bytes;
+};
+
+BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_x, bool need_w) {
+    BwdPlan p{};
+    p.Kp = round_up(K > 0 ? K : 1, 8);
+    p.Op = round_up(O > 0 ? O : 1, 64 * kBwdORR);
+    p.n_ob = (int)(p.Op / (64 * kBwdORR));
+    p.n_kb = (int)(p.Kp / kBwdKR);
+    const int np = n_entries + 2 * kPad;
+    const size_t red_bytes = (size_t)kBwdMB * kBwdKR * kRedStride * 4;
+    const size_t lut_bytes = (size_t)np * 16;
+    int wpb = 16;
+    while (wpb > 1 && lut_bytes + wpb * red_bytes > (size_t)kLdsBytes) wpb /= 2;
+    p.waves_per_block = wpb;
+    p.lds_bytes = lut_bytes + (size_t)wpb * red_bytes;
+    // token splits: enough wave items to cover the chip several times over
+    const int64_t base_items = (int64_t)p.n_ob * p.n_kb;
+    const int64_t target = 3 * 256 * 16;
+    int64_t splits = (target + base_items - 1) / base_items;
+    const int64_t max_splits = (M + 63) / 64;  // keep at least 64 tokens per split
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    p.m_chunk = (int)round_up((M + splits - 1) / splits, kBwdMB);
+    if (p.m_chunk < kBwdMB) p.m_chunk = kBwdMB;
+    p.n_split = (int)((M + p.m_chunk - 1) / p.m_chunk);
+    if (p.n_split < 1) p.n_split = 1;
+    p.n_items = (int)(base_items * p.n_split);
+    p.blocks = (p.n_items + wpb - 1) / wpb;
+    p.grad_padded = (O % (64 * kBwdORR)) != 0;
+    size_t off = 0;
+    p.off_xrec = off;
+    off += (size_t)round_up((int64_t)M * p.Kp * 16, 256);
+    p.off_wsT = off;
+    off += (size_t)round_up(p.Kp * p.Op * 8, 256);
+    p.off_part = off;
+    off += (size_t)round_up((kPrepBlocksX + kPrepBlocksW) * 8, 256);
+    p.off_gpad = off;
+    if (p.grad_padded) off += (size_t)round_up((int64_t)M * p.Op * 4, 256);
+    p.off_dx = off;
+    if (need_x) off += (size_t)round_up((int64_t)p.n_ob * M * (K > 0 ? K : 1) * 4, 256);
+    p.off_dv = off;
+    if (need_w) off += (size_t)round_up((int64_t)p.n_split * 2 * p.Kp * p.Op * 4, 256);
+    p.bytes = round_up((int64_t)off, 256);
+    return p;
+}
+
+__global__ __launch_bounds__(256) void pad_grad_kernel(const float* __restrict__ g, int64_t M, int64_t O,
+                                                       int64_t Op, float* __restrict__ gp) {
+    const int64_t total = M * Op;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = e / Op, o = e - m * Op;
+        gp[e] = o < O ? g[m * O + o] : 0.0f;  // padded outputs contribute nothing to dX
+    }
+}
+
+int check_common(const float* x, const float* wp, const float* wn, const void* lut, int64_t M, int64_t K,
+                 int64_t O, int n_entries, float delta_min, float delta_max, float v_sat) {
+    if (M < 0 || K < 0 || O < 0) return fail(ISA_EKV_EINVAL, "negative shape (M=%lld, K=%lld, O=%lld)",
+                                             (long long)M, (long long)K, (long long)O);
+    if (M > INT32_MAX / 2 || K > INT32_MAX / 2 || O > INT32_MAX / 2)
+        return fail(ISA_EKV_EINVAL, "shape too large for 32-bit tile indices");
+    if (n_entries < 1) return fail(ISA_EKV_EINVAL, "LUT_DELTA_SIZE must be >= 1 (got %d)", n_entries);
+    if (!(delta_max > delta_min)) return fail(ISA_EKV_EINVAL, "LUT range must satisfy delta_max > delta_min");
+    if (!(v_sat != 0.0f)) return fail(ISA_EKV_EINVAL, "V_sat must be nonzero");
+    if (M * K > 0 && !x) return fail(ISA_EKV_EINVAL, "x is null");
+    if (O * K > 0 && (!wp || !wn)) return fail(ISA_EKV_EINVAL, "vth_pos/vth_neg is null");
+    if (!lut) return fail(ISA_EKV_EINVAL, "lut is null");
+    return 0;
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------------------------
+// C ABI
+// ----------------------------------------------------------------------------------
+
+extern "C" {
+
+int isa_ekv_abi_version(void) { return ISA_EKV_ABI_VERSION; }
+
+const char* isa_ekv_last_error(void) { return g_last_error; }
+
+int isa_ekv_lut_pad(void) { return kPad; }
+
+size_t isa_ekv_lut_bytes(int n_entries, int layout) {
+    if (n_entries < 1) return 0;
+    switch (layout) {
+        case ISA_EKV_LUT_PLAIN_F32: return (size_t)n_entries * 2 * 4;
+        case ISA_EKV_LUT_PLAIN_BF16: return (size_t)n_entries * 2 * 2;
+        case ISA_EKV_LUT_FWD: return (size_t)(n_entries + 2 * kPad) * 8;
+        case ISA_EKV_LUT_BWD: return (size_t)(n_entries + 2 * kPad) * 16;
+        default: return 0;
+    }
+}
+
+int isa_ekv_lut_build(const double params[4], double delta_min, double delta_max, int n_entries, int layout,
+                      void* dst, void* stream) {
+    if (!params) return fail(ISA_EKV_EINVAL, "params is null");
+    if (!dst) return fail(ISA_EKV_EINVAL, "dst is null");
+    if (n_entries < 1) return fail(ISA_EKV_EINVAL, "LUT_DELTA_SIZE must be >= 1 (got %d)", n_entries);
+    if (!(delta_max > delta_min)) return fail(ISA_EKV_EINVAL, "LUT range must satisfy delta_max > delta_min");
+    if (isa_ekv_lut_bytes(n_entries, layout) == 0) return fail(ISA_EKV_EINVAL, "unknown LUT layout %d", layout);
+    if (!(params[0] > 0.0) || !(params[1] > 0.0))
+        return fail(ISA_EKV_EINVAL, "n and U_T must be positive");
+    DeviceParams p{params[0], params[1], params[2], params[3], delta_min, delta_max, n_entries};
+    const int total = (layout == ISA_EKV_LUT_PLAIN_F32 || layout == ISA_EKV_LUT_PLAIN_BF16)
+                          ? n_entries
+                          : n_entries + 2 * kPad;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(lut_build_kernel, dim3((total + 255) / 256), dim3(256), 0, s, p, layout, dst);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "lut_build launch");
+    return 0;
+}
+
+int isa_ekv_lut_pack(const void* table_i, const void* table_ddelta, int n_entries, int src_dtype, int layout,
+                     void* dst, void* stream) {
+    if (!table_i || !dst) return fail(ISA_EKV_EINVAL, "table_i/dst is null");
+    if (layout == ISA_EKV_LUT_BWD && !table_ddelta) return fail(ISA_EKV_EINVAL, "table_ddelta is null");
+    if (n_entries < 1) return fail(ISA_EKV_EINVAL, "LUT_DELTA_SIZE must be >= 1 (got %d)", n_entries);
+    if (layout != ISA_EKV_LUT_FWD && layout != ISA_EKV_LUT_BWD)
+        return fail(ISA_EKV_EINVAL, "pack layout must be ISA_EKV_LUT_FWD or ISA_EKV_LUT_BWD (got %d)", layout);
+    if (src_dtype != ISA_EKV_DTYPE_F32 && src_dtype != ISA_EKV_DTYPE_BF16)
+        return fail(ISA_EKV_EINVAL, "unknown table dtype %d", src_dtype);
+    const int total = n_entries + 2 * kPad;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(lut_pack_kernel, dim3((total + 255) / 256), dim3(256), 0, s, table_i, table_ddelta, n_entries,
+                       src_dtype == ISA_EKV_DTYPE_BF16 ? 1 : 0, layout, dst);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "lut_pack launch");
+    return 0;
+}
+
+size_t isa_ekv_forward_workspace(int64_t M, int64_t K, int64_t O) {
+    if (M < 0 || K < 0 || O < 0) return 0;
+    return plan_forward(M, K, O).bytes;
+}
+
+int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd, int64_t M,
+                    int64_t K, int64_t O, int n_entries, float delta_min, float delta_max, float v_sat,
+                    float out_min, float out_max, float* out, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+    int rc = check_common(x, vth_pos, vth_neg, lut_fwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
+    if (rc) return rc;
+    if (n_entries > kMaxEntriesFwd)
+        return fail(ISA_EKV_EINVAL, "LDS-resident forward supports LUT_DELTA_SIZE <= %d (got %d)",
+                    kMaxEntriesFwd, n_entries);
+    if (M == 0 || O == 0) return 0;
+    if (!out) return fail(ISA_EKV_EINVAL, "out is null");
+    const FwdPlan p = plan_forward(M, K, O);
+    if (!workspace || workspace_bytes < p.bytes)
+        return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    const double scale_d = n_entries > 1 ? (double)(n_entries - 1) / ((double)delta_max - (double)delta_min) : 0.0;
+    PrepArgs pa{x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, delta_min, (float)scale_d, v_sat, 2,
+                reinterpret_cast<float*>(ws + p.off_xrec), reinterpret_cast<float2*>(ws + p.off_wsT),
+                reinterpret_cast<float2*>(ws + p.off_part)};
+    hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "forward prep launch");
+    const int np = n_entries + 2 * kPad;
+    FwdArgs fa{reinterpret_cast<const float2*>(ws + p.off_xrec), reinterpret_cast<const float2*>(ws + p.off_wsT),
+               static_cast<const float2*>(lut_fwd), reinterpret_cast<const float2*>(ws + p.off_part), out,
+               (int)M, (int)O, (int)p.Kp, (int)p.Op, np, p.n_mt, p.n_ot,
+               (float)kPad, (float)(kPad + n_entries - 1), out_min, out_max};
+    const size_t lds = (size_t)np * 8;
+    switch (p.mr) {
+        case 8: hipLaunchKernelGGL(fwd_kernel<8>, dim3(p.blocks), dim3(kFwdWaves * 64), lds, s, fa); break;
+        case 4: hipLaunchKernelGGL(fwd_kernel<4>, dim3(p.blocks), dim3(kFwdWaves * 64), lds, s, fa); break;
+        default: hipLaunchKernelGGL(fwd_kernel<2>, dim3(p.blocks), dim3(kFwdWaves * 64), lds, s, fa); break;
+    }
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "forward launch");
+    return 0;
+}
+
+size_t isa_ekv_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x,
+                                  int need_grad_w) {
+    if (M < 0 || K < 0 || O < 0 || n_entries < 1) return 0;
+    return plan_backward(M, K, O, n_entries, need_grad_x != 0, need_grad_w != 0).bytes;
+}
+
+int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
+                     const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries, float delta_min,
+                     float delta_max, float v_sat, float* grad_x, float* grad_vth_pos, float* grad_vth_neg,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_common(x, vth_pos, vth_neg, lut_bwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
+    if (rc) return rc;
+    if (n_entries > kMaxEntriesBwd)
+        return fail(ISA_EKV_EINVAL, "shared backward supports LUT_DELTA_SIZE <= %d", kMaxEntriesBwd);
+    const bool need_x = grad_x != nullptr;
+    const bool need_w = grad_vth_pos != nullptr || grad_vth_neg != nullptr;
+    if (need_w && (grad_vth_pos == nullptr || grad_vth_neg == nullptr))
+        return fail(ISA_EKV_EINVAL, "grad_vth_pos and grad_vth_neg must both be given or both be null");
+    if (!need_x && !need_w) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t err;
+    // degenerate shapes: empty reductions give zero gradients
+    if (M == 0 || O == 0 || K == 0) {
+        if (need_x && M * K > 0) {
+            err = hipMemsetAsync(grad_x, 0, (size_t)(M * K) * 4, s);
+            if (err != hipSuccess) return hip_fail(err, "grad_x zero fill");
+        }
+        if (need_w && O * K > 0) {
+            err = hipMemsetAsync(grad_vth_pos, 0, (size_t)(O * K) * 4, s);
+            if (err == hipSuccess) err = hipMemsetAsync(grad_vth_neg, 0, (size_t)(O * K) * 4, s);
+            if (err != hipSuccess) return hip_fail(err, "grad_vth zero fill");
+        }
+        return 0;
+    }
+    if (!grad_out) return fail(ISA_EKV_EINVAL, "grad_out is null");
+    const BwdPlan p = plan_backward(M, K, O, n_entries, need_x, need_w);
+    if (!workspace || workspace_bytes < p.bytes)
+        return fail(ISA_EKV_EINVAL, "backward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
+    char* ws = static_cast<char*>(workspace);
+    const double scale_d = n_entries > 1 ? (double)(n_entries - 1) / ((double)delta_max - (double)delta_min) : 0.0;
+    PrepArgs pa{x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, delta_min, (float)scale_d, v_sat, 4,
+                reinterpret_cast<float*>(ws + p.off_xrec), reinterpret_cast<float2*>(ws + p.off_wsT),
+                reinterpret_cast<float2*>(ws + p.off_part)};
+    hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "backward prep launch");
+    const float* g = grad_out;
+    int ldg = (int)O;
+    if (p.grad_padded) {
+        float* gp = reinterpret_cast<float*>(ws + p.off_gpad);
+        hipLaunchKernelGGL(pad_grad_kernel, dim3(1024), dim3(256), 0, s, grad_out, M, O, p.Op, gp);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "grad pad launch");
+        g = gp;
+        ldg = (int)p.Op;
+    }
+    const int np = n_entries + 2 * kPad;
+    BwdArgs ba{reinterpret_cast<const float4*>(ws + p.off_xrec), reinterpret_cast<const float2*>(ws + p.off_wsT),
+               g, static_cast<const float4*>(lut_bwd), reinterpret_cast<const float2*>(ws + p.off_part),
+               reinterpret_cast<float*>(ws + p.off_dx), reinterpret_cast<float*>(ws + p.off_dv),
+               (int)M, (int)K, (int)O, (int)p.Kp, (int)p.Op, ldg, np,
+               p.n_ob, p.n_kb, p.n_split, p.m_chunk, p.n_items,
+               (float)kPad, (float)(kPad + n_entries - 1)};
+    const dim3 grid(p.blocks), block(p.waves_per_block * 64);
+    if (need_x && need_w)
+        hipLaunchKernelGGL((bwd_kernel<true, true>), grid, block, p.lds_bytes, s, ba);
+    else if (need_x)
+        hipLaunchKernelGGL((bwd_kernel<true, false>), grid, block, p.lds_bytes, s, ba);
+    else
+        hipLaunchKernelGGL((bwd_kernel<false, true>), grid, block, p.lds_bytes, s, ba);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "backward launch");
+    if (need_x) {
+        hipLaunchKernelGGL(dx_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dx),
+                           p.n_ob, M * K, grad_x);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
+    }
+    if (need_w) {
+        hipLaunchKernelGGL(dv_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dv),
+                           p.n_split, (int)K, (int)O, (int)p.Kp, (int)p.Op, grad_vth_pos, grad_vth_neg);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "dv reduce launch");
+    }
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,108 @@
+"""ctypes binding of libisa_ekv_hip.so (declared in include/isa_ekv.h).
+
+The library is the only compute path: loading fails loudly when it is missing or was
+built for another ABI. ``torch`` is imported first so the library binds to the HIP
+runtime torch already loaded (both carry the soname libamdhip64.so.7).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime the library must share)
+
+ABI_VERSION = 1
+LIB_NAME = "libisa_ekv_hip.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+
+LUT_PLAIN_F32 = 0
+LUT_FWD = 1
+LUT_BWD = 2
+LUT_PLAIN_BF16 = 3
+
+EXPORTS = (
+    "isa_ekv_abi_version",
+    "isa_ekv_last_error",
+    "isa_ekv_lut_pad",
+    "isa_ekv_lut_bytes",
+    "isa_ekv_lut_build",
+    "isa_ekv_lut_pack",
+    "isa_ekv_forward_workspace",
+    "isa_ekv_forward",
+    "isa_ekv_backward_workspace",
+    "isa_ekv_backward",
+)
+
+_lock = threading.Lock()
+_lib = None
+
+
+class HipExtensionError(RuntimeError):
+    pass
+
+
+def _declare(lib) -> None:
+    vp = ctypes.c_void_p
+    i64 = ctypes.c_int64
+    f32 = ctypes.c_float
+    f64 = ctypes.c_double
+    ci = ctypes.c_int
+    sz = ctypes.c_size_t
+    lib.isa_ekv_abi_version.argtypes = []
+    lib.isa_ekv_abi_version.restype = ci
+    lib.isa_ekv_last_error.argtypes = []
+    lib.isa_ekv_last_error.restype = ctypes.c_char_p
+    lib.isa_ekv_lut_pad.argtypes = []
+    lib.isa_ekv_lut_pad.restype = ci
+    lib.isa_ekv_lut_bytes.argtypes = [ci, ci]
+    lib.isa_ekv_lut_bytes.restype = sz
+    lib.isa_ekv_lut_build.argtypes = [ctypes.POINTER(f64), f64, f64, ci, ci, vp, vp]
+    lib.isa_ekv_lut_build.restype = ci
+    lib.isa_ekv_lut_pack.argtypes = [vp, vp, ci, ci, ci, vp, vp]
+    lib.isa_ekv_lut_pack.restype = ci
+    lib.isa_ekv_forward_workspace.argtypes = [i64, i64, i64]
+    lib.isa_ekv_forward_workspace.restype = sz
+    lib.isa_ekv_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, f32, f32, vp, vp, sz, vp]
+    lib.isa_ekv_forward.restype = ci
+    lib.isa_ekv_backward_workspace.argtypes = [i64, i64, i64, ci, ci, ci]
+    lib.isa_ekv_backward_workspace.restype = sz
+    lib.isa_ekv_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, vp, vp, vp, vp, sz, vp]
+    lib.isa_ekv_backward.restype = ci
+
+
+def load(path: Path | None = None):
+    """Load and cache the library; raise HipExtensionError if it is absent or mismatched."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise HipExtensionError(
+                f"{LIB_NAME} not found at {p}; build it with `python isa-_amd/csrc/build.py` "
+                "(or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(str(p))
+        missing = [name for name in EXPORTS if not hasattr(lib, name)]
+        if missing:
+            raise HipExtensionError(f"{p} lacks exports {missing}")
+        _declare(lib)
+        version = lib.isa_ekv_abi_version()
+        if version != ABI_VERSION:
+            raise HipExtensionError(f"{p} has ABI version {version}, expected {ABI_VERSION}; rebuild it")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise RuntimeError carrying the library's message for a nonzero status."""
+    if rc != 0:
+        msg = load().isa_ekv_last_error()
+        text = msg.decode("utf-8", "replace") if msg else ""
+        raise RuntimeError(f"{what} failed ({rc}): {text}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

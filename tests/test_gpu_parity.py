@@ -1,0 +1,180 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Gates (norm-wise max|d|/max|ref|, against the fp32-table LUT oracle): forward <= 1e-4,
+dX and dVth+- <= 1e-3. Elementwise relative error (floor 1e-3 * max|ref|) is printed.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests.helpers import errs, flash_cfg, make_inputs, oracle_all
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-4
+BWD_TOL = 1e-3
+
+
+def _dev_run(x, vp, vn, grad, cfg, dev, need_x=True, need_w=True, out_min=-4.0, out_max=4.0):
+    from isa.approximations.delta_lut import get_packed_tables, lut_range
+    from isa.kernels.transformer_ffn import ops
+
+    dmin, dmax, n = lut_range(cfg)
+    fwd, bwd = get_packed_tables(cfg, dev)
+    xd, pd, nd, gd = (t.to(dev) for t in (x, vp, vn, grad))
+    out = ops.lut_forward(xd, pd, nd, fwd, n, dmin, dmax, cfg["V_sat"], out_min, out_max)
+    gx, gp, gn = ops.lut_backward(xd, pd, nd, gd, bwd, n, dmin, dmax, cfg["V_sat"], need_x, need_w)
+    torch.cuda.synchronize()
+    return out, gx, gp, gn
+
+
+SHAPES = [
+    (1, 1, 1),
+    (17, 27, 13),      # reference GPU tile test shape (test_exact_direct_conv.py:137-140)
+    (31, 67, 19),      # (test_exact_direct_conv.py:167-171)
+    (5, 8, 256),
+    (70, 129, 300),    # ragged in every dimension
+    (64, 192, 768),
+    (520, 192, 768),   # config 1: ViT-S up-projection, full size
+]
+
+
+@pytest.mark.parametrize("M,K,O", SHAPES)
+def test_forward_backward_parity(cuda_device, M, K, O):
+    print(f"[case] parity M={M} K={K} O={O}", flush=True)
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = make_inputs(M, K, O, seed=M * 7 + K)
+    ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg)
+    out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    e = {"fwd": errs(out, ref_out), "dX": errs(gx, ref_dx), "dVth+": errs(gp, ref_gp), "dVth-": errs(gn, ref_gn)}
+    print({k: f"{v[0]:.2e}/{v[1]:.2e}" for k, v in e.items()})
+    assert e["fwd"][0] <= FWD_TOL
+    assert e["dX"][0] <= BWD_TOL and e["dVth+"][0] <= BWD_TOL and e["dVth-"][0] <= BWD_TOL
+
+
+@pytest.mark.parametrize("x_mode,vth_mode", [("signed", "full"), ("wide", "wide"), ("mapped", "full")])
+def test_parity_input_ranges(cuda_device, x_mode, vth_mode):
+    """fc2-like signed inputs, trained-like thresholds, and out-of-table coordinates (clamping loop)."""
+    print(f"[case] ranges {x_mode}/{vth_mode}", flush=True)
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = make_inputs(96, 160, 320, seed=3, x_mode=x_mode, vth_mode=vth_mode)
+    ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
+    out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf)
+    e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
+    print([f"{v:.2e}" for v in e])
+    assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL
+
+
+@pytest.mark.parametrize("size", [257, 1024, 8192])
+def test_parity_table_sizes(cuda_device, size):
+    print(f"[case] table size {size}", flush=True)
+    cfg = flash_cfg(size)
+    x, vp, vn, g = make_inputs(48, 96, 256, seed=size)
+    ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg)
+    out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    assert errs(out, ref_out)[0] <= FWD_TOL
+    assert max(errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]) <= BWD_TOL
+
+
+def test_forward_16384_entries(cuda_device):
+    """The forward keeps the reference's fallback LUT size (delta_lut.py:48) resident in LDS."""
+    cfg = flash_cfg(16384)
+    x, vp, vn, g = make_inputs(40, 64, 256, seed=11)
+    dmin, dmax, n = oracle.lut_range(cfg)
+    ti, _ = oracle.lut_tables(cfg)
+    ref = oracle.forward(x.numpy(), vp.numpy(), vn.numpy(), ti, dmin, dmax, cfg["V_sat"])
+    from isa.kernels.transformer_ffn.ekv_lut_triton import triton_lut_ekv_matmul
+
+    out = triton_lut_ekv_matmul(x.to(cuda_device), vp.to(cuda_device), vn.to(cuda_device), cfg)
+    assert errs(out, ref)[0] <= FWD_TOL
+
+
+def test_gradient_subsets(cuda_device):
+    """need_grad_x / need_grad_w alone give the same values as both together."""
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = make_inputs(64, 72, 256, seed=5)
+    _, gx_all, gp_all, gn_all = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    _, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, need_x=True, need_w=False)
+    assert gp is None and gn is None
+    assert torch.equal(gx, gx_all)
+    _, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, need_x=False, need_w=True)
+    assert gx is None
+    assert torch.equal(gp, gp_all) and torch.equal(gn, gn_all)
+
+
+def test_bitwise_determinism(cuda_device):
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = make_inputs(200, 192, 512, seed=9)
+    a = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    b = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_invariants_on_device(cuda_device):
+    """vth_pos == vth_neg gives exactly zero Idiff and dX, and dVth+ == -dVth-."""
+    cfg = flash_cfg(4096)
+    x, vp, _, g = make_inputs(33, 50, 70, seed=2)
+    out, gx, gp, gn = _dev_run(x, vp, vp.clone(), g, cfg, cuda_device)
+    assert torch.count_nonzero(out) == 0
+    assert torch.count_nonzero(gx) == 0
+    assert torch.equal(gp, -gn)
+
+
+def test_nan_semantics(cuda_device):
+    """NaN x: r is NaN so its cells are NaN and the NaN row sum clamps to out_min (fminf/fmaxf);
+    NaN vth reads table entry 0 like ekv_cuda.cu:19-21. Same rules as the oracle."""
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = make_inputs(8, 16, 256, seed=4)
+    x[3, 5] = float("nan")
+    vp[7, 2] = float("nan")
+    ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg)
+    out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    o = out.cpu().numpy()
+    assert np.array_equal(np.isnan(o), np.isnan(ref_out))
+    fin = np.isfinite(ref_out)
+    assert np.allclose(o[fin], ref_out[fin], rtol=1e-4, atol=1e-4 * np.abs(ref_out[fin]).max())
+    for a, r in ((gx, ref_dx), (gp, ref_gp), (gn, ref_gn)):
+        a = a.cpu().numpy()
+        assert np.array_equal(np.isnan(a), np.isnan(r))
+
+
+def test_lut_build_matches_oracle(cuda_device):
+    from isa.approximations.delta_lut import get_ekv_lut_tables
+
+    for size in (257, 4096, 8192):
+        cfg = flash_cfg(size)
+        ti_d, td_d = get_ekv_lut_tables(cfg, cuda_device)
+        ti, td = oracle.lut_tables(cfg)
+        a_i, a_d = ti_d.cpu().numpy(), td_d.cpu().numpy()
+        # both round the same fp64 value once; allow 1 ulp for libm differences
+        assert np.all(np.abs(a_i.view(np.int32).astype(np.int64) - ti.view(np.int32)) <= 1)
+        assert np.all(np.abs(a_d.view(np.int32).astype(np.int64) - td.view(np.int32)) <= 1)
+
+
+def test_bf16_table_mode(cuda_device):
+    """LUT_DTYPE=bfloat16 reproduces the reference's bf16 tables (delta_lut.py:35) and the
+    kernels then compute with the widened bf16 values (cuda_backend.py:68-69)."""
+    from isa.approximations.delta_lut import get_ekv_lut_tables
+
+    cfg = flash_cfg(4096, LUT_DTYPE="bfloat16")
+    ti_d, td_d = get_ekv_lut_tables(cfg, cuda_device)
+    assert ti_d.dtype == torch.bfloat16
+    ti, td = oracle.lut_tables(cfg)
+    ref_i = torch.from_numpy(ti).to(torch.bfloat16)
+    ref_d = torch.from_numpy(td).to(torch.bfloat16)
+    assert torch.equal(ti_d.cpu(), ref_i) and torch.equal(td_d.cpu(), ref_d)
+    x, vp, vn, g = make_inputs(40, 64, 256, seed=8)
+    dmin, dmax, n = oracle.lut_range(cfg)
+    ti_w, td_w = ref_i.float().numpy(), ref_d.float().numpy()
+    ref = oracle.forward(x.numpy(), vp.numpy(), vn.numpy(), ti_w, dmin, dmax, cfg["V_sat"])
+    dx = oracle.grad_x(x.numpy(), vp.numpy(), vn.numpy(), g.numpy(), ti_w, td_w, dmin, dmax, cfg["V_sat"])
+    out, gx, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    assert errs(out, ref)[0] <= FWD_TOL
+    assert errs(gx, dx)[0] <= BWD_TOL
