@@ -1,0 +1,244 @@
+"""Benchmark: Flash-EKV LUT CIMLinear cell-evals/s, fwd+bwd, Physical GPT-L FFN, 1 GPU.
+
+A step is one forward and backward pass of the drop-in `PhysicalFFN` (VoltageMapping ->
+CIMLinear 768->3072 -> CIMLinear 3072->768 -> ADC affine) over one batch X[8, 1024, 768]
+~ N(0, 1) with an N(0, 1) upstream gradient, fp32, 4096-entry LUT, random-init
+thresholds U(2.5 +- 0.5*2nU_T) (the reference's CIMLinear initialisation). Inputs and
+parameters are resident in HBM before timing starts.
+
+value = cell-evals per second over the timed steps, counting M*K*O cells per CIM layer
+in the forward and again in the backward. `roofline` reports the dominant kernel (the
+backward main kernel) against the VALU lane-instruction peak, from HIP events the library
+records around each launch on its own stream; `cpu_baseline` times the reference's
+PyTorch CPU path (exact formula, chunked over 64 outputs, analytic backward) restated in
+oracle/exact.py, on a bounded token sample of fc1.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT / "isa-_amd"), str(ROOT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+# gfx950 VALU issue peak: 256 CUs x 64 lanes x 2.4 GHz (lane-instructions per second)
+VALU_PEAK = 256 * 64 * 2.4e9
+FWD_INSTR_PER_CELL = 12  # algorithmic lane-instructions per cell-eval, forward
+BWD_INSTR_PER_CELL = 16  # backward
+
+CONFIGS = {
+    # name: (batch, tokens, d_model, d_ffn, physical fc2)
+    "gptl_ffn": (8, 1024, 768, 3072, True),     # configs[3], the headline
+    "vitm_ffn": (128, 65, 256, 1024, True),     # configs[1]
+    "gptm_hybrid": (16, 1024, 384, 1536, False),  # configs[2]
+    "vits_up": (8, 65, 192, 768, None),          # configs[0]: one CIMLinear
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_info() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields[k.strip()] = v.strip()
+        return f"{fields.get('Model name', platform.processor())}; sockets {fields.get('Socket(s)', '?')}, " \
+               f"cores/socket {fields.get('Core(s) per socket', '?')}"
+    except Exception:
+        return platform.processor() or "unknown"
+
+
+def cpu_baseline(d_model: int, d_ffn: int, target_s: float) -> dict:
+    """Reference CPU path (exact formula, cim.py:201-214 + flash_transistor.py:95-131) on fc1."""
+    import torch
+
+    from oracle import exact, oracle
+
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    torch.set_num_threads(threads)
+    cfg = dict(oracle.FLASH_PARAMS)
+    g = torch.Generator().manual_seed(0)
+    lo, hi = 2.5 - 0.5 * 2 * cfg["n"] * cfg["U_T"], 2.5 + 0.5 * 2 * cfg["n"] * cfg["U_T"]
+    vp = torch.empty(d_ffn, d_model).uniform_(lo, hi, generator=g).requires_grad_(True)
+    vn = torch.empty(d_ffn, d_model).uniform_(lo, hi, generator=g).requires_grad_(True)
+
+    def run(tokens: int) -> float:
+        x = torch.randn(1, tokens, d_model, generator=g).clamp(0.0, 4.0).requires_grad_(True)
+        gr = torch.randn(1, tokens, d_ffn, generator=g)
+        t0 = time.perf_counter()
+        out = exact.cim_idiff_cpu(x, vp, vn, cfg)
+        out.backward(gr)
+        return time.perf_counter() - t0
+
+    run(2)  # warm-up
+    tokens = 4
+    dt = run(tokens)
+    # scale the sample to roughly target_s of CPU work
+    want = max(4, min(4096, int(tokens * target_s / max(dt, 1e-3))))
+    dt = run(want)
+    cells = 2.0 * want * d_model * d_ffn
+    return {
+        "value": cells / dt,
+        "unit": "cell-evals/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"reference CPU path (exact EKV formula, chunked over 64 outputs, analytic backward) "
+                  f"restated in oracle/exact.py: fc1 {d_model}->{d_ffn} fwd+bwd on {want} tokens "
+                  f"({cells:.3e} cell-evals, {dt:.1f} s); host {cpu_info()}, os.cpu_count()={os.cpu_count()}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="gptl_ffn", choices=sorted(CONFIGS))
+    ap.add_argument("--lut-size", type=int, default=4096)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the kernel shards over "
+              "tokens; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    import torch.nn as nn
+
+    from isa.device_models.config import make_flash_transistor_ekv_config
+    from isa.kernels.transformer_ffn import _hip
+    from isa.operators.cim import CIMLinear, HybridFFN, PhysicalFFN
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    dev = torch.device("cuda", 0)
+    B, T, D, F, physical = CONFIGS[args.config]
+    M = B * T
+    cfg = make_flash_transistor_ekv_config(default_lut_size=args.lut_size)
+    cfg["LUT_DELTA_SIZE"] = args.lut_size
+
+    torch.manual_seed(0)
+    if physical is True:
+        model: nn.Module = PhysicalFFN(D, F, cfg)
+        layers = [(M, D, F), (M, F, D)]
+    elif physical is False:
+        model = HybridFFN(D, F, cfg)
+        layers = [(M, D, F)]
+    else:
+        model = CIMLinear(D, F, cfg)
+        layers = [(M, D, F)]
+    model = model.to(dev)
+    x = torch.randn(B, T, D, device=dev)
+    if physical is None:
+        x = x.clamp(0.0, 4.0)  # VoltageMapping defaults, applied once up front
+    x.requires_grad_(True)
+    with torch.no_grad():
+        g = torch.randn_like(model(x))
+    cells_fwd = float(sum(m * k * o for m, k, o in layers))
+    cells_step = 2.0 * cells_fwd
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        x.grad = None
+        out = model(x)
+        out.backward(g)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with _hip.KernelTimer() as kt:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    value = cells_step / (ms * 1e-3)
+    log(f"[bench] {args.config}: {ms:.3f} ms/step (wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
+
+    fwd_avg = kt.fwd_ms / max(kt.fwd_launches, 1)
+    bwd_avg = kt.bwd_ms / max(kt.bwd_launches, 1)
+    cells_launch = cells_fwd / len(layers)  # per-launch cells (equal for fc1 and fc2)
+    fwd_cells_s = cells_fwd * args.steps / (kt.fwd_ms * 1e-3) if kt.fwd_ms else 0.0
+    bwd_cells_s = cells_fwd * args.steps / (kt.bwd_ms * 1e-3) if kt.bwd_ms else 0.0
+    achieved = bwd_cells_s * BWD_INSTR_PER_CELL / 1e12
+    peak = VALU_PEAK / 1e12
+    roofline = {
+        "bound": "valu",
+        "achieved": round(achieved, 3),
+        "peak": round(peak, 3),
+        "unit": "TOP/s",
+        "frac": round(achieved / peak, 4),
+        "traffic": None,
+        "kernel": "bwd_kernel<true,true> (backward main kernel, dominant)",
+        "work": f"{BWD_INSTR_PER_CELL} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
+        "avg_launch_ms": round(bwd_avg, 4),
+        "forward_kernel": {
+            "kernel": "fwd_kernel", "avg_launch_ms": round(fwd_avg, 4),
+            "achieved": round(fwd_cells_s * FWD_INSTR_PER_CELL / 1e12, 3),
+            "frac": round(fwd_cells_s * FWD_INSTR_PER_CELL / VALU_PEAK, 4),
+        },
+        "step_frac_of_cell_roofline": round(value / (2.0 / (FWD_INSTR_PER_CELL / VALU_PEAK + BWD_INSTR_PER_CELL / VALU_PEAK)), 4),
+    }
+    log(f"[bench] fwd kernel {fwd_avg:.3f} ms/launch ({roofline['forward_kernel']['frac']:.3f} of VALU peak), "
+        f"bwd kernel {bwd_avg:.3f} ms/launch ({roofline['frac']:.3f})")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU baseline ...")
+        cpu = cpu_baseline(D, F, args.cpu_seconds)
+        log(f"[bench] cpu {cpu['value']:.4e} cell-evals/s on {cpu['cores']} threads")
+
+    result = {
+        "metric": "CIM cell-evals/sec fwd+bwd, Physical GPT-L FFN, 1 GPU; % of VALU roofline",
+        "value": value,
+        "unit": "cell-evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": {
+                "gptl_ffn": "Physical GPT-L FFN: CIMLinear 768->3072->768, X[8,1024,768] fp32, fwd+bwd",
+                "vitm_ffn": "Physical ViT-M FFN: CIMLinear 256->1024->256, X[128,65,256] fp32, fwd+bwd",
+                "gptm_hybrid": "Hybrid GPT-M FFN: CIMLinear 384->1536 + Linear 1536->384, X[16,1024,384], fwd+bwd",
+                "vits_up": "ViT-S up-projection: CIMLinear 192->768, X[8,65,192] fp32, fwd+bwd",
+            }[args.config],
+            "tokens": M,
+            "lut_entries": args.lut_size,
+            "cell_evals_per_step": cells_step,
+            "parallelism": "single GPU",
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

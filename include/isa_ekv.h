@@ -36,8 +36,12 @@ extern "C" {
 
 /* LUT layouts produced by isa_ekv_lut_build */
 #define ISA_EKV_LUT_PLAIN_F32 0  /* float table_i[N], then float table_ddelta[N]       */
-#define ISA_EKV_LUT_FWD 1        /* float2 {I, I[i+1]-I[i]} x (N + 2*pad), forward      */
-#define ISA_EKV_LUT_BWD 2        /* float4 {I, dI, D, dD} x (N + 2*pad), backward       */
+#define ISA_EKV_LUT_FWD 1        /* float2 {A_I, dI} x (N + 2*pad), forward              */
+#define ISA_EKV_LUT_BWD 2        /* float4 {A_I, dI, A_D, dD} x (N + 2*pad), backward     */
+/* Padded record r (0 <= r < N + 2*pad) serves coordinates c in [r, r+1) of the shifted
+ * index space c = (dV - delta_min) * s + pad: dT = T[j+1] - T[j] and A = T[j] - r * dT
+ * with j = r - pad, so L(c) = A + c * dT; records outside the table repeat the end
+ * values with dT = 0. */
 #define ISA_EKV_LUT_PLAIN_BF16 3 /* bf16 table_i[N], then bf16 table_ddelta[N]          */
 
 /* ABI version of the loaded library (ISA_EKV_ABI_VERSION). No reference counterpart. */
@@ -99,6 +103,13 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
                      const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries, float delta_min,
                      float delta_max, float v_sat, float* grad_x, float* grad_vth_pos, float* grad_vth_neg,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Profiling aid, no reference counterpart: between begin and end, every forward and
+ * backward call records HIP events on its stream around its main kernel (up to 4096
+ * launches). end synchronises those events and returns the summed milliseconds and
+ * launch counts (any pointer may be null). Not thread-safe; for benchmarks. */
+int isa_ekv_profile_begin(void);
+int isa_ekv_profile_end(double* fwd_ms, int* fwd_launches, double* bwd_ms, int* bwd_launches);
 
 #ifdef __cplusplus
 }

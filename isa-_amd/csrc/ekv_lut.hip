@@ -13,12 +13,14 @@
 //   dVth-[o,k] = +sum_m G[m,o] * L_D(dV-) * r
 //
 // MI355X design (one process, one device, caller-owned memory):
-//  * The table lives in LDS as padded, pre-differenced records: forward {I, I[i+1]-I[i]}
-//    (8 B, one ds_read_b64 per branch), backward {I, dI, D, dD} (16 B, one ds_read_b128).
+//  * The table lives in LDS as padded records in intercept form: record i holds
+//    {T[i] - i*dT[i], dT[i]} with dT[i] = T[i+1] - T[i], so L(c) = fma(c, dT, A) on the raw
+//    coordinate c. Forward records {A_I, dI} (8 B, one ds_read_b64 per branch), backward
+//    {A_I, dI, A_D, dD} (16 B, one ds_read_b128).
 //    kPad replicated end records on each side reproduce the reference's coordinate clamp
 //    exactly for coordinates within kPad-1 entries of the table range, so a kernel whose
 //    operand ranges fit (checked on device from the prep kernel's range partials) runs a
-//    clamp-free inner loop: sub, cvt_u32, fract, lshl_add, ds_read, fma per branch.
+//    clamp-free inner loop: sub, cvt_u32, lshl_add, ds_read, fma per branch.
 //  * A prep kernel writes the token-side operands pre-scaled into LUT-index units
 //    (xs = (x - dmin) * s + kPad, r, and -r/V_sat for the backward) and the threshold
 //    operands transposed to [K][O] as {vth_pos * s, vth_neg * s}, padded so the hot loops
@@ -56,9 +58,41 @@ constexpr int kPrepBlocksX = 128; // prep blocks for the token side
 constexpr int kPrepBlocksW = 128; // prep blocks for the threshold side
 constexpr int kMaxEntriesFwd = 16384;
 constexpr int kMaxEntriesBwd = 8192;
+
+__host__ __device__ inline int lut_records(int n) { return n + 2 * kPad; }
 constexpr int kLdsBytes = 160 * 1024;
 
 thread_local char g_last_error[512] = "";
+
+// Optional per-launch timing of the two main kernels (isa_ekv_profile_begin/_end): HIP
+// events recorded on the launch stream around each forward / backward main kernel.
+struct ProfiledLaunch {
+    hipEvent_t start, stop;
+    int kind;  // 0 forward, 1 backward
+};
+constexpr int kMaxProfiled = 4096;
+bool g_profiling = false;
+ProfiledLaunch g_prof[kMaxProfiled];
+int g_prof_count = 0;
+
+void prof_start(hipStream_t s, int kind, ProfiledLaunch** slot) {
+    *slot = nullptr;
+    if (!g_profiling || g_prof_count >= kMaxProfiled) return;
+    ProfiledLaunch* p = &g_prof[g_prof_count];
+    if (hipEventCreate(&p->start) != hipSuccess) return;
+    if (hipEventCreate(&p->stop) != hipSuccess) {
+        (void)hipEventDestroy(p->start);
+        return;
+    }
+    p->kind = kind;
+    (void)hipEventRecord(p->start, s);
+    ++g_prof_count;
+    *slot = p;
+}
+
+void prof_stop(hipStream_t s, ProfiledLaunch* slot) {
+    if (slot) (void)hipEventRecord(slot->stop, s);
+}
 
 int fail(int code, const char* fmt, ...) {
     va_list ap;
@@ -115,11 +149,27 @@ __device__ inline unsigned short f32_to_bf16_rne(float f) {
     return (unsigned short)(u >> 16);
 }
 
+// Intercept form of padded record idx: L(c) = T[i] + (c - idx) * dT = (T[i] - idx * dT) + c * dT,
+// so the kernels evaluate fma(c, dT, A) on the raw coordinate c (no fractional part).
+// A is formed in fp64 from the fp32 entry and slope and rounded once.
+__device__ inline float intercept(float t, float dt, int idx) {
+    return (float)((double)t - (double)idx * (double)dt);
+}
+
+// Records are stored whole (forward 8 B, backward 16 B) so one ds_read_b64/b128 fetches
+// a record: the words of a record sit in adjacent banks.
+__device__ inline void store_record(void* dst, int layout, int idx, float t, float dt, float d, float dd) {
+    if (layout == ISA_EKV_LUT_FWD)
+        static_cast<float2*>(dst)[idx] = make_float2(intercept(t, dt, idx), dt);
+    else
+        static_cast<float4*>(dst)[idx] = make_float4(intercept(t, dt, idx), dt, intercept(d, dd, idx), dd);
+}
+
 __global__ void lut_build_kernel(DeviceParams p, int layout, void* dst) {
     const int n = p.n_entries;
     const int total = (layout == ISA_EKV_LUT_PLAIN_F32 || layout == ISA_EKV_LUT_PLAIN_BF16)
                           ? n
-                          : n + 2 * kPad;
+                          : lut_records(n);
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= total) return;
     if (layout == ISA_EKV_LUT_PLAIN_F32) {
@@ -149,11 +199,7 @@ __global__ void lut_build_kernel(DeviceParams p, int layout, void* dst) {
         si = i1 - i0;
         sd = d1 - d0;
     }
-    if (layout == ISA_EKV_LUT_FWD) {
-        static_cast<float2*>(dst)[idx] = make_float2(i0, si);
-    } else {
-        static_cast<float4*>(dst)[idx] = make_float4(i0, si, d0, sd);
-    }
+    store_record(dst, layout, idx, i0, si, d0, sd);
 }
 
 // Pack plain tables into the padded records. bf16 sources are widened exactly as the
@@ -165,7 +211,7 @@ __device__ inline float load_table(const void* t, int i, int bf16) {
 
 __global__ void lut_pack_kernel(const void* ti, const void* td, int n, int src_bf16, int layout, void* dst) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n + 2 * kPad) return;
+    if (idx >= lut_records(n)) return;
     const int j = idx - kPad;
     const int jc = j < 0 ? 0 : (j > n - 1 ? n - 1 : j);
     const float i0 = load_table(ti, jc, src_bf16);
@@ -175,10 +221,7 @@ __global__ void lut_pack_kernel(const void* ti, const void* td, int n, int src_b
         si = load_table(ti, j + 1, src_bf16) - i0;
         if (layout == ISA_EKV_LUT_BWD) sd = load_table(td, j + 1, src_bf16) - d0;
     }
-    if (layout == ISA_EKV_LUT_FWD)
-        static_cast<float2*>(dst)[idx] = make_float2(i0, si);
-    else
-        static_cast<float4*>(dst)[idx] = make_float4(i0, si, d0, sd);
+    store_record(dst, layout, idx, i0, si, d0, sd);
 }
 
 // ----------------------------------------------------------------------------------
@@ -330,7 +373,7 @@ __device__ inline float coord(float xs, float ws, float cmin, float cmax) {
 struct FwdArgs {
     const float2* xrec;     // [M][Kp] {xs, r}
     const float2* wsT;      // [Kp][Op]
-    const float2* lut;      // [NP] {I, dI}
+    const float2* lut;      // [NP] {A_I, dI}
     const float2* partials;
     float* out;             // [M][O]
     int M, O, Kp, Op, NP;
@@ -378,8 +421,8 @@ __device__ inline void fwd_body(const FwdArgs& a, const float2* lut, int m0, int
                     const float cn = coord<CLAMP>(xv.x, w[kk][j].y, a.cmin, a.cmax);
                     const float2 ep = lut[(unsigned)cp];
                     const float2 en = lut[(unsigned)cn];
-                    const float lp = fmaf(__builtin_amdgcn_fractf(cp), ep.y, ep.x);
-                    const float ln = fmaf(__builtin_amdgcn_fractf(cn), en.y, en.x);
+                    const float lp = fmaf(cp, ep.y, ep.x);
+                    const float ln = fmaf(cn, en.y, en.x);
                     acc[i][j] = fmaf(lp - ln, xv.y, acc[i][j]);
                 }
             }
@@ -440,7 +483,7 @@ struct BwdArgs {
     const float4* xrec;     // [M][Kp] {xs, r, -r/V_sat, 0}
     const float2* wsT;      // [Kp][Op]
     const float* grad;      // [M][ldg]
-    const float4* lut;      // [NP] {I, dI, D, dD}
+    const float4* lut;      // [NP] {A_I, dI, A_D, dD}
     const float2* partials;
     float* dx_part;         // [n_ob][M][K]            (need_x)
     float* dv_part;         // [S][2][Kp][Op]          (need_w)
@@ -503,14 +546,12 @@ __device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red,
                         const float cn = coord<CLAMP>(xv.x, w[kk][j].y, a.cmin, a.cmax);
                         const float4 ep = lut[(unsigned)cp];
                         const float4 en = lut[(unsigned)cn];
-                        const float ap = __builtin_amdgcn_fractf(cp);
-                        const float an = __builtin_amdgcn_fractf(cn);
-                        const float dp = fmaf(ap, ep.w, ep.z);
-                        const float dn = fmaf(an, en.w, en.z);
+                        const float dp = fmaf(cp, ep.w, ep.z);
+                        const float dn = fmaf(cn, en.w, en.z);
                         const float gr = g[j] * xv.y;
                         if (NEED_X) {
-                            const float lp = fmaf(ap, ep.y, ep.x);
-                            const float ln = fmaf(an, en.y, en.x);
+                            const float lp = fmaf(cp, ep.y, ep.x);
+                            const float ln = fmaf(cn, en.y, en.x);
                             x1 = fmaf(gr, dp - dn, x1);
                             x2 = fmaf(gr, lp - ln, x2);
                         }
@@ -679,9 +720,8 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     p.Op = round_up(O > 0 ? O : 1, 64 * kBwdORR);
     p.n_ob = (int)(p.Op / (64 * kBwdORR));
     p.n_kb = (int)(p.Kp / kBwdKR);
-    const int np = n_entries + 2 * kPad;
     const size_t red_bytes = (size_t)kBwdMB * kBwdKR * kRedStride * 4;
-    const size_t lut_bytes = (size_t)np * 16;
+    const size_t lut_bytes = (size_t)lut_records(n_entries) * 16;
     int wpb = 16;
     while (wpb > 1 && lut_bytes + wpb * red_bytes > (size_t)kLdsBytes) wpb /= 2;
     p.waves_per_block = wpb;
@@ -727,6 +767,26 @@ __global__ __launch_bounds__(256) void pad_grad_kernel(const float* __restrict__
     }
 }
 
+void launch_forward(int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+    const dim3 block(kFwdWaves * 64);
+    if (mr == 8)
+        hipLaunchKernelGGL(fwd_kernel<8>, grid, block, lds, s, fa);
+    else if (mr == 4)
+        hipLaunchKernelGGL(fwd_kernel<4>, grid, block, lds, s, fa);
+    else
+        hipLaunchKernelGGL(fwd_kernel<2>, grid, block, lds, s, fa);
+}
+
+void launch_backward(bool need_x, bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                     const BwdArgs& ba) {
+    if (need_x && need_w)
+        hipLaunchKernelGGL((bwd_kernel<true, true>), grid, block, lds, s, ba);
+    else if (need_x)
+        hipLaunchKernelGGL((bwd_kernel<true, false>), grid, block, lds, s, ba);
+    else
+        hipLaunchKernelGGL((bwd_kernel<false, true>), grid, block, lds, s, ba);
+}
+
 int check_common(const float* x, const float* wp, const float* wn, const void* lut, int64_t M, int64_t K,
                  int64_t O, int n_entries, float delta_min, float delta_max, float v_sat) {
     if (M < 0 || K < 0 || O < 0) return fail(ISA_EKV_EINVAL, "negative shape (M=%lld, K=%lld, O=%lld)",
@@ -761,8 +821,8 @@ size_t isa_ekv_lut_bytes(int n_entries, int layout) {
     switch (layout) {
         case ISA_EKV_LUT_PLAIN_F32: return (size_t)n_entries * 2 * 4;
         case ISA_EKV_LUT_PLAIN_BF16: return (size_t)n_entries * 2 * 2;
-        case ISA_EKV_LUT_FWD: return (size_t)(n_entries + 2 * kPad) * 8;
-        case ISA_EKV_LUT_BWD: return (size_t)(n_entries + 2 * kPad) * 16;
+        case ISA_EKV_LUT_FWD: return (size_t)lut_records(n_entries) * 8;
+        case ISA_EKV_LUT_BWD: return (size_t)lut_records(n_entries) * 16;
         default: return 0;
     }
 }
@@ -805,6 +865,39 @@ int isa_ekv_lut_pack(const void* table_i, const void* table_ddelta, int n_entrie
     return 0;
 }
 
+int isa_ekv_profile_begin(void) {
+    for (int i = 0; i < g_prof_count; ++i) {
+        (void)hipEventDestroy(g_prof[i].start);
+        (void)hipEventDestroy(g_prof[i].stop);
+    }
+    g_prof_count = 0;
+    g_profiling = true;
+    return 0;
+}
+
+int isa_ekv_profile_end(double* fwd_ms, int* fwd_launches, double* bwd_ms, int* bwd_launches) {
+    g_profiling = false;
+    double t[2] = {0.0, 0.0};
+    int c[2] = {0, 0};
+    int rc = 0;
+    for (int i = 0; i < g_prof_count; ++i) {
+        float ms = 0.0f;
+        hipError_t err = hipEventSynchronize(g_prof[i].stop);
+        if (err == hipSuccess) err = hipEventElapsedTime(&ms, g_prof[i].start, g_prof[i].stop);
+        if (err != hipSuccess && rc == 0) rc = hip_fail(err, "profile event");
+        t[g_prof[i].kind] += ms;
+        c[g_prof[i].kind] += 1;
+        (void)hipEventDestroy(g_prof[i].start);
+        (void)hipEventDestroy(g_prof[i].stop);
+    }
+    g_prof_count = 0;
+    if (fwd_ms) *fwd_ms = t[0];
+    if (fwd_launches) *fwd_launches = c[0];
+    if (bwd_ms) *bwd_ms = t[1];
+    if (bwd_launches) *bwd_launches = c[1];
+    return rc;
+}
+
 size_t isa_ekv_forward_workspace(int64_t M, int64_t K, int64_t O) {
     if (M < 0 || K < 0 || O < 0) return 0;
     return plan_forward(M, K, O).bytes;
@@ -839,12 +932,11 @@ int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, 
                (int)M, (int)O, (int)p.Kp, (int)p.Op, np, p.n_mt, p.n_ot,
                (float)kPad, (float)(kPad + n_entries - 1), out_min, out_max};
     const size_t lds = (size_t)np * 8;
-    switch (p.mr) {
-        case 8: hipLaunchKernelGGL(fwd_kernel<8>, dim3(p.blocks), dim3(kFwdWaves * 64), lds, s, fa); break;
-        case 4: hipLaunchKernelGGL(fwd_kernel<4>, dim3(p.blocks), dim3(kFwdWaves * 64), lds, s, fa); break;
-        default: hipLaunchKernelGGL(fwd_kernel<2>, dim3(p.blocks), dim3(kFwdWaves * 64), lds, s, fa); break;
-    }
+    ProfiledLaunch* prof;
+    prof_start(s, 0, &prof);
+    launch_forward(p.mr, dim3(p.blocks), lds, s, fa);
     err = hipGetLastError();
+    prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "forward launch");
     return 0;
 }
@@ -913,13 +1005,11 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
                p.n_ob, p.n_kb, p.n_split, p.m_chunk, p.n_items,
                (float)kPad, (float)(kPad + n_entries - 1)};
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
-    if (need_x && need_w)
-        hipLaunchKernelGGL((bwd_kernel<true, true>), grid, block, p.lds_bytes, s, ba);
-    else if (need_x)
-        hipLaunchKernelGGL((bwd_kernel<true, false>), grid, block, p.lds_bytes, s, ba);
-    else
-        hipLaunchKernelGGL((bwd_kernel<false, true>), grid, block, p.lds_bytes, s, ba);
+    ProfiledLaunch* prof;
+    prof_start(s, 1, &prof);
+    launch_backward(need_x, need_w, grid, block, p.lds_bytes, s, ba);
     err = hipGetLastError();
+    prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "backward launch");
     if (need_x) {
         hipLaunchKernelGGL(dx_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dx),

@@ -33,6 +33,8 @@ EXPORTS = (
     "isa_ekv_forward",
     "isa_ekv_backward_workspace",
     "isa_ekv_backward",
+    "isa_ekv_profile_begin",
+    "isa_ekv_profile_end",
 )
 
 _lock = threading.Lock()
@@ -70,6 +72,12 @@ def _declare(lib) -> None:
     lib.isa_ekv_backward_workspace.restype = sz
     lib.isa_ekv_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, vp, vp, vp, vp, sz, vp]
     lib.isa_ekv_backward.restype = ci
+    lib.isa_ekv_profile_begin.argtypes = []
+    lib.isa_ekv_profile_begin.restype = ci
+    dp = ctypes.POINTER(f64)
+    ip = ctypes.POINTER(ci)
+    lib.isa_ekv_profile_end.argtypes = [dp, ip, dp, ip]
+    lib.isa_ekv_profile_end.restype = ci
 
 
 def load(path: Path | None = None):
@@ -102,6 +110,23 @@ def check(rc: int, what: str) -> None:
         msg = load().isa_ekv_last_error()
         text = msg.decode("utf-8", "replace") if msg else ""
         raise RuntimeError(f"{what} failed ({rc}): {text}")
+
+
+class KernelTimer:
+    """Context manager summing the library's main-kernel durations (HIP events)."""
+
+    def __enter__(self):
+        check(load().isa_ekv_profile_begin(), "isa_ekv_profile_begin")
+        return self
+
+    def __exit__(self, *exc):
+        f, b = ctypes.c_double(), ctypes.c_double()
+        nf, nb = ctypes.c_int(), ctypes.c_int()
+        rc = load().isa_ekv_profile_end(ctypes.byref(f), ctypes.byref(nf), ctypes.byref(b), ctypes.byref(nb))
+        self.fwd_ms, self.fwd_launches = f.value, nf.value
+        self.bwd_ms, self.bwd_launches = b.value, nb.value
+        check(rc, "isa_ekv_profile_end")
+        return False
 
 
 def stream_handle(device: torch.device) -> int:
