@@ -1,0 +1,120 @@
+"""The C ABI library loads on a host without a GPU and exports what include/isa_ekv.h
+declares; argument validation that happens before any HIP call returns ISA_EKV_EINVAL
+with a message (CPU only: no kernel is launched here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from isa.kernels.transformer_ffn import _hip
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "isa_ekv.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(isa_ekv_\w+)\s*\(", text)))
+
+
+def test_header_lists_the_python_exports():
+    assert declared_functions() == sorted(_hip.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    raw = ctypes.CDLL(str(_hip.LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+
+
+def test_version_and_sizes():
+    lib = _hip.load()
+    assert lib.isa_ekv_abi_version() == _hip.ABI_VERSION
+    pad = lib.isa_ekv_lut_pad()
+    assert pad >= 2
+    assert lib.isa_ekv_lut_bytes(4096, _hip.LUT_PLAIN_F32) == 4096 * 8
+    assert lib.isa_ekv_lut_bytes(4096, _hip.LUT_PLAIN_BF16) == 4096 * 4
+    assert lib.isa_ekv_lut_bytes(4096, _hip.LUT_FWD) == (4096 + 2 * pad) * 8
+    assert lib.isa_ekv_lut_bytes(4096, _hip.LUT_BWD) == (4096 + 2 * pad) * 16
+    assert lib.isa_ekv_lut_bytes(0, _hip.LUT_FWD) == 0
+    assert lib.isa_ekv_lut_bytes(16, 99) == 0
+
+
+def test_workspace_queries():
+    lib = _hip.load()
+    f = lib.isa_ekv_forward_workspace(8192, 768, 3072)
+    # token records (8 B) and transposed thresholds (8 B) at least
+    assert f >= 8192 * 768 * 8 + 768 * 3072 * 8
+    b_all = lib.isa_ekv_backward_workspace(8192, 768, 3072, 4096, 1, 1)
+    b_x = lib.isa_ekv_backward_workspace(8192, 768, 3072, 4096, 1, 0)
+    b_w = lib.isa_ekv_backward_workspace(8192, 768, 3072, 4096, 0, 1)
+    assert b_all > b_x and b_all > b_w
+    assert lib.isa_ekv_forward_workspace(-1, 2, 3) == 0
+    assert lib.isa_ekv_backward_workspace(1, 2, 3, 0, 1, 1) == 0
+
+
+def _err(lib) -> str:
+    return lib.isa_ekv_last_error().decode()
+
+
+def test_forward_rejects_bad_arguments_before_launch():
+    lib = _hip.load()
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    args = dict(M=4, K=4, O=4, n=4096, dmin=-9.0, dmax=4.0, vsat=8.26)
+
+    def call(**over):
+        a = dict(args, **over)
+        return lib.isa_ekv_forward(fake, fake, fake, fake, a["M"], a["K"], a["O"], a["n"], a["dmin"], a["dmax"],
+                                   a["vsat"], -4.0, 4.0, fake, fake, 0, None)
+
+    assert call(M=-1) == -1 and "negative shape" in _err(lib)
+    assert call(n=0) == -1 and "LUT_DELTA_SIZE" in _err(lib)
+    assert call(n=16385) == -1 and "16384" in _err(lib)
+    assert call(dmax=-10.0) == -1 and "delta_max > delta_min" in _err(lib)
+    assert call(vsat=0.0) == -1 and "V_sat" in _err(lib)
+    assert call() == -1 and "workspace too small" in _err(lib)
+    # empty outputs are a no-op
+    assert call(M=0) == 0 and call(O=0) == 0
+
+
+def test_backward_rejects_bad_arguments_before_launch():
+    lib = _hip.load()
+    fake = ctypes.c_void_p(16)
+
+    def call(n=4096, gx=fake, gp=fake, gn=fake, ws_bytes=0):
+        return lib.isa_ekv_backward(fake, fake, fake, fake, fake, 8, 8, 8, n, -9.0, 4.0, 8.26, gx, gp, gn,
+                                    fake, ws_bytes, None)
+
+    assert call(n=8193) == -1 and "8192" in _err(lib)
+    assert call(gp=None) == -1 and "both" in _err(lib)
+    assert call() == -1 and "workspace too small" in _err(lib)
+    assert call(gx=None, gp=None, gn=None) == 0  # nothing requested
+
+
+def test_lut_build_and_pack_reject_bad_arguments():
+    lib = _hip.load()
+    params = (ctypes.c_double * 4)(4.136, 0.0259, 7.5875e-7, 0.1)
+    fake = ctypes.c_void_p(16)
+    assert lib.isa_ekv_lut_build(None, -9.0, 4.0, 16, _hip.LUT_FWD, fake, None) == -1
+    assert lib.isa_ekv_lut_build(params, -9.0, 4.0, 16, 7, fake, None) == -1 and "layout" in _err(lib)
+    assert lib.isa_ekv_lut_build(params, 4.0, 4.0, 16, _hip.LUT_FWD, fake, None) == -1
+    bad = (ctypes.c_double * 4)(0.0, 0.0259, 7.5875e-7, 0.1)
+    assert lib.isa_ekv_lut_build(bad, -9.0, 4.0, 16, _hip.LUT_FWD, fake, None) == -1
+    assert lib.isa_ekv_lut_pack(fake, fake, 16, 0, _hip.LUT_PLAIN_F32, fake, None) == -1
+    assert lib.isa_ekv_lut_pack(fake, None, 16, 0, _hip.LUT_BWD, fake, None) == -1
+    assert lib.isa_ekv_lut_pack(fake, fake, 16, 5, _hip.LUT_FWD, fake, None) == -1
+
+
+def test_profiler_round_trip_without_launches():
+    with _hip.KernelTimer() as kt:
+        pass
+    assert kt.fwd_launches == 0 and kt.bwd_launches == 0 and kt.fwd_ms == 0.0
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_hip, "_lib", None)
+    with pytest.raises(_hip.HipExtensionError, match="not found"):
+        _hip.load(tmp_path / "absent.so")

@@ -1,0 +1,77 @@
+"""Headline-size parity (Physical GPT-L FFN, M = 8 x 1024 tokens, 768 -> 3072 -> 768).
+
+The oracle cannot redo 3.9e10 cell-evals in test time, so each full-size launch is checked
+on samples that are exact sub-problems: forward rows and dX rows depend only on their own
+token, dVth columns only on their own output (summed over all 8192 tokens). Size-independent
+properties (bitwise determinism, the equal-threshold invariant) run on the full tensors.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests.helpers import errs, flash_cfg, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(x, vp, vn, g, cfg, dev):
+    from isa.approximations.delta_lut import get_packed_tables, lut_range
+    from isa.kernels.transformer_ffn import ops
+
+    dmin, dmax, n = lut_range(cfg)
+    fwd, bwd = get_packed_tables(cfg, dev)
+    out = ops.lut_forward(x, vp, vn, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0)
+    gx, gp, gn = ops.lut_backward(x, vp, vn, g, bwd, n, dmin, dmax, cfg["V_sat"], True, True)
+    torch.cuda.synchronize()
+    return out, gx, gp, gn
+
+
+def _check_samples(x, vp, vn, g, res, cfg, rng, n_rows=48, n_cols=24):
+    out, gx, gp, gn = res
+    dmin, dmax, n = oracle.lut_range(cfg)
+    ti, td = oracle.lut_tables(cfg)
+    X, P, N, G = (t.cpu().numpy() for t in (x, vp, vn, g))
+    rows = np.sort(rng.choice(X.shape[0], n_rows, replace=False))
+    cols = np.sort(rng.choice(P.shape[0], n_cols, replace=False))
+    ref = oracle.forward(X[rows], P, N, ti, dmin, dmax, cfg["V_sat"])
+    rdx = oracle.grad_x(X[rows], P, N, G[rows], ti, td, dmin, dmax, cfg["V_sat"])
+    rgp, rgn = oracle.grad_w(X, P[cols], N[cols], np.ascontiguousarray(G[:, cols]), td, dmin, dmax, cfg["V_sat"])
+    e = {"fwd": errs(out[rows], ref), "dX": errs(gx[rows], rdx),
+         "dVth+": errs(gp[cols], rgp), "dVth-": errs(gn[cols], rgn)}
+    print({k: f"{v[0]:.2e}/{v[1]:.2e}" for k, v in e.items()})
+    assert e["fwd"][0] <= 1e-4
+    assert max(e["dX"][0], e["dVth+"][0], e["dVth-"][0]) <= 1e-3
+
+
+def test_headline_ffn_layers(cuda_device):
+    print("[case] headline fc1 768->3072, fc2 3072->768, M=8192", flush=True)
+    cfg = flash_cfg(4096)
+    rng = np.random.default_rng(0)
+    x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=0))
+    res1 = _run(x, vp, vn, g, cfg, cuda_device)
+    _check_samples(x, vp, vn, g, res1, cfg, rng)
+    # fc2 is driven by the TIA output of fc1: clamp(R_TIA * Idiff, -4, 4) (cim.py:192-193)
+    x2 = (res1[0] * 1e5).clamp(-4.0, 4.0).contiguous()
+    frac_sat = float((x2.abs() >= 4.0).float().mean())
+    print(f"fc2 input saturation {frac_sat:.3f}")
+    _, vp2, vn2, g2 = make_inputs(1, 3072, 768, seed=1)
+    g2 = torch.randn(8192, 768, generator=torch.Generator().manual_seed(2))
+    vp2, vn2, g2 = (t.to(cuda_device) for t in (vp2, vn2, g2))
+    res2 = _run(x2, vp2, vn2, g2, cfg, cuda_device)
+    _check_samples(x2, vp2, vn2, g2, res2, cfg, rng)
+    # bitwise determinism at full size
+    again = _run(x2, vp2, vn2, g2, cfg, cuda_device)
+    for a, b in zip(res2, again):
+        assert torch.equal(a, b)
+
+
+def test_headline_equal_threshold_invariant(cuda_device):
+    cfg = flash_cfg(4096)
+    x, vp, _, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=5))
+    out, gx, gp, gn = _run(x, vp, vp, g, cfg, cuda_device)
+    assert torch.count_nonzero(out) == 0 and torch.count_nonzero(gx) == 0
+    assert torch.equal(gp, -gn)
