@@ -48,14 +48,39 @@
 
 namespace {
 
+// Token-side records are read-only for the whole launch and their addresses are
+// wave-uniform: reading them through the constant address space lets the compiler use
+// scalar loads (SGPR operands) instead of vector loads with per-use latency stalls.
+using const_f32 = const __attribute__((address_space(4))) float;
+
+__device__ inline float2 load_uniform2(const float2* p) {
+    const_f32* q = (const_f32*)(p);
+    return make_float2(q[0], q[1]);
+}
+
+__device__ inline float4 load_uniform4(const float4* p) {
+    const_f32* q = (const_f32*)(p);
+    return make_float4(q[0], q[1], q[2], q[3]);
+}
+
 constexpr int kPad = 16;          // replicated end records on each side of the LDS table
 constexpr int kFwdORR = 4;        // outputs per lane, forward
-constexpr int kBwdORR = 4;        // outputs per lane, backward
-constexpr int kBwdKR = 4;         // inputs per wave, backward
-constexpr int kBwdMB = 4;         // tokens per dX transpose batch, backward
+#ifndef ISA_EKV_BWD_ORR
+#define ISA_EKV_BWD_ORR 4
+#endif
+#ifndef ISA_EKV_BWD_KR
+#define ISA_EKV_BWD_KR 4
+#endif
+#ifndef ISA_EKV_BWD_SCHED
+#define ISA_EKV_BWD_SCHED 1
+#endif
+constexpr int kBwdORR = ISA_EKV_BWD_ORR;  // outputs per lane, backward (2 or 4)
+constexpr int kBwdKR = ISA_EKV_BWD_KR;    // inputs per wave, backward (2 or 4)
+constexpr int kBwdMB = 16 / kBwdKR;       // tokens per dX transpose batch: 16 slots per batch
+static_assert((kBwdORR == 2 || kBwdORR == 4) && (kBwdKR == 2 || kBwdKR == 4), "backward tile");
 constexpr int kRedStride = 68;    // floats per slot row in the transpose buffer (64 + pad)
-constexpr int kPrepBlocksX = 128; // prep blocks for the token side
-constexpr int kPrepBlocksW = 128; // prep blocks for the threshold side
+constexpr int kPrepBlocksX = 1024; // prep blocks for the token side
+constexpr int kPrepBlocksW = 256; // prep blocks for the threshold side
 constexpr int kMaxEntriesFwd = 16384;
 constexpr int kMaxEntriesBwd = 8192;
 
@@ -267,28 +292,29 @@ __device__ inline void block_minmax(float lo, float hi, float2* out) {
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     float lo = INFINITY, hi = -INFINITY;
     if (blockIdx.x < kPrepBlocksX) {
-        const int64_t total = a.M * a.Kp;
+        // rows m are strided over the token-side blocks; threads walk k (coalesced)
         const float pad_coord = (float)kPad + 1.0f;
-        for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-             e += (int64_t)kPrepBlocksX * blockDim.x) {
-            const int64_t m = e / a.Kp;
-            const int64_t k = e - m * a.Kp;
-            float xs, r;
-            if (k < a.K) {
-                const float xv = a.x[m * a.K + k];
-                xs = fmaf(xv - a.delta_min, a.scale, (float)kPad);
-                r = 1.0f / (1.0f + xv / a.v_sat);
-                const bool bad = xs != xs;
-                lo = fminf(lo, bad ? -INFINITY : xs);
-                hi = fmaxf(hi, bad ? INFINITY : xs);
-            } else {
-                xs = pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
-                r = 0.0f;
-            }
-            if (a.rec_floats == 2) {
-                reinterpret_cast<float2*>(a.xrec)[e] = make_float2(xs, r);
-            } else {
-                reinterpret_cast<float4*>(a.xrec)[e] = make_float4(xs, r, -r / a.v_sat, 0.0f);
+        for (int64_t m = blockIdx.x; m < a.M; m += kPrepBlocksX) {
+            const float* xrow = a.x + m * a.K;
+            for (int k = threadIdx.x; k < (int)a.Kp; k += blockDim.x) {
+                float xs, r;
+                if (k < a.K) {
+                    const float xv = xrow[k];
+                    xs = fmaf(xv - a.delta_min, a.scale, (float)kPad);
+                    r = 1.0f / (1.0f + xv / a.v_sat);
+                    const bool bad = xs != xs;
+                    lo = fminf(lo, bad ? -INFINITY : xs);
+                    hi = fmaxf(hi, bad ? INFINITY : xs);
+                } else {
+                    xs = pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
+                    r = 0.0f;
+                }
+                const int64_t e = m * a.Kp + k;
+                if (a.rec_floats == 2) {
+                    reinterpret_cast<float2*>(a.xrec)[e] = make_float2(xs, r);
+                } else {
+                    reinterpret_cast<float4*>(a.xrec)[e] = make_float4(xs, r, -r / a.v_sat, 0.0f);
+                }
             }
         }
         block_minmax(lo, hi, &a.partials[blockIdx.x]);
@@ -414,7 +440,7 @@ __device__ inline void fwd_body(const FwdArgs& a, const float2* lut, int m0, int
         for (int kk = 0; kk < KU; ++kk) {
 #pragma unroll
             for (int i = 0; i < MR; ++i) {
-                const float2 xv = xrow[i][k0 + kk];
+                const float2 xv = load_uniform2(xrow[i] + k0 + kk);
 #pragma unroll
                 for (int j = 0; j < ORR; ++j) {
                     const float cp = coord<CLAMP>(xv.x, w[kk][j].x, a.cmin, a.cmax);
@@ -527,18 +553,40 @@ __device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red,
     const int my_slot = lane >> 2;
     const int my_quarter = lane & 3;
 
+    // token m's operands are prefetched one step ahead (scalar token records, vector grads)
+    const float4* xbase = a.xrec + k0;
+    const float* gbase = a.grad + o_lane;
+    float4 xn[KR];
+    float gn[ORR];
+    auto fetch = [&](int m) {
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) xn[kk] = load_uniform4(xbase + (size_t)m * a.Kp + kk);
+        if constexpr (ORR == 4) {
+            const float4 g4 = *reinterpret_cast<const float4*>(gbase + (size_t)m * a.ldg);
+            gn[0] = g4.x; gn[1] = g4.y; gn[2] = g4.z; gn[3] = g4.w;
+        } else {
+            const float2 g2 = *reinterpret_cast<const float2*>(gbase + (size_t)m * a.ldg);
+            gn[0] = g2.x; gn[1] = g2.y;
+        }
+    };
+    fetch(m_begin);
+
     for (int mb = m_begin; mb < m_end; mb += MB) {
 #pragma unroll 1
         for (int s = 0; s < MB; ++s) {
             const int m = mb + s;
             float tv[KR];
             if (m < m_end) {
-                const float4 g4 = *reinterpret_cast<const float4*>(a.grad + (size_t)m * a.ldg + o_lane);
-                const float g[4] = {g4.x, g4.y, g4.z, g4.w};
-                const float4* xr = a.xrec + (size_t)m * a.Kp + k0;
+                float4 xcur[KR];
+                float g[ORR];
+#pragma unroll
+                for (int kk = 0; kk < KR; ++kk) xcur[kk] = xn[kk];
+#pragma unroll
+                for (int j = 0; j < ORR; ++j) g[j] = gn[j];
+                fetch(min(m + 1, m_end - 1));
 #pragma unroll
                 for (int kk = 0; kk < KR; ++kk) {
-                    const float4 xv = xr[kk];
+                    const float4 xv = xcur[kk];
                     float x1 = 0.0f, x2 = 0.0f;
 #pragma unroll
                     for (int j = 0; j < ORR; ++j) {
@@ -563,7 +611,7 @@ __device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red,
                     tv[kk] = fmaf(x2, xv.z, x1);  // r*sum(G dL') - r^2/V_sat*sum(G dL)
                     // keep one input's gathers in flight at a time: bounds register pressure
                     // to the 128 VGPRs of a 16-wave block; other waves hide the LDS latency
-                    __builtin_amdgcn_sched_barrier(0);
+                    if (ISA_EKV_BWD_SCHED) __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
 #pragma unroll
@@ -603,10 +651,13 @@ __device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red,
         float* dst_n = dst_p + (size_t)a.Kp * a.Op;
 #pragma unroll
         for (int kk = 0; kk < KR; ++kk) {
-            float4* pp = reinterpret_cast<float4*>(dst_p + (size_t)(k0 + kk) * a.Op + o_lane);
-            float4* pn = reinterpret_cast<float4*>(dst_n + (size_t)(k0 + kk) * a.Op + o_lane);
-            *pp = make_float4(accp[kk][0], accp[kk][1], accp[kk][2], accp[kk][3]);
-            *pn = make_float4(accn[kk][0], accn[kk][1], accn[kk][2], accn[kk][3]);
+            float* pp = dst_p + (size_t)(k0 + kk) * a.Op + o_lane;
+            float* pn = dst_n + (size_t)(k0 + kk) * a.Op + o_lane;
+#pragma unroll
+            for (int j = 0; j < ORR; ++j) {
+                pp[j] = accp[kk][j];
+                pn[j] = accn[kk][j];
+            }
         }
     }
 }
