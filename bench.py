@@ -102,6 +102,19 @@ def cpu_baseline(d_model: int, d_ffn: int, target_s: float) -> dict:
     }
 
 
+def measured_traffic(config: str):
+    """HBM bytes per backward main-kernel launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel), or None if absent."""
+    path = ROOT / "profiles" / f"bwd_kernel_{config}_hbm_traffic.txt"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,11 +124,14 @@ def main() -> int:
     ap.add_argument("--lut-size", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after timing, run one plain device-to-device copy of this many MiB (a reference "
+                         "kernel of known HBM traffic for counter runs)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the kernel shards over "
-              "tokens; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the operator would shard "
+              "over tokens with one all-reduce of dVth per layer). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
@@ -175,6 +191,15 @@ def main() -> int:
     value = cells_step / (ms * 1e-3)
     log(f"[bench] {args.config}: {ms:.3f} ms/step (wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
 
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.empty(n, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.mul(src, 1.0, out=dst)  # an elementwise kernel (a hipMemcpy may use the DMA engines)
+        torch.cuda.synchronize()
+        del src, dst
+
     fwd_avg = kt.fwd_ms / max(kt.fwd_launches, 1)
     bwd_avg = kt.bwd_ms / max(kt.bwd_launches, 1)
     cells_launch = cells_fwd / len(layers)  # per-launch cells (equal for fc1 and fc2)
@@ -188,7 +213,7 @@ def main() -> int:
         "peak": round(peak, 3),
         "unit": "TOP/s",
         "frac": round(achieved / peak, 4),
-        "traffic": None,
+        "traffic": measured_traffic(args.config),
         "kernel": "bwd_kernel<true,true> (backward main kernel, dominant)",
         "work": f"{BWD_INSTR_PER_CELL} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
         "avg_launch_ms": round(bwd_avg, 4),

@@ -523,10 +523,12 @@ template <bool CLAMP, bool NEED_X, bool NEED_W>
 __device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red, int item) {
     constexpr int ORR = kBwdORR, KR = kBwdKR, MB = kBwdMB;
     const int lane = threadIdx.x & 63;
-    const int ob = item % a.n_ob;
-    const int rest = item / a.n_ob;
-    const int kb = rest % a.n_kb;
-    const int sp = rest / a.n_kb;
+    // inputs vary fastest: the waves of a block share (output block, token split), so the
+    // G row slices they stream are fetched once into the CU's L1 and reused
+    const int kb = item % a.n_kb;
+    const int rest = item / a.n_kb;
+    const int ob = rest % a.n_ob;
+    const int sp = rest / a.n_ob;
     const int o_lane = ob * 64 * ORR + lane * ORR;
     const int k0 = kb * KR;
     const int m_begin = sp * a.m_chunk;
