@@ -115,12 +115,110 @@ def measured_traffic(config: str):
     return None
 
 
+def gpt_train_step(args) -> int:
+    """one GPT training step (12 layers, d=768, 12 heads, Physical FFN 3072 on the
+    HIP kernels, causal SDPA attention, vocab 50304 tied embeddings, 8 x 1024 tokens, AdamW,
+    then the thresholds are clamped to [V_TH_MIN, V_TH_MAX] as the reference's language
+    trainer does). Reports tokens/s and the share of step time spent in the CIM library calls."""
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    from isa.device_models.config import make_flash_transistor_ekv_config
+    from isa.kernels.transformer_ffn import _hip
+    from isa.operators.cim import PhysicalFFN
+
+    dev = torch.device("cuda", 0)
+    n_layer, n_head, d, d_ffn, vocab, B, T = 12, 12, 768, 3072, 50304, 8, 1024
+    cfg = make_flash_transistor_ekv_config(default_lut_size=args.lut_size)
+    cfg["LUT_DELTA_SIZE"] = args.lut_size
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ln1 = nn.LayerNorm(d)
+            self.qkv = nn.Linear(d, 3 * d)
+            self.proj = nn.Linear(d, d)
+            self.ln2 = nn.LayerNorm(d)
+            self.ffn = PhysicalFFN(d, d_ffn, cfg)
+
+        def forward(self, x):
+            b, t, _ = x.shape
+            q, k, v = self.qkv(self.ln1(x)).view(b, t, 3, n_head, d // n_head).unbind(dim=2)
+            a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                               is_causal=True)
+            x = x + self.proj(a.transpose(1, 2).reshape(b, t, d))
+            return x + self.ffn(self.ln2(x))
+
+    class GPT(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.tok = nn.Embedding(vocab, d)
+            self.pos = nn.Embedding(T, d)
+            self.blocks = nn.ModuleList(Block() for _ in range(n_layer))
+            self.ln_f = nn.LayerNorm(d)
+            self.head = nn.Linear(d, vocab, bias=False)
+            self.head.weight = self.tok.weight
+
+        def forward(self, ids):
+            x = self.tok(ids) + self.pos(torch.arange(ids.shape[1], device=ids.device))[None]
+            for blk in self.blocks:
+                x = blk(x)
+            return self.head(self.ln_f(x))
+
+    torch.manual_seed(0)
+    model = GPT().to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.0)
+    ids = torch.randint(0, vocab, (B, T + 1), device=dev)
+    inp, tgt = ids[:, :-1].contiguous(), ids[:, 1:].contiguous()
+    ffns = [blk.ffn for blk in model.blocks]
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        logits = model(inp)
+        loss = F.cross_entropy(logits.view(-1, vocab), tgt.view(-1))
+        loss.backward()
+        opt.step()
+        for f in ffns:
+            f.clamp_vth()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with _hip.KernelTimer() as kt:
+        e0.record()
+        for _ in range(args.steps):
+            loss = step()
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    cim_ms = (kt.fwd_call_ms + kt.bwd_call_ms) / args.steps
+    main_ms = (kt.fwd_ms + kt.bwd_ms) / args.steps
+    cells = 2.0 * n_layer * 2 * (B * T) * d * d_ffn
+    result = {
+        "metric": "GPT-L training step tokens/s, 1 GPU (Physical FFN on the CIM kernels); FFN share of step time",
+        "value": B * T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "GPT 12 layers, d=768, 12 heads, Physical FFN 3072, vocab 50304, 8x1024 tokens, AdamW",
+                   "lut_entries": args.lut_size, "parallelism": "single GPU"},
+        "ffn": {"cim_call_ms_per_step": cim_ms, "cim_main_kernels_ms_per_step": main_ms,
+                "cim_share_of_step": cim_ms / ms, "cell_evals_per_step": cells,
+                "cim_cell_evals_per_s": cells / (cim_ms * 1e-3), "final_loss": float(loss.detach())},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="gptl_ffn", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="gptl_ffn", choices=sorted(CONFIGS) + ["gptl_train"])
     ap.add_argument("--lut-size", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -133,6 +231,9 @@ def main() -> int:
         print("bench.py measures one GPU: this build has no multi-GPU path (the operator would shard "
               "over tokens with one all-reduce of dVth per layer). Run with --gpus 1.", file=sys.stderr)
         return 2
+
+    if args.config == "gptl_train":
+        return gpt_train_step(args)
 
     import torch
     import torch.nn as nn

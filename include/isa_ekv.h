@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 1
+#define ISA_EKV_ABI_VERSION 2
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -105,11 +105,13 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Profiling aid, no reference counterpart: between begin and end, every forward and
- * backward call records HIP events on its stream around its main kernel (up to 4096
- * launches). end synchronises those events and returns the summed milliseconds and
- * launch counts (any pointer may be null). Not thread-safe; for benchmarks. */
+ * backward call records HIP events on its stream (up to 4096 intervals). end synchronises
+ * them and writes, for k = 0..3, the summed milliseconds ms[k] and interval counts
+ * launches[k] of: 0 forward main kernel, 1 backward main kernel, 2 whole forward call
+ * (prep included), 3 whole backward call (prep and reductions included). Either
+ * pointer may be null. Not thread-safe; for benchmarks. */
 int isa_ekv_profile_begin(void);
-int isa_ekv_profile_end(double* fwd_ms, int* fwd_launches, double* bwd_ms, int* bwd_launches);
+int isa_ekv_profile_end(double* ms, int* launches);
 
 #ifdef __cplusplus
 }

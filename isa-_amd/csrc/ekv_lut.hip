@@ -93,8 +93,9 @@ thread_local char g_last_error[512] = "";
 // events recorded on the launch stream around each forward / backward main kernel.
 struct ProfiledLaunch {
     hipEvent_t start, stop;
-    int kind;  // 0 forward, 1 backward
+    int kind;  // 0 forward main kernel, 1 backward main kernel, 2 whole forward call, 3 whole backward call
 };
+constexpr int kProfKinds = 4;
 constexpr int kMaxProfiled = 4096;
 bool g_profiling = false;
 ProfiledLaunch g_prof[kMaxProfiled];
@@ -118,6 +119,14 @@ void prof_start(hipStream_t s, int kind, ProfiledLaunch** slot) {
 void prof_stop(hipStream_t s, ProfiledLaunch* slot) {
     if (slot) (void)hipEventRecord(slot->stop, s);
 }
+
+// Times a whole library call (every kernel it enqueues), closing on every return path.
+struct CallTimer {
+    hipStream_t stream;
+    ProfiledLaunch* slot;
+    CallTimer(hipStream_t s, int kind) : stream(s) { prof_start(s, kind, &slot); }
+    ~CallTimer() { prof_stop(stream, slot); }
+};
 
 int fail(int code, const char* fmt, ...) {
     va_list ap;
@@ -928,10 +937,10 @@ int isa_ekv_profile_begin(void) {
     return 0;
 }
 
-int isa_ekv_profile_end(double* fwd_ms, int* fwd_launches, double* bwd_ms, int* bwd_launches) {
+int isa_ekv_profile_end(double* ms, int* launches) {
     g_profiling = false;
-    double t[2] = {0.0, 0.0};
-    int c[2] = {0, 0};
+    double t[kProfKinds] = {0.0, 0.0, 0.0, 0.0};
+    int c[kProfKinds] = {0, 0, 0, 0};
     int rc = 0;
     for (int i = 0; i < g_prof_count; ++i) {
         float ms = 0.0f;
@@ -944,10 +953,10 @@ int isa_ekv_profile_end(double* fwd_ms, int* fwd_launches, double* bwd_ms, int* 
         (void)hipEventDestroy(g_prof[i].stop);
     }
     g_prof_count = 0;
-    if (fwd_ms) *fwd_ms = t[0];
-    if (fwd_launches) *fwd_launches = c[0];
-    if (bwd_ms) *bwd_ms = t[1];
-    if (bwd_launches) *bwd_launches = c[1];
+    for (int k = 0; k < kProfKinds; ++k) {
+        if (ms) ms[k] = t[k];
+        if (launches) launches[k] = c[k];
+    }
     return rc;
 }
 
@@ -972,6 +981,7 @@ int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, 
         return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
+    CallTimer call_timer(s, 2);
     const double scale_d = n_entries > 1 ? (double)(n_entries - 1) / ((double)delta_max - (double)delta_min) : 0.0;
     PrepArgs pa{x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, delta_min, (float)scale_d, v_sat, 2,
                 reinterpret_cast<float*>(ws + p.off_xrec), reinterpret_cast<float2*>(ws + p.off_wsT),
@@ -1033,6 +1043,7 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
     if (!workspace || workspace_bytes < p.bytes)
         return fail(ISA_EKV_EINVAL, "backward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
     char* ws = static_cast<char*>(workspace);
+    CallTimer call_timer(s, 3);
     const double scale_d = n_entries > 1 ? (double)(n_entries - 1) / ((double)delta_max - (double)delta_min) : 0.0;
     PrepArgs pa{x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, delta_min, (float)scale_d, v_sat, 4,
                 reinterpret_cast<float*>(ws + p.off_xrec), reinterpret_cast<float2*>(ws + p.off_wsT),

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -74,9 +74,7 @@ def _declare(lib) -> None:
     lib.isa_ekv_backward.restype = ci
     lib.isa_ekv_profile_begin.argtypes = []
     lib.isa_ekv_profile_begin.restype = ci
-    dp = ctypes.POINTER(f64)
-    ip = ctypes.POINTER(ci)
-    lib.isa_ekv_profile_end.argtypes = [dp, ip, dp, ip]
+    lib.isa_ekv_profile_end.argtypes = [ctypes.POINTER(f64), ctypes.POINTER(ci)]
     lib.isa_ekv_profile_end.restype = ci
 
 
@@ -113,18 +111,19 @@ def check(rc: int, what: str) -> None:
 
 
 class KernelTimer:
-    """Context manager summing the library's main-kernel durations (HIP events)."""
+    """Context manager summing HIP-event durations the library records: main kernels
+    (fwd_ms, bwd_ms) and whole calls including prep and reductions (fwd_call_ms, bwd_call_ms)."""
 
     def __enter__(self):
         check(load().isa_ekv_profile_begin(), "isa_ekv_profile_begin")
         return self
 
     def __exit__(self, *exc):
-        f, b = ctypes.c_double(), ctypes.c_double()
-        nf, nb = ctypes.c_int(), ctypes.c_int()
-        rc = load().isa_ekv_profile_end(ctypes.byref(f), ctypes.byref(nf), ctypes.byref(b), ctypes.byref(nb))
-        self.fwd_ms, self.fwd_launches = f.value, nf.value
-        self.bwd_ms, self.bwd_launches = b.value, nb.value
+        ms = (ctypes.c_double * 4)()
+        n = (ctypes.c_int * 4)()
+        rc = load().isa_ekv_profile_end(ms, n)
+        self.fwd_ms, self.bwd_ms, self.fwd_call_ms, self.bwd_call_ms = ms
+        self.fwd_launches, self.bwd_launches, self.fwd_calls, self.bwd_calls = n
         check(rc, "isa_ekv_profile_end")
         return False
 

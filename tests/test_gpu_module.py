@@ -50,7 +50,7 @@ def test_physical_ffn_autograd(cuda_device):
 
     # oracle composition on the CPU
     X = _np(x).reshape(-1, D)
-    s, b = float(ffn.input_mapping.scale), float(ffn.input_mapping.shift)
+    s, b = float(ffn.input_mapping.scale.detach()), float(ffn.input_mapping.shift.detach())
     pre0 = X * s + b
     v = np.clip(pre0, 0.0, 4.0)
     r1, r2 = float(ffn.fc1.r_tia), float(ffn.fc2.r_tia)
