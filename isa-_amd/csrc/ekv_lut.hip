@@ -83,6 +83,12 @@ constexpr int kPrepBlocksX = 1024; // prep blocks for the token side
 constexpr int kPrepBlocksW = 256; // prep blocks for the threshold side
 constexpr int kMaxEntriesFwd = 16384;
 constexpr int kMaxEntriesBwd = 8192;
+#ifndef ISA_EKV_BWD_SPLIT
+#define ISA_EKV_BWD_SPLIT 1
+#endif
+// Backward tables of up to this many padded records use the split LDS layout (the D
+// halves sit kSplitRecords * 8 bytes after the I halves: within the 16-bit ds offset).
+constexpr int kSplitRecords = 4096 + 2 * kPad;
 
 __host__ __device__ inline int lut_records(int n) { return n + 2 * kPad; }
 constexpr int kLdsBytes = 160 * 1024;
@@ -528,8 +534,26 @@ struct BwdArgs {
     float cmin, cmax;
 };
 
-template <bool CLAMP, bool NEED_X, bool NEED_W>
-__device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red, int item) {
+// LDS table views for the backward. Interleaved: one 16-byte record {A_I, dI, A_D, dD} per
+// coordinate (one ds_read_b128). Split: the I halves in one array and the D halves
+// kSplitRecords records further on, reached through the instruction's immediate offset
+// (two ds_read_b64 from one address). Random 8-byte gathers cost fewer bank-conflict
+// cycles per byte than 16-byte ones, and a dVth-only backward never reads the I halves.
+struct BwdTableInterleaved {
+    const float4* t;
+    __device__ float4 operator[](unsigned i) const { return t[i]; }
+};
+struct BwdTableSplit {
+    const float2* t;
+    __device__ float4 operator[](unsigned i) const {
+        const float2 ri = t[i];
+        const float2 rd = t[i + kSplitRecords];
+        return make_float4(ri.x, ri.y, rd.x, rd.y);
+    }
+};
+
+template <bool CLAMP, bool NEED_X, bool NEED_W, class Table>
+__device__ inline void bwd_body(const BwdArgs& a, Table lut, float* red, int item) {
     constexpr int ORR = kBwdORR, KR = kBwdKR, MB = kBwdMB;
     const int lane = threadIdx.x & 63;
     // inputs vary fastest: the waves of a block share (output block, token split), so the
@@ -673,21 +697,40 @@ __device__ inline void bwd_body(const BwdArgs& a, const float4* lut, float* red,
     }
 }
 
-template <bool NEED_X, bool NEED_W>
+template <bool NEED_X, bool NEED_W, bool SPLIT>
 __global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
     extern __shared__ float4 s_lut_bwd[];
-    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_bwd[i] = a.lut[i];
+    float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
+    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
+        const float4 rec = a.lut[i];
+        if constexpr (SPLIT) {
+            s_split[i] = make_float2(rec.x, rec.y);
+            s_split[i + kSplitRecords] = make_float2(rec.z, rec.w);
+        } else {
+            s_lut_bwd[i] = rec;
+        }
+    }
     const bool fast = coords_in_padded_range(a.partials, a.NP);
     __syncthreads();
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float* red = reinterpret_cast<float*>(s_lut_bwd + a.NP) + wave * (kBwdMB * kBwdKR * kRedStride);
+    const int table_records = SPLIT ? kSplitRecords : a.NP;
+    float* red = reinterpret_cast<float*>(s_lut_bwd + table_records) + wave * (kBwdMB * kBwdKR * kRedStride);
     const int item = blockIdx.x * waves + wave;
     if (item >= a.n_items) return;
-    if (fast)
-        bwd_body<false, NEED_X, NEED_W>(a, s_lut_bwd, red, item);
-    else
-        bwd_body<true, NEED_X, NEED_W>(a, s_lut_bwd, red, item);
+    if constexpr (SPLIT) {
+        const BwdTableSplit t{s_split};
+        if (fast)
+            bwd_body<false, NEED_X, NEED_W>(a, t, red, item);
+        else
+            bwd_body<true, NEED_X, NEED_W>(a, t, red, item);
+    } else {
+        const BwdTableInterleaved t{s_lut_bwd};
+        if (fast)
+            bwd_body<false, NEED_X, NEED_W>(a, t, red, item);
+        else
+            bwd_body<true, NEED_X, NEED_W>(a, t, red, item);
+    }
 }
 
 // dX[m,k] = sum over output blocks, in block order (deterministic)
@@ -772,7 +815,7 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O) {
 struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
-    bool grad_padded;
+    bool grad_padded, split;
     size_t off_xrec, off_wsT, off_part, off_gpad, off_dx, off_dv, bytes, lds_bytes;
 };
 
@@ -783,7 +826,8 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     p.n_ob = (int)(p.Op / (64 * kBwdORR));
     p.n_kb = (int)(p.Kp / kBwdKR);
     const size_t red_bytes = (size_t)kBwdMB * kBwdKR * kRedStride * 4;
-    const size_t lut_bytes = (size_t)lut_records(n_entries) * 16;
+    p.split = ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
+    const size_t lut_bytes = (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
     int wpb = 16;
     while (wpb > 1 && lut_bytes + wpb * red_bytes > (size_t)kLdsBytes) wpb /= 2;
     p.waves_per_block = wpb;
@@ -839,14 +883,23 @@ void launch_forward(int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs&
         hipLaunchKernelGGL(fwd_kernel<2>, grid, block, lds, s, fa);
 }
 
-void launch_backward(bool need_x, bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                     const BwdArgs& ba) {
+template <bool SPLIT>
+void launch_backward_layout(bool need_x, bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                            const BwdArgs& ba) {
     if (need_x && need_w)
-        hipLaunchKernelGGL((bwd_kernel<true, true>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<true, true, SPLIT>), grid, block, lds, s, ba);
     else if (need_x)
-        hipLaunchKernelGGL((bwd_kernel<true, false>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<true, false, SPLIT>), grid, block, lds, s, ba);
     else
-        hipLaunchKernelGGL((bwd_kernel<false, true>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<false, true, SPLIT>), grid, block, lds, s, ba);
+}
+
+void launch_backward(bool need_x, bool need_w, bool split, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                     const BwdArgs& ba) {
+    if (split)
+        launch_backward_layout<true>(need_x, need_w, grid, block, lds, s, ba);
+    else
+        launch_backward_layout<false>(need_x, need_w, grid, block, lds, s, ba);
 }
 
 int check_common(const float* x, const float* wp, const float* wn, const void* lut, int64_t M, int64_t K,
@@ -1071,7 +1124,7 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
     ProfiledLaunch* prof;
     prof_start(s, 1, &prof);
-    launch_backward(need_x, need_w, grid, block, p.lds_bytes, s, ba);
+    launch_backward(need_x, need_w, p.split, grid, block, p.lds_bytes, s, ba);
     err = hipGetLastError();
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "backward launch");
