@@ -6,7 +6,9 @@
  *   - the pybind11 module of src/isa/kernels/transformer_ffn/cuda/binding.cpp:56-62
  *     (forward, grad_x, grad_x_shared, grad_w, grad_w_shared),
  *   - the Triton forward launch of src/isa/kernels/transformer_ffn/ekv_lut_triton.py:151-157,
- *   - the LUT construction of src/isa/approximations/delta_lut.py:12-35.
+ *   - the LUT construction of src/isa/approximations/delta_lut.py:12-35,
+ *   - the exact-formula Triton kernels of src/isa/kernels/transformer_ffn/ekv_triton.py:69-169
+ *     (ekv_approx != "lut").
  *
  * Conventions (differences from the reference are deliberate):
  *   - Plain pointers and sizes; no torch types. All tensors are fp32, row-major,
@@ -31,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 2
+#define ISA_EKV_ABI_VERSION 3
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -104,10 +106,38 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
                      float delta_max, float v_sat, float* grad_x, float* grad_vth_pos, float* grad_vth_neg,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Exact-formula path: the same products with the EKV current evaluated directly,
+ *   I(v, vth) = I_S [sp(u1)^2 - sp(u2)^2] / (1 + v/V_sat),  u1 = (v - vth)/(2 n U_T),
+ *   u2 = u1 - V_D/(2 n U_T),  sp = softplus (threshold 20),
+ * params = {n, U_T, I_S, V_D}. No table; no output clamp. */
+
+/* Workspace bytes for isa_ekv_exact_forward at this shape. */
+size_t isa_ekv_exact_forward_workspace(int64_t M, int64_t K, int64_t O);
+
+/* out[m,o] = sum_k (I(x, vth_pos) - I(x, vth_neg)).
+ * Replaces the _forward_kernel launch of TritonEKVMatmulFn.forward (ekv_triton.py:69-91,
+ * :175-188). */
+int isa_ekv_exact_forward(const float* x, const float* vth_pos, const float* vth_neg, int64_t M, int64_t K,
+                          int64_t O, const double params[4], float v_sat, float* out, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for isa_ekv_exact_backward at this shape and gradient selection. */
+size_t isa_ekv_exact_backward_workspace(int64_t M, int64_t K, int64_t O, int need_grad_x, int need_grad_w);
+
+/* grad_x[m,k] = sum_o G[m,o] (dI/dv(x, vth_pos) - dI/dv(x, vth_neg)),
+ * grad_vth_pos[o,k] = sum_m G[m,o] dI/dvth(x, vth_pos),
+ * grad_vth_neg[o,k] = -sum_m G[m,o] dI/dvth(x, vth_neg); null pointers as isa_ekv_backward.
+ * Replaces the _grad_x_kernel and _grad_w_kernel launches of TritonEKVMatmulFn.backward
+ * (ekv_triton.py:94-169, :194-207); deterministic (no atomics). */
+int isa_ekv_exact_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
+                           int64_t M, int64_t K, int64_t O, const double params[4], float v_sat, float* grad_x,
+                           float* grad_vth_pos, float* grad_vth_neg, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 /* Profiling aid, no reference counterpart: between begin and end, every forward and
  * backward call records HIP events on its stream (up to 4096 intervals). end synchronises
  * them and writes, for k = 0..3, the summed milliseconds ms[k] and interval counts
- * launches[k] of: 0 forward main kernel, 1 backward main kernel, 2 whole forward call
+ * launches[k] of (LUT and exact calls alike): 0 forward main kernel, 1 backward main kernel, 2 whole forward call
  * (prep included), 3 whole backward call (prep and reductions included). Either
  * pointer may be null. Not thread-safe; for benchmarks. */
 int isa_ekv_profile_begin(void);

@@ -38,6 +38,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
+#include <cmath>
 #include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -265,9 +268,14 @@ __global__ void lut_pack_kernel(const void* ti, const void* td, int n, int src_b
 }
 
 // ----------------------------------------------------------------------------------
-// Prep: token side [M][Kp] records and threshold side [Kp][Op] {wp*s, wn*s}, plus
-// per-block (min, max) partials of the pre-scaled coordinates. NaN maps to an
-// infinite partial so the range test fails and the clamping loop runs.
+// Prep: token side [M][Kp] records and threshold side [Kp][Op] pairs, plus per-block
+// (min, max) partials of the scaled coordinates. NaN maps to an infinite partial so the
+// kernels' range tests fail and their general (clamping / selecting) loops run.
+//   LUT mode:   token coordinate xs = (x - dmin) * s + kPad, threshold coordinate w * s.
+//   exact mode: coordinates in log2 units, tx = x * a, tw = w * a with a = log2(e)/(2 n U_T);
+//               the records for the range-checked loop hold 2^tx and 2^-tw (formed in fp64),
+//               so 2^(tx - tw) is one multiply; the general loop reads tx and tw.
+// Token records: {c, r} (forward) or {c, r, -r / z_div, 0} (backward), r = 1/(1 + x/V_sat).
 // ----------------------------------------------------------------------------------
 
 struct PrepArgs {
@@ -275,11 +283,17 @@ struct PrepArgs {
     const float* wp;
     const float* wn;
     int64_t M, K, O, Kp, Op;
-    float delta_min, scale, v_sat;
-    int rec_floats;      // 2: {xs, r}; 4: {xs, r, -r/V_sat, 0}
-    float* xrec;         // [M][Kp][rec_floats]
-    float2* wsT;         // [Kp][Op]
-    float2* partials;    // [kPrepBlocksX + kPrepBlocksW]
+    float xoff, scale, xadd;  // token coordinate fma(x - xoff, scale, xadd); threshold w * scale
+    double scale_d;           // exact mode: the same scale in fp64 for the exponentials
+    float v_sat, z_div;        // backward token z = -r / z_div
+    float pad_coord;          // coordinate of padded inputs k >= K (r = 0 there)
+    int rec_floats;           // 2 or 4
+    int exact;
+    float* xrec;              // [M][Kp][rec_floats]: LUT coordinates, or 2^tx in exact mode
+    float2* wsT;              // [Kp][Op]: LUT coordinates, or 2^-tw in exact mode
+    float* xrec_slow;         // exact mode: [M][Kp][rec_floats] with tx
+    float2* wsT_slow;         // exact mode: [Kp][Op] with tw
+    float2* partials;         // [kPrepBlocksX + kPrepBlocksW]
 };
 
 __device__ inline void block_minmax(float lo, float hi, float2* out) {
@@ -304,38 +318,47 @@ __device__ inline void block_minmax(float lo, float hi, float2* out) {
     }
 }
 
+__device__ inline void store_token(float* dst, int rec_floats, int64_t e, float c, float r, float z) {
+    if (rec_floats == 2)
+        reinterpret_cast<float2*>(dst)[e] = make_float2(c, r);
+    else
+        reinterpret_cast<float4*>(dst)[e] = make_float4(c, r, z, 0.0f);
+}
+
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     float lo = INFINITY, hi = -INFINITY;
     if (blockIdx.x < kPrepBlocksX) {
         // rows m are strided over the token-side blocks; threads walk k (coalesced)
-        const float pad_coord = (float)kPad + 1.0f;
         for (int64_t m = blockIdx.x; m < a.M; m += kPrepBlocksX) {
             const float* xrow = a.x + m * a.K;
             for (int k = threadIdx.x; k < (int)a.Kp; k += blockDim.x) {
-                float xs, r;
+                float c, r, f = 1.0f;
                 if (k < a.K) {
                     const float xv = xrow[k];
-                    xs = fmaf(xv - a.delta_min, a.scale, (float)kPad);
+                    c = fmaf(xv - a.xoff, a.scale, a.xadd);
                     r = 1.0f / (1.0f + xv / a.v_sat);
-                    const bool bad = xs != xs;
-                    lo = fminf(lo, bad ? -INFINITY : xs);
-                    hi = fmaxf(hi, bad ? INFINITY : xs);
+                    if (a.exact) f = (float)exp2((double)xv * a.scale_d);
+                    const bool bad = c != c;
+                    lo = fminf(lo, bad ? -INFINITY : c);
+                    hi = fmaxf(hi, bad ? INFINITY : c);
                 } else {
-                    xs = pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
+                    c = a.pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
                     r = 0.0f;
                 }
                 const int64_t e = m * a.Kp + k;
-                if (a.rec_floats == 2) {
-                    reinterpret_cast<float2*>(a.xrec)[e] = make_float2(xs, r);
+                const float z = -r / a.z_div;
+                if (a.exact) {
+                    store_token(a.xrec, a.rec_floats, e, f, r, z);
+                    store_token(a.xrec_slow, a.rec_floats, e, c, r, z);
                 } else {
-                    reinterpret_cast<float4*>(a.xrec)[e] = make_float4(xs, r, -r / a.v_sat, 0.0f);
+                    store_token(a.xrec, a.rec_floats, e, c, r, z);
                 }
             }
         }
         block_minmax(lo, hi, &a.partials[blockIdx.x]);
         return;
     }
-    // threshold side: 64(o) x 32(k) tiles transposed through LDS
+    // threshold side: 64(o) x 32(k) tiles of raw thresholds transposed through LDS
     __shared__ float2 tile[32][65];
     const int64_t n_ot = a.Op / 64, n_kt = (a.Kp + 31) / 32;  // Op: multiple of 256; Kp: of 8
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
@@ -349,10 +372,9 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
             if (k < a.K && a.O > 0) {
                 const bool real = o < a.O;
                 if (!real) o = a.O - 1;  // padded outputs copy a real row; results are dropped
-                const float p = a.wp[o * a.K + k] * a.scale;
-                const float q = a.wn[o * a.K + k] * a.scale;
-                v = make_float2(p, q);
+                v = make_float2(a.wp[o * a.K + k], a.wn[o * a.K + k]);
                 if (real) {
+                    const float p = v.x * a.scale, q = v.y * a.scale;
                     const bool bad = (p != p) || (q != q);
                     lo = fminf(lo, bad ? -INFINITY : fminf(p, q));
                     hi = fmaxf(hi, bad ? INFINITY : fmaxf(p, q));
@@ -365,8 +387,19 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
         for (int rr = ty; rr < 32; rr += 8) {
             const int64_t k = kt * 32 + rr;
             if (k < a.Kp) {
-                a.wsT[k * a.Op + ot * 64 + tx] = tile[rr][tx];
-                a.wsT[k * a.Op + ot * 64 + 32 + tx] = tile[rr][32 + tx];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float2 v = tile[rr][h * 32 + tx];
+                    const int64_t e = k * a.Op + ot * 64 + h * 32 + tx;
+                    const float2 c = make_float2(v.x * a.scale, v.y * a.scale);
+                    if (a.exact) {
+                        a.wsT[e] = make_float2((float)exp2(-(double)v.x * a.scale_d),
+                                               (float)exp2(-(double)v.y * a.scale_d));
+                        a.wsT_slow[e] = c;
+                    } else {
+                        a.wsT[e] = c;
+                    }
+                }
             }
         }
         __syncthreads();
@@ -374,9 +407,13 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     block_minmax(lo, hi, &a.partials[blockIdx.x]);
 }
 
-// Reads the prep partials and decides, identically in every wave, whether every cell
-// coordinate xs - ws lies in [1, NP-2] (then the padded table makes the clamp redundant).
-__device__ inline bool coords_in_padded_range(const float2* __restrict__ partials, int n_pad_entries) {
+// Range of the prep kernel's coordinates: token side (xlo, xhi), threshold side (wlo, whi),
+// wave-uniform.
+struct CoordRange {
+    float xlo, xhi, wlo, whi;
+};
+
+__device__ inline CoordRange read_coord_range(const float2* __restrict__ partials) {
     const int lane = threadIdx.x & 63;
     float xlo = INFINITY, xhi = -INFINITY, wlo = INFINITY, whi = -INFINITY;
     for (int i = lane; i < kPrepBlocksX; i += 64) {
@@ -395,7 +432,14 @@ __device__ inline bool coords_in_padded_range(const float2* __restrict__ partial
         wlo = fminf(wlo, __shfl_xor(wlo, off));
         whi = fmaxf(whi, __shfl_xor(whi, off));
     }
-    const bool ok = (xlo - whi >= 1.0f) && (xhi - wlo <= (float)(n_pad_entries - 2));
+    return CoordRange{xlo, xhi, wlo, whi};
+}
+
+// LUT kernels: every coordinate difference lies within the padded table, so the loop needs
+// no clamp (the kPad replicated end records reproduce the reference's clamp there).
+__device__ inline bool coords_in_padded_range(const float2* __restrict__ partials, int n_pad_entries) {
+    const CoordRange c = read_coord_range(partials);
+    const bool ok = (c.xlo - c.whi >= 1.0f) && (c.xhi - c.wlo <= (float)(n_pad_entries - 2));
     return __builtin_amdgcn_readfirstlane((int)ok) != 0;
 }
 
@@ -407,23 +451,185 @@ __device__ inline float coord(float xs, float ws, float cmin, float cmax) {
 }
 
 // ----------------------------------------------------------------------------------
+// Cell evaluators. The forward and backward loops are written once over a cell policy
+// that turns a token operand t (from the token record) and a threshold operand w (from
+// the threshold record) into the per-threshold current term l (forward) or the pair
+// (l, d) of current and derivative terms (backward), in the policy's units:
+//   LUT:   l = L_I(dV), d = L_D(dV) from the LDS table (physical units).
+//   exact: l = l1^2 - l2^2 and d = l1 s1 - l2 s2 with l_i = log2(1 + 2^t_i) and
+//          s_i = sigmoid, t1 = tx - tw, t2 = t1 - V_D a; the caller's constants
+//          I_S ln2^2 (current) and 2 a I_S ln2 (derivative, a in natural units) restore
+//          the reference's I_S [sp1^2 - sp2^2] and I_S 2/(2nU_T) [sp1 s1 - sp2 s2]
+//          (ekv_triton.py:33-66).
+// ----------------------------------------------------------------------------------
+
+// Cells take both thresholds of a (token, output, input) cell at once: forward cells return
+// l(+) - l(-); the LUT cells issue both gathers before using either.
+template <bool CLAMP>
+struct LutFwdCell {
+    const float2* lut;
+    float cmin, cmax;
+    __device__ float operator()(float xs, float wsp, float wsn) const {
+        const float cp = coord<CLAMP>(xs, wsp, cmin, cmax);
+        const float cn = coord<CLAMP>(xs, wsn, cmin, cmax);
+        const float2 ep = lut[(unsigned)cp];
+        const float2 en = lut[(unsigned)cn];
+        return fmaf(cp, ep.y, ep.x) - fmaf(cn, en.y, en.x);
+    }
+};
+
+// Backward cells return a pair view whose dp()/dn() (derivative terms) and lp()/ln()
+// (current terms) the loop reads where it uses them; the LUT view holds the two gathered
+// records and evaluates each term on demand.
+struct LutBwdPair {
+    float cp, cn;
+    float4 ep, en;
+    __device__ float dp() const { return fmaf(cp, ep.w, ep.z); }
+    __device__ float dn() const { return fmaf(cn, en.w, en.z); }
+    __device__ float lp() const { return fmaf(cp, ep.y, ep.x); }
+    __device__ float ln() const { return fmaf(cn, en.y, en.x); }
+};
+
+template <bool CLAMP, class Table>
+struct LutBwdCell {
+    Table lut;
+    float cmin, cmax;
+    __device__ LutBwdPair operator()(float xs, float wsp, float wsn) const {
+        LutBwdPair q;
+        q.cp = coord<CLAMP>(xs, wsp, cmin, cmax);
+        q.cn = coord<CLAMP>(xs, wsn, cmin, cmax);
+        q.ep = lut[(unsigned)q.cp];
+        q.en = lut[(unsigned)q.cn];
+        return q;
+    }
+};
+
+struct ValueBwdPair {
+    float l_p, d_p, l_n, d_n;
+    __device__ float dp() const { return d_p; }
+    __device__ float dn() const { return d_n; }
+    __device__ float lp() const { return l_p; }
+    __device__ float ln() const { return l_n; }
+};
+
+// log2(1 + 2^t) as torch's softplus (threshold 20 in natural units: t = 20 log2 e), in
+// log2 units; NaN propagates.
+constexpr float kSoftplusLog2Threshold = 28.853900817779268f;
+
+// log2(1 + e) for e >= 0, accurate to a few ulp also where 1 + e rounds (e << 1, the
+// subthreshold cells). With w = fl(1 + e), d = e - (w - 1) is w's rounding error, exactly,
+// and log2(w + d) = log2(w) + d / (w ln2) to second order. For e < 1, |d| <= 2^-25 and the
+// 1/w factor in (1/2, 1] is dropped at a relative cost below |d|; for e >= 1 the clamp keeps
+// the term below the rounding of log2(w) >= 1. v_log_f32 is accurate relative to its result.
+constexpr float kInvLn2 = 1.4426950408889634f;
+
+__device__ inline float log2_1p(float e) {
+    const float w = 1.0f + e;
+    const float d = e - (w - 1.0f);
+    return fmaf(__builtin_amdgcn_fmed3f(d, -0x1p-24f, 0x1p-24f), kInvLn2, __builtin_amdgcn_logf(w));
+}
+
+// Range-checked exact cells: operands 2^tx and 2^-tw with |tx|, |tw| <= kExactFastBound
+// and tx - tw <= kExactFastBound, so e = 2^(tx - tw) is a normal float below 2^60 and
+// log2(1 + e) equals the thresholded softplus to rounding.
+constexpr float kExactFastBound = 60.0f;
+
+struct ExactFastFwdCell {
+    float k2;  // 2^(-V_D a)
+    __device__ float one(float ex, float ew) const {
+        const float e1 = ex * ew, e2 = e1 * k2;
+        const float l1 = log2_1p(e1), l2 = log2_1p(e2);
+        return fmaf(l1, l1, -(l2 * l2));
+    }
+    __device__ float operator()(float ex, float ewp, float ewn) const { return one(ex, ewp) - one(ex, ewn); }
+};
+
+struct ExactFastBwdCell {
+    float k2;
+    __device__ void one(float ex, float ew, float& l, float& d) const {
+        const float e1 = ex * ew, e2 = e1 * k2;
+        const float w1 = 1.0f + e1, w2 = 1.0f + e2;
+        const float l1 = log2_1p(e1), l2 = log2_1p(e2);
+        const float s1 = e1 * __builtin_amdgcn_rcpf(w1), s2 = e2 * __builtin_amdgcn_rcpf(w2);
+        l = fmaf(l1, l1, -(l2 * l2));
+        d = fmaf(l1, s1, -(l2 * s2));
+    }
+    __device__ ValueBwdPair operator()(float ex, float ewp, float ewn) const {
+        ValueBwdPair q;
+        one(ex, ewp, q.l_p, q.d_p);
+        one(ex, ewn, q.l_n, q.d_n);
+        return q;
+    }
+};
+
+// General exact cells: any operands, including NaN and infinities.
+__device__ inline void softplus_log2(float t, float& l, float& s) {
+    const float e = __builtin_amdgcn_exp2f(t);
+    const bool lin = t > kSoftplusLog2Threshold;
+    l = lin ? t : log2_1p(e);
+    s = lin ? 1.0f : e * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+struct ExactGeneralFwdCell {
+    float c2;  // V_D a
+    __device__ float one(float tx, float tw) const {
+        const float t1 = tx - tw;
+        float l1, l2, s1, s2;
+        softplus_log2(t1, l1, s1);
+        softplus_log2(t1 - c2, l2, s2);
+        return fmaf(l1, l1, -(l2 * l2));
+    }
+    __device__ float operator()(float tx, float twp, float twn) const { return one(tx, twp) - one(tx, twn); }
+};
+
+struct ExactGeneralBwdCell {
+    float c2;
+    __device__ void one(float tx, float tw, float& l, float& d) const {
+        const float t1 = tx - tw;
+        float l1, l2, s1, s2;
+        softplus_log2(t1, l1, s1);
+        softplus_log2(t1 - c2, l2, s2);
+        l = fmaf(l1, l1, -(l2 * l2));
+        d = fmaf(l1, s1, -(l2 * s2));
+    }
+    __device__ ValueBwdPair operator()(float tx, float twp, float twn) const {
+        ValueBwdPair q;
+        one(tx, twp, q.l_p, q.d_p);
+        one(tx, twn, q.l_n, q.d_n);
+        return q;
+    }
+};
+
+__device__ inline bool exact_operands_in_fast_range(const float2* __restrict__ partials) {
+    const CoordRange c = read_coord_range(partials);
+    const float b = kExactFastBound;
+    const bool ok = c.xlo >= -b && c.xhi <= b && c.wlo >= -b && c.whi <= b && c.xhi - c.wlo <= b;
+    return __builtin_amdgcn_readfirstlane((int)ok) != 0;
+}
+
+// ----------------------------------------------------------------------------------
 // Forward. Block = FWD_WAVES waves sharing one LDS table and one output block of
 // 64*ORR outputs; wave w owns tokens [ (tile_m * FWD_WAVES + w) * MR, +MR ).
 // ----------------------------------------------------------------------------------
 
 struct FwdArgs {
-    const float2* xrec;     // [M][Kp] {xs, r}
-    const float2* wsT;      // [Kp][Op]
-    const float2* lut;      // [NP] {A_I, dI}
+    const float2* xrec;     // [M][Kp] token records {t, r}
+    const float2* wsT;      // [Kp][Op] threshold records
+    const float2* xrec_alt; // exact: general-loop token records {tx, r}
+    const float2* wsT_alt;  // exact: general-loop threshold records
+    const float2* lut;      // LUT: [NP] {A_I, dI}
     const float2* partials;
     float* out;             // [M][O]
     int M, O, Kp, Op, NP;
     int n_mt, n_ot;         // tiles along M (per block) and O
     float cmin, cmax, out_min, out_max;
+    float out_scale;        // exact: I_S ln2^2
+    float k2, c2;           // exact: 2^(-V_D a), V_D a
 };
 
-template <int MR, int ORR, bool CLAMP>
-__device__ inline void fwd_body(const FwdArgs& a, const float2* lut, int m0, int o_lane) {
+template <int MR, int ORR, bool CLAMP_OUT, class Cell>
+__device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2* xrec, const float2* wsT,
+                                int m0, int o_lane) {
     float acc[MR][ORR];
 #pragma unroll
     for (int i = 0; i < MR; ++i)
@@ -434,9 +640,9 @@ __device__ inline void fwd_body(const FwdArgs& a, const float2* lut, int m0, int
 #pragma unroll
     for (int i = 0; i < MR; ++i) {
         const int m = min(m0 + i, a.M - 1);
-        xrow[i] = a.xrec + (size_t)m * a.Kp;
+        xrow[i] = xrec + (size_t)m * a.Kp;
     }
-    const float4* wcol = reinterpret_cast<const float4*>(a.wsT + o_lane);
+    const float4* wcol = reinterpret_cast<const float4*>(wsT + o_lane);
     const size_t wstride = (size_t)a.Op / 2;  // float4 per k row
 
     constexpr int KU = 16 / MR;  // 32 SGPRs of token operands per step
@@ -458,13 +664,7 @@ __device__ inline void fwd_body(const FwdArgs& a, const float2* lut, int m0, int
                 const float2 xv = load_uniform2(xrow[i] + k0 + kk);
 #pragma unroll
                 for (int j = 0; j < ORR; ++j) {
-                    const float cp = coord<CLAMP>(xv.x, w[kk][j].x, a.cmin, a.cmax);
-                    const float cn = coord<CLAMP>(xv.x, w[kk][j].y, a.cmin, a.cmax);
-                    const float2 ep = lut[(unsigned)cp];
-                    const float2 en = lut[(unsigned)cn];
-                    const float lp = fmaf(cp, ep.y, ep.x);
-                    const float ln = fmaf(cn, en.y, en.x);
-                    acc[i][j] = fmaf(lp - ln, xv.y, acc[i][j]);
+                    acc[i][j] = fmaf(cell(xv.x, w[kk][j].x, w[kk][j].y), xv.y, acc[i][j]);
                 }
             }
         }
@@ -477,23 +677,21 @@ __device__ inline void fwd_body(const FwdArgs& a, const float2* lut, int m0, int
 #pragma unroll
         for (int j = 0; j < ORR; ++j) {
             const int o = o_lane + j;
-            if (o < a.O) orow[o] = fminf(fmaxf(acc[i][j], a.out_min), a.out_max);
+            if (o >= a.O) continue;
+            if (CLAMP_OUT)
+                orow[o] = fminf(fmaxf(acc[i][j], a.out_min), a.out_max);
+            else
+                orow[o] = acc[i][j] * a.out_scale;
         }
     }
 }
 
 constexpr int kFwdWaves = 8;
 
-template <int MR>
-__global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
-    extern __shared__ float2 s_lut_fwd[];
-    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
-    const bool fast = coords_in_padded_range(a.partials, a.NP);
-    __syncthreads();
-
-    // XCD-aware order: consecutive hardware block ids go round-robin over 8 XCDs; remap so
-    // the blocks of one XCD walk consecutive token tiles of the same output block and share
-    // that output block's threshold columns in their L2.
+// XCD-aware order: consecutive hardware block ids go round-robin over 8 XCDs; remap so
+// the blocks of one XCD walk consecutive token tiles of the same output block and share
+// that output block's threshold columns in their L2. Returns false for waves past M.
+__device__ inline bool fwd_tile(const FwdArgs& a, int MR, int& m0, int& o_lane) {
     const int nb = gridDim.x;
     const int bid = blockIdx.x;
     const int per_xcd = nb / 8;
@@ -501,16 +699,37 @@ __global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     if (per_xcd > 0 && bid < per_xcd * 8) t = (bid % 8) * per_xcd + bid / 8;
     const int tile_m = t % a.n_mt;
     const int tile_o = t / a.n_mt;
-
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int m0 = (tile_m * kFwdWaves + wave) * MR;
-    const int o_lane = tile_o * 64 * kFwdORR + lane * kFwdORR;
-    if (m0 >= a.M) return;
+    m0 = (tile_m * kFwdWaves + wave) * MR;
+    o_lane = tile_o * 64 * kFwdORR + lane * kFwdORR;
+    return m0 < a.M;
+}
+
+template <int MR>
+__global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
+    extern __shared__ float2 s_lut_fwd[];
+    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
+    const bool fast = coords_in_padded_range(a.partials, a.NP);
+    __syncthreads();
+    int m0, o_lane;
+    if (!fwd_tile(a, MR, m0, o_lane)) return;
     if (fast)
-        fwd_body<MR, kFwdORR, false>(a, s_lut_fwd, m0, o_lane);
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, m0, o_lane);
     else
-        fwd_body<MR, kFwdORR, true>(a, s_lut_fwd, m0, o_lane);
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, m0, o_lane);
+}
+
+// Exact-formula forward (reference: ekv_triton.py:69-91): same tiling, no table.
+template <int MR>
+__global__ __launch_bounds__(kFwdWaves * 64) void fwd_exact_kernel(FwdArgs a) {
+    const bool fast = exact_operands_in_fast_range(a.partials);
+    int m0, o_lane;
+    if (!fwd_tile(a, MR, m0, o_lane)) return;
+    if (fast)
+        fwd_body<MR, kFwdORR, false>(a, ExactFastFwdCell{a.k2}, a.xrec, a.wsT, m0, o_lane);
+    else
+        fwd_body<MR, kFwdORR, false>(a, ExactGeneralFwdCell{a.c2}, a.xrec_alt, a.wsT_alt, m0, o_lane);
 }
 
 // ----------------------------------------------------------------------------------
@@ -521,10 +740,12 @@ __global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
 // ----------------------------------------------------------------------------------
 
 struct BwdArgs {
-    const float4* xrec;     // [M][Kp] {xs, r, -r/V_sat, 0}
-    const float2* wsT;      // [Kp][Op]
+    const float4* xrec;     // [M][Kp] token records {t, r, -r / z_div, 0}
+    const float2* wsT;      // [Kp][Op] threshold records
+    const float4* xrec_alt; // exact: general-loop token records {tx, r, -r / z_div, 0}
+    const float2* wsT_alt;  // exact: general-loop threshold records
     const float* grad;      // [M][ldg]
-    const float4* lut;      // [NP] {A_I, dI, A_D, dD}
+    const float4* lut;      // LUT: [NP] {A_I, dI, A_D, dD}
     const float2* partials;
     float* dx_part;         // [n_ob][M][K]            (need_x)
     float* dv_part;         // [S][2][Kp][Op]          (need_w)
@@ -532,6 +753,7 @@ struct BwdArgs {
     int n_ob, n_kb, n_split, m_chunk;
     int n_items;
     float cmin, cmax;
+    float k2, c2;           // exact: 2^(-V_D a), V_D a
 };
 
 // LDS table views for the backward. Interleaved: one 16-byte record {A_I, dI, A_D, dD} per
@@ -552,8 +774,9 @@ struct BwdTableSplit {
     }
 };
 
-template <bool CLAMP, bool NEED_X, bool NEED_W, class Table>
-__device__ inline void bwd_body(const BwdArgs& a, Table lut, float* red, int item) {
+template <bool NEED_X, bool NEED_W, class Cell>
+__device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4* xrec, const float2* wsT,
+                                float* red, int item) {
     constexpr int ORR = kBwdORR, KR = kBwdKR, MB = kBwdMB;
     const int lane = threadIdx.x & 63;
     // inputs vary fastest: the waves of a block share (output block, token split), so the
@@ -570,7 +793,7 @@ __device__ inline void bwd_body(const BwdArgs& a, Table lut, float* red, int ite
     float2 w[KR][ORR];
 #pragma unroll
     for (int kk = 0; kk < KR; ++kk) {
-        const float4* src = reinterpret_cast<const float4*>(a.wsT + (size_t)(k0 + kk) * a.Op + o_lane);
+        const float4* src = reinterpret_cast<const float4*>(wsT + (size_t)(k0 + kk) * a.Op + o_lane);
 #pragma unroll
         for (int j = 0; j < ORR / 2; ++j) {
             const float4 v = src[j];
@@ -589,7 +812,7 @@ __device__ inline void bwd_body(const BwdArgs& a, Table lut, float* red, int ite
     const int my_quarter = lane & 3;
 
     // token m's operands are prefetched one step ahead (scalar token records, vector grads)
-    const float4* xbase = a.xrec + k0;
+    const float4* xbase = xrec + k0;
     const float* gbase = a.grad + o_lane;
     float4 xn[KR];
     float gn[ORR];
@@ -625,16 +848,13 @@ __device__ inline void bwd_body(const BwdArgs& a, Table lut, float* red, int ite
                     float x1 = 0.0f, x2 = 0.0f;
 #pragma unroll
                     for (int j = 0; j < ORR; ++j) {
-                        const float cp = coord<CLAMP>(xv.x, w[kk][j].x, a.cmin, a.cmax);
-                        const float cn = coord<CLAMP>(xv.x, w[kk][j].y, a.cmin, a.cmax);
-                        const float4 ep = lut[(unsigned)cp];
-                        const float4 en = lut[(unsigned)cn];
-                        const float dp = fmaf(cp, ep.w, ep.z);
-                        const float dn = fmaf(cn, en.w, en.z);
+                        const auto q = cell(xv.x, w[kk][j].x, w[kk][j].y);
+                        const float dp = q.dp();
+                        const float dn = q.dn();
                         const float gr = g[j] * xv.y;
                         if (NEED_X) {
-                            const float lp = fmaf(cp, ep.y, ep.x);
-                            const float ln = fmaf(cn, en.y, en.x);
+                            const float lp = q.lp();
+                            const float ln = q.ln();
                             x1 = fmaf(gr, dp - dn, x1);
                             x2 = fmaf(gr, lp - ln, x2);
                         }
@@ -643,7 +863,7 @@ __device__ inline void bwd_body(const BwdArgs& a, Table lut, float* red, int ite
                             accn[kk][j] = fmaf(gr, dn, accn[kk][j]);
                         }
                     }
-                    tv[kk] = fmaf(x2, xv.z, x1);  // r*sum(G dL') - r^2/V_sat*sum(G dL)
+                    tv[kk] = fmaf(x2, xv.z, x1);  // r*sum(G L_D) - r^2/V_sat*sum(G L_I), in d units
                     // keep one input's gathers in flight at a time: bounds register pressure
                     // to the 128 VGPRs of a 16-wave block; other waves hide the LDS latency
                     if (ISA_EKV_BWD_SCHED) __builtin_amdgcn_sched_barrier(0);
@@ -718,35 +938,51 @@ __global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
     float* red = reinterpret_cast<float*>(s_lut_bwd + table_records) + wave * (kBwdMB * kBwdKR * kRedStride);
     const int item = blockIdx.x * waves + wave;
     if (item >= a.n_items) return;
-    if constexpr (SPLIT) {
-        const BwdTableSplit t{s_split};
-        if (fast)
-            bwd_body<false, NEED_X, NEED_W>(a, t, red, item);
-        else
-            bwd_body<true, NEED_X, NEED_W>(a, t, red, item);
-    } else {
-        const BwdTableInterleaved t{s_lut_bwd};
-        if (fast)
-            bwd_body<false, NEED_X, NEED_W>(a, t, red, item);
-        else
-            bwd_body<true, NEED_X, NEED_W>(a, t, red, item);
-    }
+    using Table = typename std::conditional<SPLIT, BwdTableSplit, BwdTableInterleaved>::type;
+    Table t;
+    if constexpr (SPLIT)
+        t = BwdTableSplit{s_split};
+    else
+        t = BwdTableInterleaved{s_lut_bwd};
+    if (fast)
+        bwd_body<NEED_X, NEED_W>(a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+    else
+        bwd_body<NEED_X, NEED_W>(a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
 }
 
-// dX[m,k] = sum over output blocks, in block order (deterministic)
+// Exact-formula backward (reference: ekv_triton.py:94-169): same work decomposition; LDS
+// holds only the dX transpose buffers.
+template <bool NEED_X, bool NEED_W>
+__global__ __launch_bounds__(1024) void bwd_exact_kernel(BwdArgs a) {
+    extern __shared__ float4 s_red_exact[];
+    const bool fast = exact_operands_in_fast_range(a.partials);
+    const int waves = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* red = reinterpret_cast<float*>(s_red_exact) + wave * (kBwdMB * kBwdKR * kRedStride);
+    const int item = blockIdx.x * waves + wave;
+    if (item >= a.n_items) return;
+    if (fast)
+        bwd_body<NEED_X, NEED_W>(a, ExactFastBwdCell{a.k2}, a.xrec, a.wsT, red, item);
+    else
+        bwd_body<NEED_X, NEED_W>(a, ExactGeneralBwdCell{a.c2}, a.xrec_alt, a.wsT_alt, red, item);
+}
+
+// dX[m,k] = scale * sum over output blocks, in block order (deterministic); scale is 1 for
+// the LUT path and the derivative constant of the exact cells
 __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict__ part, int n_ob,
-                                                        int64_t n, float* __restrict__ dx) {
+                                                        int64_t n, float scale, float* __restrict__ dx) {
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
          e += (int64_t)gridDim.x * blockDim.x) {
         float s = part[e];
         for (int b = 1; b < n_ob; ++b) s += part[(size_t)b * n + e];
-        dx[e] = s;
+        dx[e] = s * scale;
     }
 }
 
-// dVth+[o,k] = -sum_s P[s][0][k][o], dVth-[o,k] = +sum_s P[s][1][k][o]; 32x32 transpose tiles
+// dVth+[o,k] = -scale * sum_s P[s][0][k][o], dVth-[o,k] = +scale * sum_s P[s][1][k][o];
+// 32x32 transpose tiles
 __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict__ part, int n_split,
-                                                        int K, int O, int Kp, int Op,
+                                                        int K, int O, int Kp, int Op, float scale,
                                                         float* __restrict__ dvp, float* __restrict__ dvn) {
     __shared__ float tile[2][32][33];
     const int n_ot = (O + 31) / 32, n_kt = (K + 31) / 32;
@@ -764,8 +1000,8 @@ __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict_
                     sn += part[(size_t)s * 2 * plane + plane + e];
                 }
             }
-            tile[0][rr][tx] = -sp;
-            tile[1][rr][tx] = sn;
+            tile[0][rr][tx] = -sp * scale;
+            tile[1][rr][tx] = sn * scale;
         }
         __syncthreads();
         for (int rr = ty; rr < 32; rr += 8) {
@@ -786,10 +1022,10 @@ __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict_
 struct FwdPlan {
     int64_t Kp, Op;
     int mr, n_mt, n_ot, blocks;
-    size_t off_xrec, off_wsT, off_part, bytes;
+    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, bytes;
 };
 
-FwdPlan plan_forward(int64_t M, int64_t K, int64_t O) {
+FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
     FwdPlan p{};
     p.Kp = round_up(K > 0 ? K : 1, 8);
     p.Op = round_up(O > 0 ? O : 1, 64 * kFwdORR);
@@ -801,11 +1037,17 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O) {
     const int64_t tokens_per_block = (int64_t)kFwdWaves * p.mr;
     p.n_mt = (int)((M + tokens_per_block - 1) / tokens_per_block);
     p.blocks = p.n_mt * p.n_ot;
+    const size_t xrec_bytes = (size_t)round_up((int64_t)M * p.Kp * 8, 256);
+    const size_t wsT_bytes = (size_t)round_up(p.Kp * p.Op * 8, 256);
     size_t off = 0;
     p.off_xrec = off;
-    off += (size_t)round_up((int64_t)M * p.Kp * 8, 256);
+    off += xrec_bytes;
     p.off_wsT = off;
-    off += (size_t)round_up(p.Kp * p.Op * 8, 256);
+    off += wsT_bytes;
+    p.off_xrec_alt = off;
+    if (exact) off += xrec_bytes;
+    p.off_wsT_alt = off;
+    if (exact) off += wsT_bytes;
     p.off_part = off;
     off += (size_t)(kPrepBlocksX + kPrepBlocksW) * 8;
     p.bytes = round_up((int64_t)off, 256);
@@ -816,18 +1058,20 @@ struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
     bool grad_padded, split;
-    size_t off_xrec, off_wsT, off_part, off_gpad, off_dx, off_dv, bytes, lds_bytes;
+    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_gpad, off_dx, off_dv, bytes, lds_bytes;
 };
 
+// n_entries = 0 plans the exact-formula backward (no LDS table, general-loop records).
 BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_x, bool need_w) {
     BwdPlan p{};
+    const bool exact = n_entries == 0;
     p.Kp = round_up(K > 0 ? K : 1, 8);
     p.Op = round_up(O > 0 ? O : 1, 64 * kBwdORR);
     p.n_ob = (int)(p.Op / (64 * kBwdORR));
     p.n_kb = (int)(p.Kp / kBwdKR);
     const size_t red_bytes = (size_t)kBwdMB * kBwdKR * kRedStride * 4;
-    p.split = ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
-    const size_t lut_bytes = (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
+    p.split = !exact && ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
+    const size_t lut_bytes = exact ? 0 : (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
     int wpb = 16;
     while (wpb > 1 && lut_bytes + wpb * red_bytes > (size_t)kLdsBytes) wpb /= 2;
     p.waves_per_block = wpb;
@@ -846,11 +1090,17 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     p.n_items = (int)(base_items * p.n_split);
     p.blocks = (p.n_items + wpb - 1) / wpb;
     p.grad_padded = (O % (64 * kBwdORR)) != 0;
+    const size_t xrec_bytes = (size_t)round_up((int64_t)M * p.Kp * 16, 256);
+    const size_t wsT_bytes = (size_t)round_up(p.Kp * p.Op * 8, 256);
     size_t off = 0;
     p.off_xrec = off;
-    off += (size_t)round_up((int64_t)M * p.Kp * 16, 256);
+    off += xrec_bytes;
     p.off_wsT = off;
-    off += (size_t)round_up(p.Kp * p.Op * 8, 256);
+    off += wsT_bytes;
+    p.off_xrec_alt = off;
+    if (exact) off += xrec_bytes;
+    p.off_wsT_alt = off;
+    if (exact) off += wsT_bytes;
     p.off_part = off;
     off += (size_t)round_up((kPrepBlocksX + kPrepBlocksW) * 8, 256);
     p.off_gpad = off;
@@ -873,8 +1123,23 @@ __global__ __launch_bounds__(256) void pad_grad_kernel(const float* __restrict__
     }
 }
 
-void launch_forward(int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+// Zero fill by kernel (not hipMemsetAsync), so a caller may capture the call in a graph.
+__global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_t n) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x)
+        p[e] = 0.0f;
+}
+
+void launch_forward(bool exact, int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
     const dim3 block(kFwdWaves * 64);
+    if (exact) {
+        if (mr == 8)
+            hipLaunchKernelGGL(fwd_exact_kernel<8>, grid, block, 0, s, fa);
+        else if (mr == 4)
+            hipLaunchKernelGGL(fwd_exact_kernel<4>, grid, block, 0, s, fa);
+        else
+            hipLaunchKernelGGL(fwd_exact_kernel<2>, grid, block, 0, s, fa);
+        return;
+    }
     if (mr == 8)
         hipLaunchKernelGGL(fwd_kernel<8>, grid, block, lds, s, fa);
     else if (mr == 4)
@@ -894,26 +1159,269 @@ void launch_backward_layout(bool need_x, bool need_w, dim3 grid, dim3 block, siz
         hipLaunchKernelGGL((bwd_kernel<false, true, SPLIT>), grid, block, lds, s, ba);
 }
 
-void launch_backward(bool need_x, bool need_w, bool split, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                     const BwdArgs& ba) {
-    if (split)
+void launch_backward(bool exact, bool need_x, bool need_w, bool split, dim3 grid, dim3 block, size_t lds,
+                     hipStream_t s, const BwdArgs& ba) {
+    if (exact) {
+        if (need_x && need_w)
+            hipLaunchKernelGGL((bwd_exact_kernel<true, true>), grid, block, lds, s, ba);
+        else if (need_x)
+            hipLaunchKernelGGL((bwd_exact_kernel<true, false>), grid, block, lds, s, ba);
+        else
+            hipLaunchKernelGGL((bwd_exact_kernel<false, true>), grid, block, lds, s, ba);
+    } else if (split) {
         launch_backward_layout<true>(need_x, need_w, grid, block, lds, s, ba);
-    else
+    } else {
         launch_backward_layout<false>(need_x, need_w, grid, block, lds, s, ba);
+    }
+}
+
+int check_shapes(const float* x, const float* wp, const float* wn, int64_t M, int64_t K, int64_t O, float v_sat) {
+    if (M < 0 || K < 0 || O < 0) return fail(ISA_EKV_EINVAL, "negative shape (M=%lld, K=%lld, O=%lld)",
+                                             (long long)M, (long long)K, (long long)O);
+    if (M > INT32_MAX / 2 || K > INT32_MAX / 2 || O > INT32_MAX / 2)
+        return fail(ISA_EKV_EINVAL, "shape too large for 32-bit tile indices");
+    if (!(v_sat != 0.0f)) return fail(ISA_EKV_EINVAL, "V_sat must be nonzero");
+    if (M * K > 0 && !x) return fail(ISA_EKV_EINVAL, "x is null");
+    if (O * K > 0 && (!wp || !wn)) return fail(ISA_EKV_EINVAL, "vth_pos/vth_neg is null");
+    return 0;
 }
 
 int check_common(const float* x, const float* wp, const float* wn, const void* lut, int64_t M, int64_t K,
                  int64_t O, int n_entries, float delta_min, float delta_max, float v_sat) {
     if (M < 0 || K < 0 || O < 0) return fail(ISA_EKV_EINVAL, "negative shape (M=%lld, K=%lld, O=%lld)",
                                              (long long)M, (long long)K, (long long)O);
-    if (M > INT32_MAX / 2 || K > INT32_MAX / 2 || O > INT32_MAX / 2)
-        return fail(ISA_EKV_EINVAL, "shape too large for 32-bit tile indices");
     if (n_entries < 1) return fail(ISA_EKV_EINVAL, "LUT_DELTA_SIZE must be >= 1 (got %d)", n_entries);
     if (!(delta_max > delta_min)) return fail(ISA_EKV_EINVAL, "LUT range must satisfy delta_max > delta_min");
-    if (!(v_sat != 0.0f)) return fail(ISA_EKV_EINVAL, "V_sat must be nonzero");
-    if (M * K > 0 && !x) return fail(ISA_EKV_EINVAL, "x is null");
-    if (O * K > 0 && (!wp || !wn)) return fail(ISA_EKV_EINVAL, "vth_pos/vth_neg is null");
+    const int rc = check_shapes(x, wp, wn, M, K, O, v_sat);
+    if (rc) return rc;
     if (!lut) return fail(ISA_EKV_EINVAL, "lut is null");
+    return 0;
+}
+
+// Operand transform of one call: LUT coordinates, or the exact formula's log2-unit operands.
+struct CallSetup {
+    bool exact;
+    const void* lut;  // LUT records
+    int n_entries;
+    float delta_min, delta_max;
+    double a_log2;    // exact: log2(e) / (2 n U_T)
+    float k2, c2;     // exact: 2^(-V_D a_log2), V_D a_log2
+    double cur_scale; // exact: I_S ln2^2 (current constant of the cells)
+    double der_scale; // exact: 2 I_S ln2 / (2 n U_T) (derivative constant of the cells)
+};
+
+CallSetup lut_setup(const void* lut, int n_entries, float delta_min, float delta_max) {
+    CallSetup cs{};
+    cs.lut = lut;
+    cs.n_entries = n_entries;
+    cs.delta_min = delta_min;
+    cs.delta_max = delta_max;
+    return cs;
+}
+
+int exact_setup(const double* params, CallSetup* cs) {
+    if (!params) return fail(ISA_EKV_EINVAL, "params is null");
+    const double n = params[0], u_t = params[1], i_s = params[2], v_d = params[3];
+    if (!(n > 0.0) || !(u_t > 0.0) || !std::isfinite(n * u_t))
+        return fail(ISA_EKV_EINVAL, "n and U_T must be positive and finite");
+    if (!std::isfinite(i_s) || !std::isfinite(v_d)) return fail(ISA_EKV_EINVAL, "I_S and V_D must be finite");
+    const double ln2 = 0.69314718055994530942;
+    const double inv_2nut = 1.0 / (2.0 * n * u_t);
+    *cs = CallSetup{};
+    cs->exact = true;
+    cs->a_log2 = inv_2nut / ln2;
+    cs->c2 = (float)(v_d * cs->a_log2);
+    cs->k2 = (float)std::exp2(-v_d * cs->a_log2);
+    cs->cur_scale = i_s * ln2 * ln2;
+    cs->der_scale = 2.0 * i_s * inv_2nut * ln2;
+    if (!(cs->a_log2 < 1e30)) return fail(ISA_EKV_EINVAL, "2 n U_T too small");
+    return 0;
+}
+
+PrepArgs make_prep(const CallSetup& cs, const float* x, const float* wp, const float* wn, int64_t M, int64_t K,
+                   int64_t O, int64_t Kp, int64_t Op, float v_sat, int rec_floats, char* ws, size_t off_xrec,
+                   size_t off_wsT, size_t off_xrec_alt, size_t off_wsT_alt, size_t off_part) {
+    PrepArgs pa{};
+    pa.x = x;
+    pa.wp = wp;
+    pa.wn = wn;
+    pa.M = M;
+    pa.K = K;
+    pa.O = O;
+    pa.Kp = Kp;
+    pa.Op = Op;
+    pa.v_sat = v_sat;
+    pa.rec_floats = rec_floats;
+    pa.xrec = reinterpret_cast<float*>(ws + off_xrec);
+    pa.wsT = reinterpret_cast<float2*>(ws + off_wsT);
+    pa.partials = reinterpret_cast<float2*>(ws + off_part);
+    if (!cs.exact) {
+        const int n = cs.n_entries;
+        const double scale_d = n > 1 ? (double)(n - 1) / ((double)cs.delta_max - (double)cs.delta_min) : 0.0;
+        pa.xoff = cs.delta_min;
+        pa.scale = (float)scale_d;
+        pa.xadd = (float)kPad;
+        pa.scale_d = scale_d;
+        pa.z_div = v_sat;
+        pa.pad_coord = (float)kPad + 1.0f;
+        pa.exact = 0;
+    } else {
+        pa.xoff = 0.0f;
+        pa.scale = (float)cs.a_log2;
+        pa.xadd = 0.0f;
+        pa.scale_d = cs.a_log2;
+        pa.z_div = (float)((double)v_sat * cs.der_scale / cs.cur_scale);
+        pa.pad_coord = 0.0f;
+        pa.exact = 1;
+        pa.xrec_slow = reinterpret_cast<float*>(ws + off_xrec_alt);
+        pa.wsT_slow = reinterpret_cast<float2*>(ws + off_wsT_alt);
+    }
+    return pa;
+}
+
+int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg, int64_t M,
+                int64_t K, int64_t O, float v_sat, float out_min, float out_max, float* out, void* workspace,
+                size_t workspace_bytes, hipStream_t s) {
+    if (M == 0 || O == 0) return 0;
+    if (!out) return fail(ISA_EKV_EINVAL, "out is null");
+    const FwdPlan p = plan_forward(M, K, O, cs.exact);
+    if (!workspace || workspace_bytes < p.bytes)
+        return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
+    char* ws = static_cast<char*>(workspace);
+    CallTimer call_timer(s, 2);
+    const PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 2, ws, p.off_xrec, p.off_wsT,
+                                  p.off_xrec_alt, p.off_wsT_alt, p.off_part);
+    hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "forward prep launch");
+    FwdArgs fa{};
+    fa.xrec = reinterpret_cast<const float2*>(ws + p.off_xrec);
+    fa.wsT = reinterpret_cast<const float2*>(ws + p.off_wsT);
+    fa.xrec_alt = reinterpret_cast<const float2*>(ws + p.off_xrec_alt);
+    fa.wsT_alt = reinterpret_cast<const float2*>(ws + p.off_wsT_alt);
+    fa.partials = reinterpret_cast<const float2*>(ws + p.off_part);
+    fa.out = out;
+    fa.M = (int)M;
+    fa.O = (int)O;
+    fa.Kp = (int)p.Kp;
+    fa.Op = (int)p.Op;
+    fa.n_mt = p.n_mt;
+    fa.n_ot = p.n_ot;
+    fa.out_min = out_min;
+    fa.out_max = out_max;
+    size_t lds = 0;
+    if (cs.exact) {
+        fa.out_scale = (float)cs.cur_scale;
+        fa.k2 = cs.k2;
+        fa.c2 = cs.c2;
+    } else {
+        fa.lut = static_cast<const float2*>(cs.lut);
+        fa.NP = cs.n_entries + 2 * kPad;
+        fa.cmin = (float)kPad;
+        fa.cmax = (float)(kPad + cs.n_entries - 1);
+        fa.out_scale = 1.0f;
+        lds = (size_t)fa.NP * 8;
+    }
+    ProfiledLaunch* prof;
+    prof_start(s, 0, &prof);
+    launch_forward(cs.exact, p.mr, dim3(p.blocks), lds, s, fa);
+    err = hipGetLastError();
+    prof_stop(s, prof);
+    if (err != hipSuccess) return hip_fail(err, "forward launch");
+    return 0;
+}
+
+int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg,
+                 const float* grad_out, int64_t M, int64_t K, int64_t O, float v_sat, float* grad_x,
+                 float* grad_vth_pos, float* grad_vth_neg, void* workspace, size_t workspace_bytes, hipStream_t s) {
+    const bool need_x = grad_x != nullptr;
+    const bool need_w = grad_vth_pos != nullptr || grad_vth_neg != nullptr;
+    if (need_w && (grad_vth_pos == nullptr || grad_vth_neg == nullptr))
+        return fail(ISA_EKV_EINVAL, "grad_vth_pos and grad_vth_neg must both be given or both be null");
+    if (!need_x && !need_w) return 0;
+    hipError_t err;
+    // degenerate shapes: empty reductions give zero gradients
+    if (M == 0 || O == 0 || K == 0) {
+        if (need_x && M * K > 0) hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, s, grad_x, M * K);
+        if (need_w && O * K > 0) {
+            hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, s, grad_vth_pos, O * K);
+            hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, s, grad_vth_neg, O * K);
+        }
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "zero fill launch");
+        return 0;
+    }
+    if (!grad_out) return fail(ISA_EKV_EINVAL, "grad_out is null");
+    const BwdPlan p = plan_backward(M, K, O, cs.exact ? 0 : cs.n_entries, need_x, need_w);
+    if (!workspace || workspace_bytes < p.bytes)
+        return fail(ISA_EKV_EINVAL, "backward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
+    char* ws = static_cast<char*>(workspace);
+    CallTimer call_timer(s, 3);
+    const PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 4, ws, p.off_xrec, p.off_wsT,
+                                  p.off_xrec_alt, p.off_wsT_alt, p.off_part);
+    hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "backward prep launch");
+    const float* g = grad_out;
+    int ldg = (int)O;
+    if (p.grad_padded) {
+        float* gp = reinterpret_cast<float*>(ws + p.off_gpad);
+        hipLaunchKernelGGL(pad_grad_kernel, dim3(1024), dim3(256), 0, s, grad_out, M, O, p.Op, gp);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "grad pad launch");
+        g = gp;
+        ldg = (int)p.Op;
+    }
+    BwdArgs ba{};
+    ba.xrec = reinterpret_cast<const float4*>(ws + p.off_xrec);
+    ba.wsT = reinterpret_cast<const float2*>(ws + p.off_wsT);
+    ba.xrec_alt = reinterpret_cast<const float4*>(ws + p.off_xrec_alt);
+    ba.wsT_alt = reinterpret_cast<const float2*>(ws + p.off_wsT_alt);
+    ba.grad = g;
+    ba.partials = reinterpret_cast<const float2*>(ws + p.off_part);
+    ba.dx_part = reinterpret_cast<float*>(ws + p.off_dx);
+    ba.dv_part = reinterpret_cast<float*>(ws + p.off_dv);
+    ba.M = (int)M;
+    ba.K = (int)K;
+    ba.O = (int)O;
+    ba.Kp = (int)p.Kp;
+    ba.Op = (int)p.Op;
+    ba.ldg = ldg;
+    ba.n_ob = p.n_ob;
+    ba.n_kb = p.n_kb;
+    ba.n_split = p.n_split;
+    ba.m_chunk = p.m_chunk;
+    ba.n_items = p.n_items;
+    float scale = 1.0f;
+    if (cs.exact) {
+        ba.k2 = cs.k2;
+        ba.c2 = cs.c2;
+        scale = (float)cs.der_scale;
+    } else {
+        ba.lut = static_cast<const float4*>(cs.lut);
+        ba.NP = cs.n_entries + 2 * kPad;
+        ba.cmin = (float)kPad;
+        ba.cmax = (float)(kPad + cs.n_entries - 1);
+    }
+    const dim3 grid(p.blocks), block(p.waves_per_block * 64);
+    ProfiledLaunch* prof;
+    prof_start(s, 1, &prof);
+    launch_backward(cs.exact, need_x, need_w, p.split, grid, block, p.lds_bytes, s, ba);
+    err = hipGetLastError();
+    prof_stop(s, prof);
+    if (err != hipSuccess) return hip_fail(err, "backward launch");
+    if (need_x) {
+        hipLaunchKernelGGL(dx_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dx),
+                           p.n_ob, M * K, scale, grad_x);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
+    }
+    if (need_w) {
+        hipLaunchKernelGGL(dv_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dv),
+                           p.n_split, (int)K, (int)O, (int)p.Kp, (int)p.Op, scale, grad_vth_pos, grad_vth_neg);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "dv reduce launch");
+    }
     return 0;
 }
 
@@ -1015,46 +1523,20 @@ int isa_ekv_profile_end(double* ms, int* launches) {
 
 size_t isa_ekv_forward_workspace(int64_t M, int64_t K, int64_t O) {
     if (M < 0 || K < 0 || O < 0) return 0;
-    return plan_forward(M, K, O).bytes;
+    return plan_forward(M, K, O, false).bytes;
 }
 
 int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd, int64_t M,
                     int64_t K, int64_t O, int n_entries, float delta_min, float delta_max, float v_sat,
                     float out_min, float out_max, float* out, void* workspace, size_t workspace_bytes,
                     void* stream) {
-    int rc = check_common(x, vth_pos, vth_neg, lut_fwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
+    const int rc = check_common(x, vth_pos, vth_neg, lut_fwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
     if (rc) return rc;
     if (n_entries > kMaxEntriesFwd)
         return fail(ISA_EKV_EINVAL, "LDS-resident forward supports LUT_DELTA_SIZE <= %d (got %d)",
                     kMaxEntriesFwd, n_entries);
-    if (M == 0 || O == 0) return 0;
-    if (!out) return fail(ISA_EKV_EINVAL, "out is null");
-    const FwdPlan p = plan_forward(M, K, O);
-    if (!workspace || workspace_bytes < p.bytes)
-        return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    char* ws = static_cast<char*>(workspace);
-    CallTimer call_timer(s, 2);
-    const double scale_d = n_entries > 1 ? (double)(n_entries - 1) / ((double)delta_max - (double)delta_min) : 0.0;
-    PrepArgs pa{x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, delta_min, (float)scale_d, v_sat, 2,
-                reinterpret_cast<float*>(ws + p.off_xrec), reinterpret_cast<float2*>(ws + p.off_wsT),
-                reinterpret_cast<float2*>(ws + p.off_part)};
-    hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return hip_fail(err, "forward prep launch");
-    const int np = n_entries + 2 * kPad;
-    FwdArgs fa{reinterpret_cast<const float2*>(ws + p.off_xrec), reinterpret_cast<const float2*>(ws + p.off_wsT),
-               static_cast<const float2*>(lut_fwd), reinterpret_cast<const float2*>(ws + p.off_part), out,
-               (int)M, (int)O, (int)p.Kp, (int)p.Op, np, p.n_mt, p.n_ot,
-               (float)kPad, (float)(kPad + n_entries - 1), out_min, out_max};
-    const size_t lds = (size_t)np * 8;
-    ProfiledLaunch* prof;
-    prof_start(s, 0, &prof);
-    launch_forward(p.mr, dim3(p.blocks), lds, s, fa);
-    err = hipGetLastError();
-    prof_stop(s, prof);
-    if (err != hipSuccess) return hip_fail(err, "forward launch");
-    return 0;
+    return run_forward(lut_setup(lut_fwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, M, K, O, v_sat,
+                       out_min, out_max, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 size_t isa_ekv_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x,
@@ -1067,80 +1549,48 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
                      const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries, float delta_min,
                      float delta_max, float v_sat, float* grad_x, float* grad_vth_pos, float* grad_vth_neg,
                      void* workspace, size_t workspace_bytes, void* stream) {
-    int rc = check_common(x, vth_pos, vth_neg, lut_bwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
+    const int rc = check_common(x, vth_pos, vth_neg, lut_bwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
     if (rc) return rc;
     if (n_entries > kMaxEntriesBwd)
         return fail(ISA_EKV_EINVAL, "shared backward supports LUT_DELTA_SIZE <= %d", kMaxEntriesBwd);
-    const bool need_x = grad_x != nullptr;
-    const bool need_w = grad_vth_pos != nullptr || grad_vth_neg != nullptr;
-    if (need_w && (grad_vth_pos == nullptr || grad_vth_neg == nullptr))
-        return fail(ISA_EKV_EINVAL, "grad_vth_pos and grad_vth_neg must both be given or both be null");
-    if (!need_x && !need_w) return 0;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t err;
-    // degenerate shapes: empty reductions give zero gradients
-    if (M == 0 || O == 0 || K == 0) {
-        if (need_x && M * K > 0) {
-            err = hipMemsetAsync(grad_x, 0, (size_t)(M * K) * 4, s);
-            if (err != hipSuccess) return hip_fail(err, "grad_x zero fill");
-        }
-        if (need_w && O * K > 0) {
-            err = hipMemsetAsync(grad_vth_pos, 0, (size_t)(O * K) * 4, s);
-            if (err == hipSuccess) err = hipMemsetAsync(grad_vth_neg, 0, (size_t)(O * K) * 4, s);
-            if (err != hipSuccess) return hip_fail(err, "grad_vth zero fill");
-        }
-        return 0;
-    }
-    if (!grad_out) return fail(ISA_EKV_EINVAL, "grad_out is null");
-    const BwdPlan p = plan_backward(M, K, O, n_entries, need_x, need_w);
-    if (!workspace || workspace_bytes < p.bytes)
-        return fail(ISA_EKV_EINVAL, "backward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
-    char* ws = static_cast<char*>(workspace);
-    CallTimer call_timer(s, 3);
-    const double scale_d = n_entries > 1 ? (double)(n_entries - 1) / ((double)delta_max - (double)delta_min) : 0.0;
-    PrepArgs pa{x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, delta_min, (float)scale_d, v_sat, 4,
-                reinterpret_cast<float*>(ws + p.off_xrec), reinterpret_cast<float2*>(ws + p.off_wsT),
-                reinterpret_cast<float2*>(ws + p.off_part)};
-    hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
-    err = hipGetLastError();
-    if (err != hipSuccess) return hip_fail(err, "backward prep launch");
-    const float* g = grad_out;
-    int ldg = (int)O;
-    if (p.grad_padded) {
-        float* gp = reinterpret_cast<float*>(ws + p.off_gpad);
-        hipLaunchKernelGGL(pad_grad_kernel, dim3(1024), dim3(256), 0, s, grad_out, M, O, p.Op, gp);
-        err = hipGetLastError();
-        if (err != hipSuccess) return hip_fail(err, "grad pad launch");
-        g = gp;
-        ldg = (int)p.Op;
-    }
-    const int np = n_entries + 2 * kPad;
-    BwdArgs ba{reinterpret_cast<const float4*>(ws + p.off_xrec), reinterpret_cast<const float2*>(ws + p.off_wsT),
-               g, static_cast<const float4*>(lut_bwd), reinterpret_cast<const float2*>(ws + p.off_part),
-               reinterpret_cast<float*>(ws + p.off_dx), reinterpret_cast<float*>(ws + p.off_dv),
-               (int)M, (int)K, (int)O, (int)p.Kp, (int)p.Op, ldg, np,
-               p.n_ob, p.n_kb, p.n_split, p.m_chunk, p.n_items,
-               (float)kPad, (float)(kPad + n_entries - 1)};
-    const dim3 grid(p.blocks), block(p.waves_per_block * 64);
-    ProfiledLaunch* prof;
-    prof_start(s, 1, &prof);
-    launch_backward(need_x, need_w, p.split, grid, block, p.lds_bytes, s, ba);
-    err = hipGetLastError();
-    prof_stop(s, prof);
-    if (err != hipSuccess) return hip_fail(err, "backward launch");
-    if (need_x) {
-        hipLaunchKernelGGL(dx_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dx),
-                           p.n_ob, M * K, grad_x);
-        err = hipGetLastError();
-        if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
-    }
-    if (need_w) {
-        hipLaunchKernelGGL(dv_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dv),
-                           p.n_split, (int)K, (int)O, (int)p.Kp, (int)p.Op, grad_vth_pos, grad_vth_neg);
-        err = hipGetLastError();
-        if (err != hipSuccess) return hip_fail(err, "dv reduce launch");
-    }
-    return 0;
+    return run_backward(lut_setup(lut_bwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, grad_out, M, K,
+                        O, v_sat, grad_x, grad_vth_pos, grad_vth_neg, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(stream));
+}
+
+size_t isa_ekv_exact_forward_workspace(int64_t M, int64_t K, int64_t O) {
+    if (M < 0 || K < 0 || O < 0) return 0;
+    return plan_forward(M, K, O, true).bytes;
+}
+
+int isa_ekv_exact_forward(const float* x, const float* vth_pos, const float* vth_neg, int64_t M, int64_t K,
+                          int64_t O, const double params[4], float v_sat, float* out, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    int rc = check_shapes(x, vth_pos, vth_neg, M, K, O, v_sat);
+    if (rc) return rc;
+    CallSetup cs;
+    rc = exact_setup(params, &cs);
+    if (rc) return rc;
+    return run_forward(cs, x, vth_pos, vth_neg, M, K, O, v_sat, -INFINITY, INFINITY, out, workspace,
+                       workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t isa_ekv_exact_backward_workspace(int64_t M, int64_t K, int64_t O, int need_grad_x, int need_grad_w) {
+    if (M < 0 || K < 0 || O < 0) return 0;
+    return plan_backward(M, K, O, 0, need_grad_x != 0, need_grad_w != 0).bytes;
+}
+
+int isa_ekv_exact_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
+                           int64_t M, int64_t K, int64_t O, const double params[4], float v_sat, float* grad_x,
+                           float* grad_vth_pos, float* grad_vth_neg, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+    int rc = check_shapes(x, vth_pos, vth_neg, M, K, O, v_sat);
+    if (rc) return rc;
+    CallSetup cs;
+    rc = exact_setup(params, &cs);
+    if (rc) return rc;
+    return run_backward(cs, x, vth_pos, vth_neg, grad_out, M, K, O, v_sat, grad_x, grad_vth_pos, grad_vth_neg,
+                        workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -33,6 +33,10 @@ EXPORTS = (
     "isa_ekv_forward",
     "isa_ekv_backward_workspace",
     "isa_ekv_backward",
+    "isa_ekv_exact_forward_workspace",
+    "isa_ekv_exact_forward",
+    "isa_ekv_exact_backward_workspace",
+    "isa_ekv_exact_backward",
     "isa_ekv_profile_begin",
     "isa_ekv_profile_end",
 )
@@ -72,6 +76,15 @@ def _declare(lib) -> None:
     lib.isa_ekv_backward_workspace.restype = sz
     lib.isa_ekv_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, vp, vp, vp, vp, sz, vp]
     lib.isa_ekv_backward.restype = ci
+    lib.isa_ekv_exact_forward_workspace.argtypes = [i64, i64, i64]
+    lib.isa_ekv_exact_forward_workspace.restype = sz
+    lib.isa_ekv_exact_forward.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.POINTER(f64), f32, vp, vp, sz, vp]
+    lib.isa_ekv_exact_forward.restype = ci
+    lib.isa_ekv_exact_backward_workspace.argtypes = [i64, i64, i64, ci, ci]
+    lib.isa_ekv_exact_backward_workspace.restype = sz
+    lib.isa_ekv_exact_backward.argtypes = [vp, vp, vp, vp, i64, i64, i64, ctypes.POINTER(f64), f32,
+                                           vp, vp, vp, vp, sz, vp]
+    lib.isa_ekv_exact_backward.restype = ci
     lib.isa_ekv_profile_begin.argtypes = []
     lib.isa_ekv_profile_begin.restype = ci
     lib.isa_ekv_profile_end.argtypes = [ctypes.POINTER(f64), ctypes.POINTER(ci)]

@@ -1,4 +1,5 @@
-"""Tensor-level calls into libisa_ekv_hip.so (forward, backward, table build and pack).
+"""Tensor-level calls into libisa_ekv_hip.so (LUT forward/backward, table build and pack,
+and the exact-formula forward/backward).
 
 Every function validates on the host what the kernels assume (device, dtype, shape,
 contiguity, 16-byte alignment) before launching, allocates outputs and workspace with
@@ -141,4 +142,52 @@ def lut_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_o
                                   _ptr(gx), _ptr(gp), _ptr(gn), ws.data_ptr(), ws.numel(),
                                   _hip.stream_handle(dev))
     _hip.check(rc, "isa_ekv_backward")
+    return gx, gp, gn
+
+
+def _exact_params(params) -> ctypes.Array:
+    """{n, U_T, I_S, V_D} as the library's double[4]."""
+    return (ctypes.c_double * 4)(*[float(v) for v in params])
+
+
+def exact_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor,
+                  params: Tuple[float, float, float, float], v_sat: float) -> torch.Tensor:
+    """Idiff[M, O] fp32 by the exact EKV formula (no clamp)."""
+    lib = _hip.load()
+    M, K, O = _check_operands(x, wpos, wneg)
+    dev = x.device
+    out = torch.empty((M, O), dtype=torch.float32, device=dev)
+    if M == 0 or O == 0:
+        return out
+    x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
+    ws = _workspace(lib.isa_ekv_exact_forward_workspace(M, K, O), dev)
+    with torch.cuda.device(dev):
+        rc = lib.isa_ekv_exact_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), M, K, O, _exact_params(params),
+                                       float(v_sat), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                       _hip.stream_handle(dev))
+    _hip.check(rc, "isa_ekv_exact_forward")
+    return out
+
+
+def exact_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_out: torch.Tensor,
+                   params: Tuple[float, float, float, float], v_sat: float, need_grad_x: bool, need_grad_w: bool):
+    """(dX | None, dVth+ | None, dVth- | None) of sum(grad_out * Idiff), exact formula, fp32."""
+    lib = _hip.load()
+    M, K, O = _check_operands(x, wpos, wneg)
+    _require_cuda(grad_out, "grad_out")
+    if tuple(grad_out.shape) != (M, O):
+        raise RuntimeError(f"grad_out must be [{M}, {O}], got {tuple(grad_out.shape)}")
+    dev = x.device
+    gx = torch.empty((M, K), dtype=torch.float32, device=dev) if need_grad_x else None
+    gp = torch.empty((O, K), dtype=torch.float32, device=dev) if need_grad_w else None
+    gn = torch.empty((O, K), dtype=torch.float32, device=dev) if need_grad_w else None
+    if not (need_grad_x or need_grad_w):
+        return gx, gp, gn
+    x32, wp32, wn32, g32 = (as_kernel_f32(t) for t in (x, wpos, wneg, grad_out))
+    ws = _workspace(lib.isa_ekv_exact_backward_workspace(M, K, O, int(need_grad_x), int(need_grad_w)), dev)
+    with torch.cuda.device(dev):
+        rc = lib.isa_ekv_exact_backward(_ptr(x32), _ptr(wp32), _ptr(wn32), _ptr(g32), M, K, O,
+                                        _exact_params(params), float(v_sat), _ptr(gx), _ptr(gp), _ptr(gn),
+                                        ws.data_ptr(), ws.numel(), _hip.stream_handle(dev))
+    _hip.check(rc, "isa_ekv_exact_backward")
     return gx, gp, gn

@@ -3,13 +3,13 @@
 `CIMLinear`, `VoltageMapping`, `PhysicalFFN`, `HybridFFN` and `clamp_signed` keep the
 reference's constructors, parameter and buffer names (`vth_pos`, `vth_neg`,
 `r_tia_log_scale`, `r_tia_base`), initialisation and clamping, so models and checkpoints
-built on the reference load unchanged. The projection runs the HIP LUT kernels through
-`triton_lut_ekv_matmul` (same dispatch test as `cim.py:180-184`).
+built on the reference load unchanged. The projection dispatches as `cim.py:180-187`:
+`ekv_approx == "lut"` runs the HIP LUT kernels through `triton_lut_ekv_matmul`, any other
+value the HIP exact-formula kernels through `triton_ekv_matmul`.
 
-This build implements only that path: a CPU input, `use_triton=False` or an
-`ekv_approx` other than "lut" raises instead of silently running another
-implementation (the reference would fall back to its exact-formula PyTorch path,
-`cim.py:201-214`, or its exact Triton tile).
+Only the device paths exist here: a CPU input or `use_triton=False` raises instead of
+silently running another implementation (the reference would fall back to its
+exact-formula PyTorch path, `cim.py:201-214`).
 """
 
 from __future__ import annotations
@@ -21,6 +21,7 @@ import torch.nn as nn
 
 from isa.device_models.config import FLASH_TRANSISTOR_EKV_CONFIG as PHYSICAL_CONFIG
 from isa.kernels.transformer_ffn.ekv_lut_triton import triton_lut_ekv_matmul
+from isa.kernels.transformer_ffn.ekv_triton import triton_ekv_matmul
 
 
 class VoltageMapping(nn.Module):
@@ -46,17 +47,17 @@ def clamp_signed(v: torch.Tensor, v_min: float = -4.0, v_max: float = 4.0) -> to
     return v.clamp(v_min, v_max)
 
 
-def _require_lut_path(cfg: Dict, x: torch.Tensor, where: str) -> None:
+def _device_projection(cfg: Dict, x: torch.Tensor, where: str):
+    """The projection cim.py:180-187 would pick on a device: LUT or exact formula."""
     if not x.is_cuda:
         raise RuntimeError(
-            f"CIMLinear.{where}: this build runs the Flash-EKV LUT projection on a ROCm device only; "
+            f"CIMLinear.{where}: this build runs the Flash-EKV projection on a ROCm device only; "
             f"got an input on {x.device}"
         )
     if not bool(cfg.get("use_triton", False)):
         raise NotImplementedError(f"CIMLinear.{where}: use_triton=False (exact PyTorch path) is not part of this build")
     approx = str(cfg.get("ekv_approx", "lut")).lower()
-    if approx != "lut":
-        raise NotImplementedError(f"CIMLinear.{where}: ekv_approx={approx!r} is not part of this build (only 'lut')")
+    return triton_lut_ekv_matmul if approx == "lut" else triton_ekv_matmul
 
 
 class CIMLinear(nn.Module):
@@ -151,8 +152,8 @@ class CIMLinear(nn.Module):
         flat = x.reshape(-1, self.in_features).contiguous()
         if flat.shape[0] > max_rows:
             flat = flat[:max_rows]
-        _require_lut_path(self.cfg, flat, "estimate_idiff")
-        return triton_lut_ekv_matmul(flat, self.vth_pos, self.vth_neg, self.cfg)
+        project = _device_projection(self.cfg, flat, "estimate_idiff")
+        return project(flat, self.vth_pos, self.vth_neg, self.cfg)
 
     def clamp_vth(self) -> None:
         v_min = self.cfg["V_TH_MIN"]
@@ -164,16 +165,16 @@ class CIMLinear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         b, n, in_f = x.shape
         assert in_f == self.in_features
-        _require_lut_path(self.cfg, x, "forward")
+        project = _device_projection(self.cfg, x, "forward")
 
         r_tia = self.r_tia.to(device=x.device, dtype=torch.float32).view(1, 1, 1)
         v_signed_min = float(self.cfg.get("V_signed_min", -4.0))
         v_signed_max = float(self.cfg.get("V_signed_max", 4.0))
 
         flat = x.reshape(b * n, in_f).contiguous()
-        idiff = triton_lut_ekv_matmul(flat, self.vth_pos, self.vth_neg, self.cfg)
-        # the kernel returns I_diff clamped to [v_signed_min, v_signed_max]; the learnable
-        # TIA gain is applied here so autograd tracks it (cim.py:190-193)
+        idiff = project(flat, self.vth_pos, self.vth_neg, self.cfg)
+        # the LUT kernel returns I_diff clamped to [v_signed_min, v_signed_max], the exact one
+        # unclamped; the learnable TIA gain is applied here so autograd tracks it (cim.py:190-193)
         out = idiff.reshape(b, n, self.out_features) * r_tia
         out = out.clamp(v_signed_min, v_signed_max)
         if self.track_output_stats:

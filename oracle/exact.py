@@ -1,13 +1,17 @@
 """Exact-formula Flash-EKV path restated from the reference (TEST INFRASTRUCTURE ONLY).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
-import this module. It serves two purposes:
+import this module. It serves three purposes:
 
 * the closed form that pins the LUT oracle (as N grows the LUT forward and backward
   converge to it), restated from ``src/isa/device_models/flash_transistor.py:22-131``;
 * the reference's PyTorch CPU path, timed as the CPU baseline: ``CIMLinear.forward``'s
   CPU branch chunked over 64 outputs (``src/isa/operators/cim.py:201-214``) with
-  ``EKVDiffCurrentFn``'s analytic backward (``flash_transistor.py:95-131``).
+  ``EKVDiffCurrentFn``'s analytic backward (``flash_transistor.py:95-131``);
+* the float64 checker of the exact-formula kernels (``diff_current_f64`` and
+  ``diff_current_grads_f64``): the same closed form and analytic gradients evaluated in
+  the inputs' dtype, without the fp32 cast of ``flash_transistor.py:107``, in the
+  products of ``kernels/transformer_ffn/ekv_triton.py:69-169``.
 """
 
 from __future__ import annotations
@@ -118,3 +122,33 @@ def exact_backward(x2d, vth_pos, vth_neg, grad, cfg, chunk: int = 64):
     out = exact_forward(x, vp, vn, cfg, chunk)
     out.backward(grad)
     return x.grad, vp.grad, vn.grad
+
+
+def diff_current_f64(x2d: torch.Tensor, vth_pos: torch.Tensor, vth_neg: torch.Tensor, cfg: Dict,
+                     chunk: int = 64) -> torch.Tensor:
+    """Idiff[M,O] = sum_k (I(x, vth_pos) - I(x, vth_neg)) in x's dtype (ekv_triton.py:69-91)."""
+    x = x2d.unsqueeze(-1)  # [M, K, 1]
+    outs = []
+    for o0 in range(0, vth_pos.shape[0], chunk):
+        vp = vth_pos[o0:o0 + chunk].t().unsqueeze(0)  # [1, K, c]
+        vn = vth_neg[o0:o0 + chunk].t().unsqueeze(0)
+        outs.append((ekv_current(x, vp, cfg) - ekv_current(x, vn, cfg)).sum(dim=1))
+    return torch.cat(outs, dim=-1)
+
+
+def diff_current_grads_f64(x2d: torch.Tensor, vth_pos: torch.Tensor, vth_neg: torch.Tensor, grad: torch.Tensor,
+                           cfg: Dict, chunk: int = 64):
+    """(dX, dVth+, dVth-) of sum(grad * Idiff) from the analytic gradients in x's dtype
+    (ekv_triton.py:94-169): dX = sum_o G (dI/dv(+) - dI/dv(-)), dVth+ = sum_m G dI/dvth(+),
+    dVth- = -sum_m G dI/dvth(-)."""
+    x = x2d.unsqueeze(-1)
+    dx = torch.zeros_like(x2d)
+    dps, dns = [], []
+    for o0 in range(0, vth_pos.shape[0], chunk):
+        vp = vth_pos[o0:o0 + chunk].t().unsqueeze(0)
+        vn = vth_neg[o0:o0 + chunk].t().unsqueeze(0)
+        g = grad[:, o0:o0 + chunk].unsqueeze(1)  # [M, 1, c]
+        dx += (g * (ekv_current_grad_v(x, vp, cfg) - ekv_current_grad_v(x, vn, cfg))).sum(dim=2)
+        dps.append((g * ekv_current_grad_vth(x, vp, cfg)).sum(dim=0).t())
+        dns.append((-(g * ekv_current_grad_vth(x, vn, cfg))).sum(dim=0).t())
+    return dx, torch.cat(dps, dim=0), torch.cat(dns, dim=0)

@@ -94,6 +94,34 @@ def test_backward_rejects_bad_arguments_before_launch():
     assert call(gx=None, gp=None, gn=None) == 0  # nothing requested
 
 
+def test_exact_entry_points_reject_bad_arguments_before_launch():
+    lib = _hip.load()
+    fake = ctypes.c_void_p(16)
+    good = (ctypes.c_double * 4)(4.136, 0.0259, 7.5875e-7, 0.1)
+
+    def fwd(params=good, M=4, vsat=8.26, ws_bytes=0):
+        return lib.isa_ekv_exact_forward(fake, fake, fake, M, 4, 4, params, vsat, fake, fake, ws_bytes, None)
+
+    assert fwd(params=None) == -1 and "params" in _err(lib)
+    assert fwd(params=(ctypes.c_double * 4)(0.0, 0.0259, 1.0, 0.1)) == -1 and "U_T" in _err(lib)
+    assert fwd(params=(ctypes.c_double * 4)(4.1, 0.0259, float("nan"), 0.1)) == -1 and "I_S" in _err(lib)
+    assert fwd(vsat=0.0) == -1 and "V_sat" in _err(lib)
+    assert fwd(M=-3) == -1 and "negative shape" in _err(lib)
+    assert fwd() == -1 and "workspace too small" in _err(lib)
+    assert fwd(M=0) == 0
+
+    def bwd(gx=fake, gp=fake, gn=fake):
+        return lib.isa_ekv_exact_backward(fake, fake, fake, fake, 8, 8, 8, good, 8.26, gx, gp, gn, fake, 0, None)
+
+    assert bwd(gn=None) == -1 and "both" in _err(lib)
+    assert bwd() == -1 and "workspace too small" in _err(lib)
+    assert bwd(gx=None, gp=None, gn=None) == 0
+    # the exact path keeps no table: its workspace adds the general-loop records instead
+    assert lib.isa_ekv_exact_forward_workspace(64, 96, 256) > lib.isa_ekv_forward_workspace(64, 96, 256)
+    assert lib.isa_ekv_exact_backward_workspace(64, 96, 256, 1, 1) > 0
+    assert lib.isa_ekv_exact_backward_workspace(-1, 96, 256, 1, 1) == 0
+
+
 def test_lut_build_and_pack_reject_bad_arguments():
     lib = _hip.load()
     params = (ctypes.c_double * 4)(4.136, 0.0259, 7.5875e-7, 0.1)

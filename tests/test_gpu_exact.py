@@ -1,0 +1,184 @@
+"""GPU parity of the exact-formula HIP kernels (ekv_approx != "lut") against the exact
+formula restated in oracle/exact.py (diff_current_f64 / diff_current_grads_f64), evaluated
+in float64 on the CPU.
+
+Gates (norm-wise max|d|/max|ref|): forward <= 1e-4, dX and dVth+- <= 1e-3, as for the LUT
+path. Both the range-checked loop (operands as 2^tx, 2^-tw) and the general loop (wide
+operands, NaN) are exercised.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exact, oracle
+from tests.helpers import errs, flash_cfg, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-4
+BWD_TOL = 1e-3
+
+
+def _params(cfg):
+    return (cfg["n"], cfg["U_T"], cfg["I_S"], cfg["V_D"]), cfg["V_sat"]
+
+
+def _oracle(x, vp, vn, g, cfg):
+    xd, pd, nd, gd = (t.double() for t in (x, vp, vn, g))
+    out = exact.diff_current_f64(xd, pd, nd, cfg).numpy()
+    dx, gp, gn = (t.numpy() for t in exact.diff_current_grads_f64(xd, pd, nd, gd, cfg))
+    return out, dx, gp, gn
+
+
+def _dev(x, vp, vn, g, cfg, dev, need_x=True, need_w=True):
+    from isa.kernels.transformer_ffn import ops
+
+    params, v_sat = _params(cfg)
+    xd, pd, nd, gd = (t.to(dev) for t in (x, vp, vn, g))
+    out = ops.exact_forward(xd, pd, nd, params, v_sat)
+    gx, gp, gn = ops.exact_backward(xd, pd, nd, gd, params, v_sat, need_x, need_w)
+    torch.cuda.synchronize()
+    return out, gx, gp, gn
+
+
+CASES = [
+    (1, 1, 1, "mapped", "init"),
+    (17, 27, 13, "mapped", "full"),
+    (31, 67, 19, "signed", "full"),
+    (70, 129, 300, "signed", "full"),   # ragged in every dimension
+    (64, 192, 768, "mapped", "init"),
+    (520, 192, 768, "mapped", "init"),  # ViT-S up-projection shape
+    (96, 130, 260, "wide", "wide"),     # operands beyond the range-checked loop's bounds
+]
+
+
+@pytest.mark.parametrize("M,K,O,x_mode,vth_mode", CASES)
+def test_exact_parity(cuda_device, M, K, O, x_mode, vth_mode):
+    print(f"[case] exact parity M={M} K={K} O={O} x={x_mode} vth={vth_mode}", flush=True)
+    cfg = flash_cfg(4096, ekv_approx="exact")
+    x, vp, vn, g = make_inputs(M, K, O, seed=3 * M + K, x_mode=x_mode, vth_mode=vth_mode)
+    ref = _oracle(x, vp, vn, g, cfg)
+    got = _dev(x, vp, vn, g, cfg, cuda_device)
+    e = {k: errs(a, r) for k, a, r in zip(("fwd", "dX", "dVth+", "dVth-"), got, ref)}
+    print({k: f"{v[0]:.2e}/{v[1]:.2e}" for k, v in e.items()})
+    assert e["fwd"][0] <= FWD_TOL
+    assert e["dX"][0] <= BWD_TOL and e["dVth+"][0] <= BWD_TOL and e["dVth-"][0] <= BWD_TOL
+
+
+def test_exact_gradient_selection_and_determinism(cuda_device):
+    cfg = flash_cfg(4096, ekv_approx="exact")
+    x, vp, vn, g = make_inputs(40, 72, 200, seed=5, x_mode="signed", vth_mode="full")
+    full = _dev(x, vp, vn, g, cfg, cuda_device)
+    only_x = _dev(x, vp, vn, g, cfg, cuda_device, need_x=True, need_w=False)
+    only_w = _dev(x, vp, vn, g, cfg, cuda_device, need_x=False, need_w=True)
+    again = _dev(x, vp, vn, g, cfg, cuda_device)
+    assert only_x[2] is None and only_x[3] is None and only_w[1] is None
+    assert torch.equal(full[1], only_x[1])
+    assert torch.equal(full[2], only_w[2]) and torch.equal(full[3], only_w[3])
+    for a, b in zip(full, again):
+        assert torch.equal(a, b)
+
+
+def test_exact_invariants(cuda_device):
+    """Equal thresholds give exactly zero current and dX, and dVth+ == -dVth-; swapping
+    the thresholds negates the output."""
+    cfg = flash_cfg(4096, ekv_approx="exact")
+    x, vp, vn, g = make_inputs(33, 50, 70, seed=9, x_mode="mapped", vth_mode="full")
+    out, gx, gp, gn = _dev(x, vp, vp, g, cfg, cuda_device)
+    assert float(out.abs().max()) == 0.0 and float(gx.abs().max()) == 0.0
+    assert torch.equal(gp, -gn)
+    a = _dev(x, vp, vn, g, cfg, cuda_device)[0]
+    b = _dev(x, vn, vp, g, cfg, cuda_device)[0]
+    assert torch.equal(a, -b)
+
+
+def test_exact_nan_propagates(cuda_device):
+    """A NaN input gives NaN outputs in its row only (the reference's softplus propagates NaN)."""
+    cfg = flash_cfg(4096, ekv_approx="exact")
+    x, vp, vn, g = make_inputs(12, 20, 40, seed=4)
+    x[3, 7] = float("nan")
+    out = _dev(x, vp, vn, g, cfg, cuda_device)[0].cpu()
+    assert torch.isnan(out[3]).all()
+    rest = torch.cat([out[:3], out[4:]])
+    assert torch.isfinite(rest).all()
+    ref = exact.diff_current_f64(torch.cat([x[:3], x[4:]]).double(), vp.double(), vn.double(), cfg).numpy()
+    assert oracle.normwise_error(rest.double().numpy(), ref) <= FWD_TOL
+
+
+def test_reused_ffn_tile_formula(cuda_device):
+    """tests/test_exact_direct_conv.py:125-153 of the reference: TritonEKVMatmulFn with
+    scaled device parameters, loss = mean(out^2), compared here with the float64 exact
+    formula at the reference's tolerances (rtol 5e-5, atol 2e-4)."""
+    from isa.kernels.transformer_ffn.ekv_triton import TritonEKVMatmulFn
+
+    params = {"I_S": 0.75875, "n": 4.1360, "U_T": 0.026, "V_D": 0.1, "V_sat": 8.2624}
+    torch.manual_seed(20260808)
+    x_base = torch.rand(17, 27) * 4.0
+    wp_base = torch.rand(13, 27) * 5.0
+    wn_base = torch.rand(13, 27) * 5.0
+
+    def run(fn, device, dtype):
+        x = x_base.to(device, dtype).requires_grad_(True)
+        wp = wp_base.to(device, dtype).requires_grad_(True)
+        wn = wn_base.to(device, dtype).requires_grad_(True)
+        out = fn(x, wp, wn)
+        out.square().mean().backward()
+        return out.detach().double().cpu(), [t.grad.double().cpu() for t in (x, wp, wn)]
+
+    out, grads = run(lambda x, wp, wn: TritonEKVMatmulFn.apply(x, wp, wn, params), cuda_device, torch.float32)
+    ref_out, ref_grads = run(lambda x, wp, wn: exact.diff_current_f64(x, wp, wn, params), "cpu", torch.float64)
+    assert torch.allclose(out, ref_out, rtol=5.0e-5, atol=2.0e-4)
+    for a, b in zip(grads, ref_grads):
+        assert torch.allclose(a, b, rtol=5.0e-5, atol=2.0e-4)
+
+
+def test_triton_ekv_matmul_dtype_and_grad_rules(cuda_device):
+    """ekv_triton.py:175-211: output in x's dtype; dX only when x requires grad; dWpos and
+    dWneg in their own dtypes."""
+    from isa.kernels.transformer_ffn.ekv_triton import triton_ekv_matmul
+
+    cfg = flash_cfg(4096, ekv_approx="exact")
+    x, vp, vn, _ = make_inputs(9, 16, 24, seed=2)
+    xb = x.to(cuda_device, torch.bfloat16)
+    wp = vp.to(cuda_device).requires_grad_(True)
+    wn = vn.to(cuda_device).requires_grad_(True)
+    out = triton_ekv_matmul(xb, wp, wn, cfg)
+    assert out.dtype == torch.bfloat16 and out.shape == (9, 24)
+    out.float().sum().backward()
+    assert wp.grad is not None and wp.grad.dtype == torch.float32 and wn.grad is not None
+    ref = exact.diff_current_f64(xb.float().cpu().double(), vp.double(), vn.double(), cfg).numpy()
+    assert oracle.normwise_error(out.detach().float().cpu().double().numpy(), ref) <= 1e-2  # bf16 output rounding
+
+
+def test_cimlinear_exact_dispatch(cuda_device):
+    """CIMLinear with ekv_approx != 'lut' runs the exact kernels (cim.py:180-199): output
+    clamp(Idiff * R_TIA, -4, 4) and its gradients."""
+    from isa.operators.cim import CIMLinear
+
+    cfg = flash_cfg(4096, ekv_approx="exact")
+    torch.manual_seed(6)
+    layer = CIMLinear(48, 96, cfg).to(cuda_device)
+    with torch.no_grad():
+        layer.r_tia_log_scale.fill_(0.7)  # drive some outputs into the clamp
+    x = torch.rand(2, 13, 48, device=cuda_device).mul(4.0).requires_grad_(True)
+    out = layer(x)
+    g = torch.randn_like(out)
+    out.backward(g)
+    X = x.detach().double().cpu().reshape(-1, 48)
+    wp, wn = layer.vth_pos.detach().double().cpu(), layer.vth_neg.detach().double().cpu()
+    idiff = exact.diff_current_f64(X, wp, wn, cfg).numpy()
+    r = float(layer.r_tia)
+    pre = idiff * r
+    ref = np.clip(pre, -4.0, 4.0)
+    assert oracle.normwise_error(out.detach().double().cpu().numpy().reshape(-1, 96), ref) <= FWD_TOL
+    gi = (g.detach().double().cpu().numpy().reshape(-1, 96) * r * (np.abs(pre) < 4.0))
+    dx, dp, dn = exact.diff_current_grads_f64(X, wp, wn, torch.from_numpy(gi), cfg)
+    for name, got, want in (("dx", x.grad, dx), ("dvth+", layer.vth_pos.grad, dp), ("dvth-", layer.vth_neg.grad, dn)):
+        e = oracle.normwise_error(got.detach().double().cpu().numpy().reshape(want.shape), want.numpy())
+        print(name, f"{e:.2e}")
+        assert e <= BWD_TOL, name
+    est = layer.estimate_idiff(x.detach(), max_rows=10)
+    assert oracle.normwise_error(est.double().cpu().numpy(), idiff[:10]) <= FWD_TOL

@@ -101,6 +101,44 @@ def test_exact_analytic_gradients_match_autograd():
     assert torch.allclose(exact.ekv_current_grad_vth(vgs, vth, REF_TEST_CFG), gt, rtol=1e-10, atol=1e-10)
 
 
+def test_exact_products_brute_force_tiny():
+    """diff_current_f64 (the exact-path checker) against a pure-Python triple loop with
+    math.log1p/exp, including the softplus threshold (u > 20) and the sign of each term."""
+    c = REF_TEST_CFG
+    k = 1.0 / (2.0 * c["n"] * c["U_T"])
+
+    def sp(u):
+        return u if u > 20.0 else math.log1p(math.exp(u))
+
+    def cur(v, t):
+        return c["I_S"] * (sp((v - t) * k) ** 2 - sp((v - t - c["V_D"]) * k) ** 2) / (1.0 + v / c["V_sat"])
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand(3, 5, generator=g, dtype=torch.float64) * 12.0 - 4.0  # reaches u > 20
+    vp = torch.rand(4, 5, generator=g, dtype=torch.float64) * 5.0
+    vn = torch.rand(4, 5, generator=g, dtype=torch.float64) * 5.0
+    want = [[sum(cur(x[m, i].item(), vp[o, i].item()) - cur(x[m, i].item(), vn[o, i].item()) for i in range(5))
+             for o in range(4)] for m in range(3)]
+    got = exact.diff_current_f64(x, vp, vn, c, chunk=3)
+    assert torch.allclose(got, torch.tensor(want, dtype=torch.float64), rtol=1e-12, atol=1e-12)
+
+
+def test_exact_product_gradients_match_autograd():
+    """diff_current_grads_f64 == torch autograd of sum(G * Idiff) of the closed form."""
+    c = REF_TEST_CFG
+    g = torch.Generator().manual_seed(12)
+    x = (torch.rand(6, 7, generator=g, dtype=torch.float64) * 8.0 - 4.0).requires_grad_(True)
+    vp = (torch.rand(9, 7, generator=g, dtype=torch.float64) * 5.0).requires_grad_(True)
+    vn = (torch.rand(9, 7, generator=g, dtype=torch.float64) * 5.0).requires_grad_(True)
+    G = torch.randn(6, 9, generator=g, dtype=torch.float64)
+    cur = lambda v, t: exact.ekv_current(v, t, c)  # noqa: E731
+    idiff = (cur(x.unsqueeze(1), vp.unsqueeze(0)) - cur(x.unsqueeze(1), vn.unsqueeze(0))).sum(-1)
+    ax, ap, an = torch.autograd.grad((G * idiff).sum(), (x, vp, vn))
+    dx, dp, dn = exact.diff_current_grads_f64(x.detach(), vp.detach(), vn.detach(), G, c, chunk=4)
+    for a, b in ((dx, ax), (dp, ap), (dn, an)):
+        assert torch.allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
 def test_lookup_boundaries():
     cfg = flash_cfg(4096)
     dmin, dmax, n = oracle.lut_range(cfg)
