@@ -32,8 +32,11 @@ for p in (str(ROOT / "isa-_amd"), str(ROOT)):
 
 # gfx950 VALU issue peak: 256 CUs x 64 lanes x 2.4 GHz (lane-instructions per second)
 VALU_PEAK = 256 * 64 * 2.4e9
-FWD_INSTR_PER_CELL = 12  # algorithmic lane-instructions per cell-eval, forward
-BWD_INSTR_PER_CELL = 16  # backward
+# lane-instructions per cell-eval (forward, backward). LUT path: the algorithmic count of
+# the interpolated lookup formulation. Exact path: the issued count of the exact kernels'
+# range-checked inner loops (4 log2 per cell forward; 4 log2 + 4 rcp backward, each with
+# the rounding correction of log2(1 + e)), so its fraction measures issue efficiency.
+INSTR_PER_CELL = {"lut": (12, 16), "exact": (32, 52)}
 
 CONFIGS = {
     # name: (batch, tokens, d_model, d_ffn, physical fc2)
@@ -222,6 +225,8 @@ def main() -> int:
     ap.add_argument("--lut-size", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ekv-approx", default="lut", choices=["lut", "exact"],
+                    help="CIMLinear projection: the LUT kernels (headline) or the exact-formula kernels")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -248,6 +253,8 @@ def main() -> int:
     M = B * T
     cfg = make_flash_transistor_ekv_config(default_lut_size=args.lut_size)
     cfg["LUT_DELTA_SIZE"] = args.lut_size
+    cfg["ekv_approx"] = args.ekv_approx
+    fwd_instr, bwd_instr = INSTR_PER_CELL[args.ekv_approx]
 
     torch.manual_seed(0)
     if physical is True:
@@ -306,24 +313,26 @@ def main() -> int:
     cells_launch = cells_fwd / len(layers)  # per-launch cells (equal for fc1 and fc2)
     fwd_cells_s = cells_fwd * args.steps / (kt.fwd_ms * 1e-3) if kt.fwd_ms else 0.0
     bwd_cells_s = cells_fwd * args.steps / (kt.bwd_ms * 1e-3) if kt.bwd_ms else 0.0
-    achieved = bwd_cells_s * BWD_INSTR_PER_CELL / 1e12
+    achieved = bwd_cells_s * bwd_instr / 1e12
     peak = VALU_PEAK / 1e12
+    exact = args.ekv_approx == "exact"
     roofline = {
         "bound": "valu",
         "achieved": round(achieved, 3),
         "peak": round(peak, 3),
         "unit": "TOP/s",
         "frac": round(achieved / peak, 4),
-        "traffic": measured_traffic(args.config),
-        "kernel": "bwd_kernel<true,true> (backward main kernel, dominant)",
-        "work": f"{BWD_INSTR_PER_CELL} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
+        "traffic": None if exact else measured_traffic(args.config),
+        "kernel": ("bwd_exact_kernel<true,true>" if exact else "bwd_kernel<true,true,true>")
+                  + " (backward main kernel, dominant)",
+        "work": f"{bwd_instr} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
         "avg_launch_ms": round(bwd_avg, 4),
         "forward_kernel": {
-            "kernel": "fwd_kernel", "avg_launch_ms": round(fwd_avg, 4),
-            "achieved": round(fwd_cells_s * FWD_INSTR_PER_CELL / 1e12, 3),
-            "frac": round(fwd_cells_s * FWD_INSTR_PER_CELL / VALU_PEAK, 4),
+            "kernel": "fwd_exact_kernel" if exact else "fwd_kernel", "avg_launch_ms": round(fwd_avg, 4),
+            "achieved": round(fwd_cells_s * fwd_instr / 1e12, 3),
+            "frac": round(fwd_cells_s * fwd_instr / VALU_PEAK, 4),
         },
-        "step_frac_of_cell_roofline": round(value / (2.0 / (FWD_INSTR_PER_CELL / VALU_PEAK + BWD_INSTR_PER_CELL / VALU_PEAK)), 4),
+        "step_frac_of_cell_roofline": round(value / (2.0 / (fwd_instr / VALU_PEAK + bwd_instr / VALU_PEAK)), 4),
     }
     log(f"[bench] fwd kernel {fwd_avg:.3f} ms/launch ({roofline['forward_kernel']['frac']:.3f} of VALU peak), "
         f"bwd kernel {bwd_avg:.3f} ms/launch ({roofline['frac']:.3f})")
@@ -353,7 +362,7 @@ def main() -> int:
                 "vitm_ffn": "Physical ViT-M FFN: CIMLinear 256->1024->256, X[128,65,256] fp32, fwd+bwd",
                 "gptm_hybrid": "Hybrid GPT-M FFN: CIMLinear 384->1536 + Linear 1536->384, X[16,1024,384], fwd+bwd",
                 "vits_up": "ViT-S up-projection: CIMLinear 192->768, X[8,65,192] fp32, fwd+bwd",
-            }[args.config],
+            }[args.config] + (" (exact-formula kernels, ekv_approx='exact')" if exact else ""),
             "tokens": M,
             "lut_entries": args.lut_size,
             "cell_evals_per_step": cells_step,
