@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 3
+#define ISA_EKV_ABI_VERSION 4
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -133,6 +133,56 @@ int isa_ekv_exact_backward(const float* x, const float* vth_pos, const float* vt
                            int64_t M, int64_t K, int64_t O, const double params[4], float v_sat, float* grad_x,
                            float* grad_vth_pos, float* grad_vth_neg, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/* Fused layer glue (no reference counterpart: it fuses the PyTorch elementwise ops around
+ * the projection, cim.py:37-39, :190-193 and :243, into the LUT kernels' prologue/epilogue
+ * and the backward's prep and reductions; every op keeps its own rounding).
+ * Forward:  v = clamp(x * in_affine[0] + in_affine[1], in_lo, in_hi)      (if in_affine)
+ *           idiff = isa_ekv_forward(v, ...)                               (clamped to idiff_min/max)
+ *           y = clamp(idiff * r_tia[0], y_lo, y_hi)                       (if r_tia)
+ *           out = y * adc_scale[o] + adc_shift[o]                         (if adc_scale)
+ * All glue pointers are device memory and may be null (that step is skipped). */
+typedef struct isa_ekv_glue {
+    const float* in_affine; /* [2] {scale, shift} */
+    float in_lo, in_hi;
+    const float* r_tia;     /* [1] */
+    float y_lo, y_hi;
+    const float* adc_scale; /* [O] */
+    const float* adc_shift; /* [O], required with adc_scale */
+} isa_ekv_glue;
+
+/* Gradients of the glue parameters written by isa_ekv_layer_backward (device memory; each
+ * may be null when its parameter is absent or needs no gradient). */
+typedef struct isa_ekv_glue_grads {
+    float* in_affine; /* [2] d{scale, shift} */
+    float* r_tia;     /* [1] */
+    float* adc_scale; /* [O] */
+    float* adc_shift; /* [O] */
+} isa_ekv_glue_grads;
+
+/* Workspace bytes for isa_ekv_layer_forward / isa_ekv_layer_backward. */
+size_t isa_ekv_layer_forward_workspace(int64_t M, int64_t K, int64_t O);
+size_t isa_ekv_layer_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x,
+                                        int need_grad_w);
+
+/* isa_ekv_forward with the glue: writes out [M][O] and, when idiff is not null, the
+ * pre-glue idiff [M][O] that isa_ekv_layer_backward needs. Replaces, on the LUT path, the
+ * projection call and the elementwise ops of CIMLinear.forward (cim.py:180-199) and of
+ * VoltageMapping / PhysicalFFN's ADC affine (cim.py:37-39, :243). */
+int isa_ekv_layer_forward(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd, int64_t M,
+                          int64_t K, int64_t O, int n_entries, float delta_min, float delta_max, float v_sat,
+                          float idiff_min, float idiff_max, const isa_ekv_glue* glue, float* idiff, float* out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward of isa_ekv_layer_forward for the gradient grad_out of out: grad_x is the
+ * gradient for x (before the input mapping), grad_vth_pos/neg as isa_ekv_backward, and the
+ * glue parameters' gradients in *glue_grads. idiff is the forward's saved idiff. Results
+ * are deterministic (fixed-order reductions, no atomics). */
+int isa_ekv_layer_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
+                           const float* idiff, const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries,
+                           float delta_min, float delta_max, float v_sat, const isa_ekv_glue* glue, float* grad_x,
+                           float* grad_vth_pos, float* grad_vth_neg, const isa_ekv_glue_grads* glue_grads,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* Profiling aid, no reference counterpart: between begin and end, every forward and
  * backward call records HIP events on its stream (up to 4096 intervals). end synchronises

@@ -61,6 +61,8 @@ __device__ inline float2 load_uniform2(const float2* p) {
     return make_float2(q[0], q[1]);
 }
 
+__device__ inline float load_uniform1(const float* p) { return *(const_f32*)(p); }
+
 __device__ inline float4 load_uniform4(const float4* p) {
     const_f32* q = (const_f32*)(p);
     return make_float4(q[0], q[1], q[2], q[3]);
@@ -294,7 +296,23 @@ struct PrepArgs {
     float* xrec_slow;         // exact mode: [M][Kp][rec_floats] with tx
     float2* wsT_slow;         // exact mode: [Kp][Op] with tw
     float2* partials;         // [kPrepBlocksX + kPrepBlocksW]
+    const float* in_affine;   // optional device {scale, shift}: the layer input is clamp(x*scale + shift)
+    float in_lo, in_hi;
 };
+
+// Input voltage mapping clamp(x * scale + shift, lo, hi) (cim.py:37-39): product and sum
+// rounded separately as the two tensor ops do (no fma contraction); NaN stays NaN as
+// torch.clamp keeps it.
+__device__ inline float mapped_pre(float x, float scale, float shift) {
+#pragma clang fp contract(off)
+    const float prod = x * scale;
+    return prod + shift;
+}
+
+__device__ inline float input_map(float x, float scale, float shift, float lo, float hi) {
+    const float pre = mapped_pre(x, scale, shift);
+    return pre != pre ? pre : fminf(fmaxf(pre, lo), hi);
+}
 
 __device__ inline void block_minmax(float lo, float hi, float2* out) {
     __shared__ float s_lo[32], s_hi[32];
@@ -329,12 +347,15 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     float lo = INFINITY, hi = -INFINITY;
     if (blockIdx.x < kPrepBlocksX) {
         // rows m are strided over the token-side blocks; threads walk k (coalesced)
+        const float aff_s = a.in_affine ? a.in_affine[0] : 1.0f;
+        const float aff_b = a.in_affine ? a.in_affine[1] : 0.0f;
         for (int64_t m = blockIdx.x; m < a.M; m += kPrepBlocksX) {
             const float* xrow = a.x + m * a.K;
             for (int k = threadIdx.x; k < (int)a.Kp; k += blockDim.x) {
                 float c, r, f = 1.0f;
                 if (k < a.K) {
-                    const float xv = xrow[k];
+                    float xv = xrow[k];
+                    if (a.in_affine) xv = input_map(xv, aff_s, aff_b, a.in_lo, a.in_hi);
                     c = fmaf(xv - a.xoff, a.scale, a.xadd);
                     r = 1.0f / (1.0f + xv / a.v_sat);
                     if (a.exact) f = (float)exp2((double)xv * a.scale_d);
@@ -625,7 +646,30 @@ struct FwdArgs {
     float cmin, cmax, out_min, out_max;
     float out_scale;        // exact: I_S ln2^2
     float k2, c2;           // exact: 2^(-V_D a), V_D a
+    // optional epilogue (layer glue): idiff is stored when given; out = glue(idiff)
+    float* idiff;           // [M][O]
+    const float* r_tia;     // device scalar: y = clamp(idiff * r_tia, y_lo, y_hi)
+    float y_lo, y_hi;
+    const float* adc_scale; // device [O]: out = y * adc_scale[o] + adc_shift[o]
+    const float* adc_shift;
+    int glue;
 };
+
+// TIA gain, output clamp and ADC affine of cim.py:190-193 and :243, applied to one output
+// value: each tensor op's rounding kept (no contraction), NaN kept as torch.clamp does.
+__device__ inline float layer_glue(float v, float r, bool has_r, float lo, float hi, const float* a_scale,
+                                   const float* a_shift, int o) {
+#pragma clang fp contract(off)
+    if (has_r) {
+        v = v * r;
+        v = v != v ? v : fminf(fmaxf(v, lo), hi);
+    }
+    if (a_scale) {
+        const float prod = v * a_scale[o];
+        v = prod + a_shift[o];
+    }
+    return v;
+}
 
 template <int MR, int ORR, bool CLAMP_OUT, class Cell>
 __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2* xrec, const float2* wsT,
@@ -668,6 +712,26 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
                 }
             }
         }
+    }
+    if (a.glue) {
+        const bool has_r = a.r_tia != nullptr;
+        const float r = has_r ? load_uniform1(a.r_tia) : 1.0f;
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+            const int m = m0 + i;
+            if (m >= a.M) break;
+            float* orow = a.out + (size_t)m * a.O;
+            float* irow = a.idiff ? a.idiff + (size_t)m * a.O : nullptr;
+#pragma unroll
+            for (int j = 0; j < ORR; ++j) {
+                const int o = o_lane + j;
+                if (o >= a.O) continue;
+                const float id = CLAMP_OUT ? fminf(fmaxf(acc[i][j], a.out_min), a.out_max) : acc[i][j] * a.out_scale;
+                if (irow) irow[o] = id;
+                orow[o] = layer_glue(id, r, has_r, a.y_lo, a.y_hi, a.adc_scale, a.adc_shift, o);
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int i = 0; i < MR; ++i) {
@@ -968,14 +1032,50 @@ __global__ __launch_bounds__(1024) void bwd_exact_kernel(BwdArgs a) {
 }
 
 // dX[m,k] = scale * sum over output blocks, in block order (deterministic); scale is 1 for
-// the LUT path and the derivative constant of the exact cells
+// the LUT path and the derivative constant of the exact cells. With an input mapping
+// v = clamp(x * s + b) in front of the layer (in_affine), dX is the gradient for v and this
+// kernel applies the mapping's backward (cim.py:37-39 under autograd: mask where
+// lo <= x*s + b <= hi, dx = mask * dv * s) and writes per-block partial sums of
+// mask*dv*x (ds) and mask*dv (db) to aff_part[block] for glue_reduce_kernel.
+constexpr int kDxReduceBlocks = 1024;
+
 __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict__ part, int n_ob,
-                                                        int64_t n, float scale, float* __restrict__ dx) {
+                                                        int64_t n, float scale, float* __restrict__ dx,
+                                                        const float* __restrict__ x, const float* in_affine,
+                                                        float in_lo, float in_hi, float2* __restrict__ aff_part) {
+    const float aff_s = in_affine ? in_affine[0] : 1.0f;
+    const float aff_b = in_affine ? in_affine[1] : 0.0f;
+    float ds = 0.0f, db = 0.0f;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
          e += (int64_t)gridDim.x * blockDim.x) {
         float s = part[e];
         for (int b = 1; b < n_ob; ++b) s += part[(size_t)b * n + e];
-        dx[e] = s * scale;
+        s *= scale;
+        if (in_affine) {
+            const float xv = x[e];
+            const float pre = mapped_pre(xv, aff_s, aff_b);
+            const float g = (pre >= in_lo && pre <= in_hi) ? s : 0.0f;
+            ds = fmaf(g, xv, ds);
+            db += g;
+            s = g * aff_s;
+        }
+        dx[e] = s;
+    }
+    if (in_affine) {
+        __shared__ float s_ds[4], s_db[4];
+        for (int off = 32; off > 0; off >>= 1) {
+            ds += __shfl_xor(ds, off);
+            db += __shfl_xor(db, off);
+        }
+        const int wave = threadIdx.x >> 6;
+        if ((threadIdx.x & 63) == 0) {
+            s_ds[wave] = ds;
+            s_db[wave] = db;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0)
+            aff_part[blockIdx.x] = make_float2((s_ds[0] + s_ds[1]) + (s_ds[2] + s_ds[3]),
+                                               (s_db[0] + s_db[1]) + (s_db[2] + s_db[3]));
     }
 }
 
@@ -1012,6 +1112,107 @@ __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict_
             }
         }
         __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------------------------
+// Layer glue backward (the reverse of layer_glue, cim.py:190-193 and :243 under autograd).
+// For every (m, o) with G the gradient of the layer output:
+//   gy = G * adc_scale[o]                        (G without an ADC affine)
+//   y0 = idiff * r_tia, mask = lo <= y0 <= hi    (torch.clamp's backward mask)
+//   G_eff[m, o] = mask * gy * r_tia               (the CIM backward's upstream gradient)
+//   d r_tia   += mask * gy * idiff,   d adc_scale[o] += G * clamp(y0),   d adc_shift[o] += G
+// Blocks own fixed row sets; per-block partials are combined in block order by
+// glue_reduce_kernel, so every result is reproducible. G_eff is written [M][Op] with zeros
+// in the padded outputs.
+// ----------------------------------------------------------------------------------
+
+constexpr int kGlueBlocks = 256;
+
+struct GlueGradArgs {
+    const float* g;          // [M][O]
+    const float* idiff;      // [M][O]
+    int64_t M, O, Op;
+    const float* r_tia;
+    float y_lo, y_hi;
+    const float* adc_scale;  // [O] or null
+    float* geff;             // [M][Op]
+    float* col_part;         // [kGlueBlocks][2][Op] (d adc_scale, d adc_shift)
+    float* r_part;           // [kGlueBlocks]
+};
+
+__global__ __launch_bounds__(256) void glue_grad_kernel(GlueGradArgs a) {
+    const bool has_r = a.r_tia != nullptr;
+    const float r = has_r ? *a.r_tia : 1.0f;
+    float racc = 0.0f;
+    for (int64_t o = threadIdx.x; o < a.Op; o += blockDim.x) {
+        float da = 0.0f, dc = 0.0f;
+        const float as = (a.adc_scale && o < a.O) ? a.adc_scale[o] : 1.0f;
+        for (int64_t m = blockIdx.x; m < a.M; m += gridDim.x) {
+            float ge = 0.0f;
+            if (o < a.O) {
+                const float gz = a.g[m * a.O + o];
+                const float id = a.idiff[m * a.O + o];
+                const float y0 = id * r;
+                const bool pass = !has_r || (y0 >= a.y_lo && y0 <= a.y_hi);
+                if (a.adc_scale) {
+                    const float y = !has_r ? id : (y0 != y0 ? y0 : fminf(fmaxf(y0, a.y_lo), a.y_hi));
+                    da = fmaf(gz, y, da);
+                    dc += gz;
+                }
+                const float gy = a.adc_scale ? gz * as : gz;
+                const float gm = pass ? gy : 0.0f;
+                racc = fmaf(gm, id, racc);
+                ge = gm * r;
+            }
+            a.geff[m * a.Op + o] = ge;
+        }
+        if (a.adc_scale) {
+            a.col_part[(size_t)blockIdx.x * 2 * a.Op + o] = da;
+            a.col_part[(size_t)blockIdx.x * 2 * a.Op + a.Op + o] = dc;
+        }
+    }
+    if (has_r) {
+        __shared__ float s_r[4];
+        for (int off = 32; off > 0; off >>= 1) racc += __shfl_xor(racc, off);
+        if ((threadIdx.x & 63) == 0) s_r[threadIdx.x >> 6] = racc;
+        __syncthreads();
+        if (threadIdx.x == 0) a.r_part[blockIdx.x] = (s_r[0] + s_r[1]) + (s_r[2] + s_r[3]);
+    }
+}
+
+// Final sums of the glue partials in fixed order: d adc_scale/shift[o] over glue blocks,
+// d r_tia over glue blocks, d {scale, shift} of the input mapping over dx_reduce blocks.
+__global__ __launch_bounds__(256) void glue_reduce_kernel(const float* __restrict__ col_part,
+                                                          const float* __restrict__ r_part,
+                                                          const float2* __restrict__ aff_part, int64_t O,
+                                                          int64_t Op, float* d_adc_scale, float* d_adc_shift,
+                                                          float* d_r_tia, float* d_affine) {
+    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < O; o += (int64_t)gridDim.x * blockDim.x) {
+        if (!d_adc_scale && !d_adc_shift) break;
+        float sa = 0.0f, sc = 0.0f;
+        for (int b = 0; b < kGlueBlocks; ++b) {
+            sa += col_part[(size_t)b * 2 * Op + o];
+            sc += col_part[(size_t)b * 2 * Op + Op + o];
+        }
+        if (d_adc_scale) d_adc_scale[o] = sa;
+        if (d_adc_shift) d_adc_shift[o] = sc;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (d_r_tia) {
+            float sr = 0.0f;
+            for (int b = 0; b < kGlueBlocks; ++b) sr += r_part[b];
+            d_r_tia[0] = sr;
+        }
+        if (d_affine) {
+            float ss = 0.0f, sb = 0.0f;
+            for (int b = 0; b < kDxReduceBlocks; ++b) {
+                ss += aff_part[b].x;
+                sb += aff_part[b].y;
+            }
+            d_affine[0] = ss;
+            d_affine[1] = sb;
+        }
     }
 }
 
@@ -1058,11 +1259,14 @@ struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
     bool grad_padded, split;
-    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_gpad, off_dx, off_dv, bytes, lds_bytes;
+    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_gpad, off_dx, off_dv, off_glue, bytes,
+        lds_bytes;
 };
 
 // n_entries = 0 plans the exact-formula backward (no LDS table, general-loop records).
-BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_x, bool need_w) {
+// glue: the layer backward (G_eff always written [M][Op], plus the glue partial sums).
+BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_x, bool need_w,
+                      bool glue = false) {
     BwdPlan p{};
     const bool exact = n_entries == 0;
     p.Kp = round_up(K > 0 ? K : 1, 8);
@@ -1089,7 +1293,7 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     if (p.n_split < 1) p.n_split = 1;
     p.n_items = (int)(base_items * p.n_split);
     p.blocks = (p.n_items + wpb - 1) / wpb;
-    p.grad_padded = (O % (64 * kBwdORR)) != 0;
+    p.grad_padded = glue || (O % (64 * kBwdORR)) != 0;
     const size_t xrec_bytes = (size_t)round_up((int64_t)M * p.Kp * 16, 256);
     const size_t wsT_bytes = (size_t)round_up(p.Kp * p.Op * 8, 256);
     size_t off = 0;
@@ -1109,6 +1313,10 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     if (need_x) off += (size_t)round_up((int64_t)p.n_ob * M * (K > 0 ? K : 1) * 4, 256);
     p.off_dv = off;
     if (need_w) off += (size_t)round_up((int64_t)p.n_split * 2 * p.Kp * p.Op * 4, 256);
+    p.off_glue = off;  // col_part [kGlueBlocks][2][Op], r_part [kGlueBlocks], aff_part [kDxReduceBlocks]
+    if (glue)
+        off += (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) + round_up(kGlueBlocks * 4, 256) +
+               (size_t)round_up(kDxReduceBlocks * 8, 256);
     p.bytes = round_up((int64_t)off, 256);
     return p;
 }
@@ -1240,8 +1448,14 @@ int exact_setup(const double* params, CallSetup* cs) {
 
 PrepArgs make_prep(const CallSetup& cs, const float* x, const float* wp, const float* wn, int64_t M, int64_t K,
                    int64_t O, int64_t Kp, int64_t Op, float v_sat, int rec_floats, char* ws, size_t off_xrec,
-                   size_t off_wsT, size_t off_xrec_alt, size_t off_wsT_alt, size_t off_part) {
+                   size_t off_wsT, size_t off_xrec_alt, size_t off_wsT_alt, size_t off_part,
+                   const isa_ekv_glue* glue) {
     PrepArgs pa{};
+    if (glue && glue->in_affine) {
+        pa.in_affine = glue->in_affine;
+        pa.in_lo = glue->in_lo;
+        pa.in_hi = glue->in_hi;
+    }
     pa.x = x;
     pa.wp = wp;
     pa.wn = wn;
@@ -1281,7 +1495,8 @@ PrepArgs make_prep(const CallSetup& cs, const float* x, const float* wp, const f
 
 int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg, int64_t M,
                 int64_t K, int64_t O, float v_sat, float out_min, float out_max, float* out, void* workspace,
-                size_t workspace_bytes, hipStream_t s) {
+                size_t workspace_bytes, hipStream_t s, const isa_ekv_glue* glue = nullptr,
+                float* idiff = nullptr) {
     if (M == 0 || O == 0) return 0;
     if (!out) return fail(ISA_EKV_EINVAL, "out is null");
     const FwdPlan p = plan_forward(M, K, O, cs.exact);
@@ -1290,7 +1505,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
     char* ws = static_cast<char*>(workspace);
     CallTimer call_timer(s, 2);
     const PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 2, ws, p.off_xrec, p.off_wsT,
-                                  p.off_xrec_alt, p.off_wsT_alt, p.off_part);
+                                  p.off_xrec_alt, p.off_wsT_alt, p.off_part, glue);
     hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "forward prep launch");
@@ -1309,6 +1524,15 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
     fa.n_ot = p.n_ot;
     fa.out_min = out_min;
     fa.out_max = out_max;
+    if (glue) {
+        fa.glue = 1;
+        fa.idiff = idiff;
+        fa.r_tia = glue->r_tia;
+        fa.y_lo = glue->y_lo;
+        fa.y_hi = glue->y_hi;
+        fa.adc_scale = glue->adc_scale;
+        fa.adc_shift = glue->adc_shift;
+    }
     size_t lds = 0;
     if (cs.exact) {
         fa.out_scale = (float)cs.cur_scale;
@@ -1331,40 +1555,77 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
     return 0;
 }
 
+void zero_fill(float* p, int64_t n, hipStream_t s) {
+    if (p && n > 0) hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, s, p, n);
+}
+
+// glue / glue_grads: the layer backward (null for the plain projection backward).
 int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg,
                  const float* grad_out, int64_t M, int64_t K, int64_t O, float v_sat, float* grad_x,
-                 float* grad_vth_pos, float* grad_vth_neg, void* workspace, size_t workspace_bytes, hipStream_t s) {
+                 float* grad_vth_pos, float* grad_vth_neg, void* workspace, size_t workspace_bytes, hipStream_t s,
+                 const isa_ekv_glue* glue = nullptr, const float* idiff = nullptr,
+                 const isa_ekv_glue_grads* gg = nullptr) {
     const bool need_x = grad_x != nullptr;
     const bool need_w = grad_vth_pos != nullptr || grad_vth_neg != nullptr;
     if (need_w && (grad_vth_pos == nullptr || grad_vth_neg == nullptr))
         return fail(ISA_EKV_EINVAL, "grad_vth_pos and grad_vth_neg must both be given or both be null");
-    if (!need_x && !need_w) return 0;
+    const bool need_glue = gg && (gg->in_affine || gg->r_tia || gg->adc_scale || gg->adc_shift);
+    if (!need_x && !need_w && !need_glue) return 0;
     hipError_t err;
-    // degenerate shapes: empty reductions give zero gradients
-    if (M == 0 || O == 0 || K == 0) {
-        if (need_x && M * K > 0) hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, s, grad_x, M * K);
-        if (need_w && O * K > 0) {
-            hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, s, grad_vth_pos, O * K);
-            hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, s, grad_vth_neg, O * K);
+    // degenerate shapes: empty reductions give zero gradients (with glue and K == 0 the
+    // glue still acts on idiff = 0 and its gradients are computed below)
+    if (M == 0 || O == 0 || (K == 0 && !glue)) {
+        if (need_x) zero_fill(grad_x, M * K, s);
+        if (need_w) {
+            zero_fill(grad_vth_pos, O * K, s);
+            zero_fill(grad_vth_neg, O * K, s);
+        }
+        if (gg) {
+            zero_fill(gg->in_affine, 2, s);
+            zero_fill(gg->r_tia, 1, s);
+            zero_fill(gg->adc_scale, O, s);
+            zero_fill(gg->adc_shift, O, s);
         }
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "zero fill launch");
         return 0;
     }
     if (!grad_out) return fail(ISA_EKV_EINVAL, "grad_out is null");
-    const BwdPlan p = plan_backward(M, K, O, cs.exact ? 0 : cs.n_entries, need_x, need_w);
+    const BwdPlan p = plan_backward(M, K, O, cs.exact ? 0 : cs.n_entries, need_x, need_w, glue != nullptr);
     if (!workspace || workspace_bytes < p.bytes)
         return fail(ISA_EKV_EINVAL, "backward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
     char* ws = static_cast<char*>(workspace);
     CallTimer call_timer(s, 3);
+    float* col_part = reinterpret_cast<float*>(ws + p.off_glue);
+    float* r_part = col_part + (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) / 4;
+    float2* aff_part = reinterpret_cast<float2*>(r_part + (size_t)round_up(kGlueBlocks * 4, 256) / 4);
+    if (glue) {
+        GlueGradArgs ga{grad_out, idiff, M, O, p.Op, glue->r_tia, glue->y_lo, glue->y_hi, glue->adc_scale,
+                        reinterpret_cast<float*>(ws + p.off_gpad), col_part, r_part};
+        hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks), dim3(256), 0, s, ga);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "glue grad launch");
+        if (K == 0) {  // nothing reaches x or the thresholds
+            if (gg) zero_fill(gg->in_affine, 2, s);
+            if (gg && (gg->r_tia || gg->adc_scale || gg->adc_shift))
+                hipLaunchKernelGGL(glue_reduce_kernel, dim3((O + 255) / 256), dim3(256), 0, s, col_part, r_part,
+                                   aff_part, O, p.Op, gg->adc_scale, gg->adc_shift, gg->r_tia, nullptr);
+            err = hipGetLastError();
+            if (err != hipSuccess) return hip_fail(err, "glue reduce launch");
+            return 0;
+        }
+    }
     const PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 4, ws, p.off_xrec, p.off_wsT,
-                                  p.off_xrec_alt, p.off_wsT_alt, p.off_part);
+                                  p.off_xrec_alt, p.off_wsT_alt, p.off_part, glue);
     hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "backward prep launch");
     const float* g = grad_out;
     int ldg = (int)O;
-    if (p.grad_padded) {
+    if (glue) {
+        g = reinterpret_cast<const float*>(ws + p.off_gpad);
+        ldg = (int)p.Op;
+    } else if (p.grad_padded) {
         float* gp = reinterpret_cast<float*>(ws + p.off_gpad);
         hipLaunchKernelGGL(pad_grad_kernel, dim3(1024), dim3(256), 0, s, grad_out, M, O, p.Op, gp);
         err = hipGetLastError();
@@ -1411,8 +1672,10 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "backward launch");
     if (need_x) {
-        hipLaunchKernelGGL(dx_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dx),
-                           p.n_ob, M * K, scale, grad_x);
+        const float* aff = glue ? glue->in_affine : nullptr;
+        hipLaunchKernelGGL(dx_reduce_kernel, dim3(kDxReduceBlocks), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(ws + p.off_dx), p.n_ob, M * K, scale, grad_x, x, aff,
+                           glue ? glue->in_lo : 0.0f, glue ? glue->in_hi : 0.0f, aff_part);
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
     }
@@ -1421,6 +1684,29 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
                            p.n_split, (int)K, (int)O, (int)p.Kp, (int)p.Op, scale, grad_vth_pos, grad_vth_neg);
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "dv reduce launch");
+    }
+    if (need_glue) {
+        hipLaunchKernelGGL(glue_reduce_kernel, dim3((O + 255) / 256), dim3(256), 0, s, col_part, r_part, aff_part, O,
+                           p.Op, gg->adc_scale, gg->adc_shift, gg->r_tia, gg->in_affine);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "glue reduce launch");
+    }
+    return 0;
+}
+
+// need_x: whether grad_x is given (or has no elements, M * K == 0)
+int check_glue(const isa_ekv_glue* glue, const isa_ekv_glue_grads* gg, bool need_x) {
+    if (!glue) return fail(ISA_EKV_EINVAL, "glue is null");
+    if (glue->adc_scale && !glue->adc_shift) return fail(ISA_EKV_EINVAL, "adc_scale needs adc_shift");
+    if (glue->in_affine && !(glue->in_hi >= glue->in_lo)) return fail(ISA_EKV_EINVAL, "input range needs in_hi >= in_lo");
+    if (glue->r_tia && !(glue->y_hi >= glue->y_lo)) return fail(ISA_EKV_EINVAL, "output range needs y_hi >= y_lo");
+    if (gg) {
+        if (gg->in_affine && !glue->in_affine) return fail(ISA_EKV_EINVAL, "input-mapping gradient without in_affine");
+        if (gg->in_affine && !need_x)
+            return fail(ISA_EKV_EINVAL, "the input-mapping gradient needs grad_x (it is formed from dX)");
+        if (gg->r_tia && !glue->r_tia) return fail(ISA_EKV_EINVAL, "r_tia gradient without r_tia");
+        if ((gg->adc_scale || gg->adc_shift) && !glue->adc_scale)
+            return fail(ISA_EKV_EINVAL, "ADC affine gradient without adc_scale/adc_shift");
     }
     return 0;
 }
@@ -1591,6 +1877,49 @@ int isa_ekv_exact_backward(const float* x, const float* vth_pos, const float* vt
     if (rc) return rc;
     return run_backward(cs, x, vth_pos, vth_neg, grad_out, M, K, O, v_sat, grad_x, grad_vth_pos, grad_vth_neg,
                         workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t isa_ekv_layer_forward_workspace(int64_t M, int64_t K, int64_t O) {
+    return isa_ekv_forward_workspace(M, K, O);
+}
+
+size_t isa_ekv_layer_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x,
+                                        int need_grad_w) {
+    if (M < 0 || K < 0 || O < 0 || n_entries < 1) return 0;
+    return plan_backward(M, K, O, n_entries, need_grad_x != 0, need_grad_w != 0, true).bytes;
+}
+
+int isa_ekv_layer_forward(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd, int64_t M,
+                          int64_t K, int64_t O, int n_entries, float delta_min, float delta_max, float v_sat,
+                          float idiff_min, float idiff_max, const isa_ekv_glue* glue, float* idiff, float* out,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_common(x, vth_pos, vth_neg, lut_fwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
+    if (rc) return rc;
+    rc = check_glue(glue, nullptr, false);
+    if (rc) return rc;
+    if (n_entries > kMaxEntriesFwd)
+        return fail(ISA_EKV_EINVAL, "LDS-resident forward supports LUT_DELTA_SIZE <= %d (got %d)",
+                    kMaxEntriesFwd, n_entries);
+    return run_forward(lut_setup(lut_fwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, M, K, O, v_sat,
+                       idiff_min, idiff_max, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream), glue,
+                       idiff);
+}
+
+int isa_ekv_layer_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
+                           const float* idiff, const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries,
+                           float delta_min, float delta_max, float v_sat, const isa_ekv_glue* glue, float* grad_x,
+                           float* grad_vth_pos, float* grad_vth_neg, const isa_ekv_glue_grads* glue_grads,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_common(x, vth_pos, vth_neg, lut_bwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
+    if (rc) return rc;
+    rc = check_glue(glue, glue_grads, grad_x != nullptr || M * K == 0);
+    if (rc) return rc;
+    if (n_entries > kMaxEntriesBwd)
+        return fail(ISA_EKV_EINVAL, "shared backward supports LUT_DELTA_SIZE <= %d", kMaxEntriesBwd);
+    if (M * O > 0 && !idiff) return fail(ISA_EKV_EINVAL, "idiff is null");
+    return run_backward(lut_setup(lut_bwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, grad_out, M, K,
+                        O, v_sat, grad_x, grad_vth_pos, grad_vth_neg, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(stream), glue, idiff, glue_grads);
 }
 
 }  // extern "C"

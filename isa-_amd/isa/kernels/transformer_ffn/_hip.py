@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -37,6 +37,10 @@ EXPORTS = (
     "isa_ekv_exact_forward",
     "isa_ekv_exact_backward_workspace",
     "isa_ekv_exact_backward",
+    "isa_ekv_layer_forward_workspace",
+    "isa_ekv_layer_backward_workspace",
+    "isa_ekv_layer_forward",
+    "isa_ekv_layer_backward",
     "isa_ekv_profile_begin",
     "isa_ekv_profile_end",
 )
@@ -47,6 +51,32 @@ _lib = None
 
 class HipExtensionError(RuntimeError):
     pass
+
+
+class Glue(ctypes.Structure):
+    """isa_ekv_glue: device pointers (0 = step skipped) and clamp bounds of the layer glue."""
+
+    _fields_ = [
+        ("in_affine", ctypes.c_void_p),
+        ("in_lo", ctypes.c_float),
+        ("in_hi", ctypes.c_float),
+        ("r_tia", ctypes.c_void_p),
+        ("y_lo", ctypes.c_float),
+        ("y_hi", ctypes.c_float),
+        ("adc_scale", ctypes.c_void_p),
+        ("adc_shift", ctypes.c_void_p),
+    ]
+
+
+class GlueGrads(ctypes.Structure):
+    """isa_ekv_glue_grads: device pointers for the glue parameters' gradients (0 = not needed)."""
+
+    _fields_ = [
+        ("in_affine", ctypes.c_void_p),
+        ("r_tia", ctypes.c_void_p),
+        ("adc_scale", ctypes.c_void_p),
+        ("adc_shift", ctypes.c_void_p),
+    ]
 
 
 def _declare(lib) -> None:
@@ -85,6 +115,16 @@ def _declare(lib) -> None:
     lib.isa_ekv_exact_backward.argtypes = [vp, vp, vp, vp, i64, i64, i64, ctypes.POINTER(f64), f32,
                                            vp, vp, vp, vp, sz, vp]
     lib.isa_ekv_exact_backward.restype = ci
+    lib.isa_ekv_layer_forward_workspace.argtypes = [i64, i64, i64]
+    lib.isa_ekv_layer_forward_workspace.restype = sz
+    lib.isa_ekv_layer_backward_workspace.argtypes = [i64, i64, i64, ci, ci, ci]
+    lib.isa_ekv_layer_backward_workspace.restype = sz
+    lib.isa_ekv_layer_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, f32, f32,
+                                          ctypes.POINTER(Glue), vp, vp, vp, sz, vp]
+    lib.isa_ekv_layer_forward.restype = ci
+    lib.isa_ekv_layer_backward.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32,
+                                           ctypes.POINTER(Glue), vp, vp, vp, ctypes.POINTER(GlueGrads), vp, sz, vp]
+    lib.isa_ekv_layer_backward.restype = ci
     lib.isa_ekv_profile_begin.argtypes = []
     lib.isa_ekv_profile_begin.restype = ci
     lib.isa_ekv_profile_end.argtypes = [ctypes.POINTER(f64), ctypes.POINTER(ci)]

@@ -191,3 +191,115 @@ def exact_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad
                                         ws.data_ptr(), ws.numel(), _hip.stream_handle(dev))
     _hip.check(rc, "isa_ekv_exact_backward")
     return gx, gp, gn
+
+
+def _glue_struct(in_affine, in_range, r_tia, y_range, adc_scale, adc_shift) -> "_hip.Glue":
+    g = _hip.Glue()
+    g.in_affine = _ptr(in_affine)
+    g.in_lo, g.in_hi = (float(v) for v in in_range)
+    g.r_tia = _ptr(r_tia)
+    g.y_lo, g.y_hi = (float(v) for v in y_range)
+    g.adc_scale = _ptr(adc_scale)
+    g.adc_shift = _ptr(adc_shift)
+    return g
+
+
+def _glue_operand(t: Optional[torch.Tensor], numel: int, name: str, device) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    _require_cuda(t, name)
+    if t.device != device:
+        raise RuntimeError(f"{name} must be on {device}")
+    t = as_kernel_f32(t.detach().reshape(-1))
+    if t.numel() != numel:
+        raise RuntimeError(f"{name} must have {numel} elements, got {t.numel()}")
+    return t
+
+
+def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_records: torch.Tensor,
+                      n_entries: int, delta_min: float, delta_max: float, v_sat: float, idiff_min: float,
+                      idiff_max: float, *, in_affine: Optional[torch.Tensor] = None, in_range=(0.0, 4.0),
+                      r_tia: Optional[torch.Tensor] = None, y_range=(-4.0, 4.0),
+                      adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None):
+    """(out, idiff) of the LUT projection with its glue fused: x -> clamp(x*s + b) ->
+    Idiff (clamped to [idiff_min, idiff_max]) -> clamp(Idiff * r_tia) -> * adc_scale + adc_shift."""
+    lib = _hip.load()
+    M, K, O = _check_operands(x, wpos, wneg)
+    if n_entries > MAX_ENTRIES_FORWARD:
+        raise RuntimeError(f"LDS-resident LUT forward supports LUT_DELTA_SIZE <= {MAX_ENTRIES_FORWARD}")
+    dev = x.device
+    aff = _glue_operand(in_affine, 2, "in_affine", dev)
+    r = _glue_operand(r_tia, 1, "r_tia", dev)
+    a_s = _glue_operand(adc_scale, O, "adc_scale", dev)
+    a_c = _glue_operand(adc_shift, O, "adc_shift", dev)
+    if (a_s is None) != (a_c is None):
+        raise RuntimeError("adc_scale and adc_shift go together")
+    out = torch.empty((M, O), dtype=torch.float32, device=dev)
+    idiff = torch.empty((M, O), dtype=torch.float32, device=dev)
+    if M == 0 or O == 0:
+        return out, idiff
+    x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
+    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c)
+    ws = _workspace(lib.isa_ekv_layer_forward_workspace(M, K, O), dev)
+    with torch.cuda.device(dev):
+        rc = lib.isa_ekv_layer_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), fwd_records.data_ptr(), M, K, O,
+                                       int(n_entries), float(delta_min), float(delta_max), float(v_sat),
+                                       float(idiff_min), float(idiff_max), ctypes.byref(glue), idiff.data_ptr(),
+                                       out.data_ptr(), ws.data_ptr(), ws.numel(), _hip.stream_handle(dev))
+    _hip.check(rc, "isa_ekv_layer_forward")
+    return out, idiff
+
+
+def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_out: torch.Tensor,
+                       idiff: torch.Tensor, bwd_records: torch.Tensor, n_entries: int, delta_min: float,
+                       delta_max: float, v_sat: float, *, need_grad_x: bool, need_grad_w: bool,
+                       in_affine: Optional[torch.Tensor] = None, in_range=(0.0, 4.0),
+                       r_tia: Optional[torch.Tensor] = None, y_range=(-4.0, 4.0),
+                       adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None,
+                       need_in_affine: bool = False, need_r_tia: bool = False, need_adc: bool = False):
+    """Gradients of lut_layer_forward's out: dict with dx, dvth_pos, dvth_neg, d_in_affine,
+    d_r_tia, d_adc_scale, d_adc_shift (None where not requested), all fp32."""
+    lib = _hip.load()
+    M, K, O = _check_operands(x, wpos, wneg)
+    _require_cuda(grad_out, "grad_out")
+    if tuple(grad_out.shape) != (M, O) or tuple(idiff.shape) != (M, O):
+        raise RuntimeError(f"grad_out and idiff must be [{M}, {O}]")
+    if n_entries > MAX_ENTRIES_BACKWARD:
+        raise RuntimeError(f"shared backward supports LUT_DELTA_SIZE <= {MAX_ENTRIES_BACKWARD}")
+    dev = x.device
+    aff = _glue_operand(in_affine, 2, "in_affine", dev)
+    r = _glue_operand(r_tia, 1, "r_tia", dev)
+    a_s = _glue_operand(adc_scale, O, "adc_scale", dev)
+    a_c = _glue_operand(adc_shift, O, "adc_shift", dev)
+    need_in_affine = need_in_affine and aff is not None
+    need_x = need_grad_x or need_in_affine  # the mapping's gradient is formed from dX
+    f32 = dict(dtype=torch.float32, device=dev)
+    res = {
+        "dx": torch.empty((M, K), **f32) if need_x else None,
+        "dvth_pos": torch.empty((O, K), **f32) if need_grad_w else None,
+        "dvth_neg": torch.empty((O, K), **f32) if need_grad_w else None,
+        "d_in_affine": torch.empty(2, **f32) if need_in_affine else None,
+        "d_r_tia": torch.empty(1, **f32) if (need_r_tia and r is not None) else None,
+        "d_adc_scale": torch.empty(O, **f32) if (need_adc and a_s is not None) else None,
+        "d_adc_shift": torch.empty(O, **f32) if (need_adc and a_s is not None) else None,
+    }
+    grads = _hip.GlueGrads()
+    grads.in_affine = _ptr(res["d_in_affine"])
+    grads.r_tia = _ptr(res["d_r_tia"])
+    grads.adc_scale = _ptr(res["d_adc_scale"])
+    grads.adc_shift = _ptr(res["d_adc_shift"])
+    if not (need_x or need_grad_w or any(res[k] is not None for k in ("d_r_tia", "d_adc_scale"))):
+        return res
+    x32, wp32, wn32, g32, id32 = (as_kernel_f32(t) for t in (x, wpos, wneg, grad_out, idiff))
+    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c)
+    ws = _workspace(lib.isa_ekv_layer_backward_workspace(M, K, O, int(n_entries), int(need_x), int(need_grad_w)), dev)
+    with torch.cuda.device(dev):
+        rc = lib.isa_ekv_layer_backward(_ptr(x32), _ptr(wp32), _ptr(wn32), _ptr(g32), _ptr(id32),
+                                        bwd_records.data_ptr(), M, K, O, int(n_entries), float(delta_min),
+                                        float(delta_max), float(v_sat), ctypes.byref(glue), _ptr(res["dx"]),
+                                        _ptr(res["dvth_pos"]), _ptr(res["dvth_neg"]), ctypes.byref(grads),
+                                        ws.data_ptr(), ws.numel(), _hip.stream_handle(dev))
+    _hip.check(rc, "isa_ekv_layer_backward")
+    if not need_grad_x:
+        res["dx"] = None
+    return res

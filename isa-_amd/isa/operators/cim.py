@@ -10,10 +10,17 @@ value the HIP exact-formula kernels through `triton_ekv_matmul`.
 Only the device paths exist here: a CPU input or `use_triton=False` raises instead of
 silently running another implementation (the reference would fall back to its
 exact-formula PyTorch path, `cim.py:201-214`).
+
+On the LUT path the elementwise glue around each projection (TIA gain and output clamp,
+and in `PhysicalFFN`/`HybridFFN` the input voltage mapping and the ADC affine) runs fused
+into the library's kernels (`fused_layer.py`); `ISA_EKV_FUSE_GLUE=0` (or setting
+`FUSE_GLUE = False` here) keeps it as separate PyTorch ops. Output-statistics tracking
+and non-fp32 inputs to the voltage mapping use the separate ops.
 """
 
 from __future__ import annotations
 
+import os
 from typing import Dict, Optional
 
 import torch
@@ -22,6 +29,9 @@ import torch.nn as nn
 from isa.device_models.config import FLASH_TRANSISTOR_EKV_CONFIG as PHYSICAL_CONFIG
 from isa.kernels.transformer_ffn.ekv_lut_triton import triton_lut_ekv_matmul
 from isa.kernels.transformer_ffn.ekv_triton import triton_ekv_matmul
+from isa.kernels.transformer_ffn.fused_layer import fused_cim_layer
+
+FUSE_GLUE = os.environ.get("ISA_EKV_FUSE_GLUE", "1") != "0"
 
 
 class VoltageMapping(nn.Module):
@@ -162,10 +172,30 @@ class CIMLinear(nn.Module):
             self.vth_pos.clamp_(v_min, v_max)
             self.vth_neg.clamp_(v_min, v_max)
 
+    def fusable(self, x: torch.Tensor) -> bool:
+        """Whether the fused LUT layer (projection + glue in the library) serves this input."""
+        return (FUSE_GLUE and x.is_cuda and bool(self.cfg.get("use_triton", False))
+                and str(self.cfg.get("ekv_approx", "lut")).lower() == "lut" and not self.track_output_stats)
+
+    def fused_forward(self, x: torch.Tensor, in_affine: Optional[torch.Tensor] = None,
+                      in_range=(0.0, 4.0), adc_scale: Optional[torch.Tensor] = None,
+                      adc_shift: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """forward() with the glue in the library; optionally also the input mapping
+        clamp(x * in_affine[0] + in_affine[1], in_range) before and the ADC affine after."""
+        b, n, in_f = x.shape
+        assert in_f == self.in_features
+        flat = x.reshape(b * n, in_f)
+        out = fused_cim_layer(flat, self.vth_pos, self.vth_neg, self.cfg, in_affine=in_affine, in_range=in_range,
+                              r_tia=self.r_tia.to(device=x.device, dtype=torch.float32).reshape(1),
+                              adc_scale=adc_scale, adc_shift=adc_shift)
+        return out.reshape(b, n, self.out_features)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         b, n, in_f = x.shape
         assert in_f == self.in_features
         project = _device_projection(self.cfg, x, "forward")
+        if self.fusable(x):
+            return self.fused_forward(x)
 
         r_tia = self.r_tia.to(device=x.device, dtype=torch.float32).view(1, 1, 1)
         v_signed_min = float(self.cfg.get("V_signed_min", -4.0))
@@ -203,6 +233,12 @@ class PhysicalFFN(nn.Module):
         self.adc_affine_shift = nn.Parameter(torch.zeros(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.dtype == torch.float32 and self.fc1.fusable(x) and self.fc2.fusable(x):
+            _device_projection(self.fc1.cfg, x, "forward")
+            m = self.input_mapping
+            h = self.fc1.fused_forward(x, in_affine=torch.stack([m.scale, m.shift]).float(),
+                                       in_range=(0.0, m.voltage_max))
+            return self.fc2.fused_forward(h, adc_scale=self.adc_affine_scale, adc_shift=self.adc_affine_shift)
         x = self.input_mapping(x)
         x = self.fc1(x)
         x = self.fc2(x)
@@ -229,8 +265,14 @@ class HybridFFN(nn.Module):
         self.fc2 = nn.Linear(hidden_dim, dim)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x = self.input_mapping(x)
-        x = self.fc1(x)
+        if x.dtype == torch.float32 and self.fc1.fusable(x):
+            _device_projection(self.fc1.cfg, x, "forward")
+            m = self.input_mapping
+            x = self.fc1.fused_forward(x, in_affine=torch.stack([m.scale, m.shift]).float(),
+                                       in_range=(0.0, m.voltage_max))
+        else:
+            x = self.input_mapping(x)
+            x = self.fc1(x)
         x = self.fc2(x)
         return x
 

@@ -122,6 +122,43 @@ def test_exact_entry_points_reject_bad_arguments_before_launch():
     assert lib.isa_ekv_exact_backward_workspace(-1, 96, 256, 1, 1) == 0
 
 
+def test_layer_entry_points_reject_bad_glue_before_launch():
+    lib = _hip.load()
+    fake = ctypes.c_void_p(16)
+
+    def fwd(glue):
+        return lib.isa_ekv_layer_forward(fake, fake, fake, fake, 4, 4, 4, 4096, -9.0, 4.0, 8.26, -4.0, 4.0,
+                                         glue, fake, fake, fake, 0, None)
+
+    assert fwd(None) == -1 and "glue is null" in _err(lib)
+    g = _hip.Glue()
+    g.adc_scale = 16
+    assert fwd(ctypes.byref(g)) == -1 and "adc_shift" in _err(lib)
+    g = _hip.Glue()
+    g.r_tia, g.y_lo, g.y_hi = 16, 4.0, -4.0
+    assert fwd(ctypes.byref(g)) == -1 and "y_hi" in _err(lib)
+    g = _hip.Glue()
+    assert fwd(ctypes.byref(g)) == -1 and "workspace too small" in _err(lib)
+
+    def bwd(glue, grads, gx=fake, idiff=fake):
+        return lib.isa_ekv_layer_backward(fake, fake, fake, fake, idiff, fake, 8, 8, 8, 4096, -9.0, 4.0, 8.26,
+                                          glue, gx, fake, fake, grads, fake, 0, None)
+
+    g = _hip.Glue()
+    gg = _hip.GlueGrads()
+    gg.r_tia = 16
+    assert bwd(ctypes.byref(g), ctypes.byref(gg)) == -1 and "r_tia gradient without r_tia" in _err(lib)
+    g.in_affine, g.in_lo, g.in_hi = 16, 0.0, 4.0
+    gg = _hip.GlueGrads()
+    gg.in_affine = 16
+    assert bwd(ctypes.byref(g), ctypes.byref(gg), gx=None) == -1 and "needs grad_x" in _err(lib)
+    assert bwd(ctypes.byref(g), ctypes.byref(gg), idiff=None) == -1 and "idiff is null" in _err(lib)
+    assert bwd(ctypes.byref(g), ctypes.byref(gg)) == -1 and "workspace too small" in _err(lib)
+    # the layer backward needs room for G_eff and the glue partials beyond the plain backward's
+    assert lib.isa_ekv_layer_backward_workspace(64, 96, 256, 4096, 1, 1) > \
+        lib.isa_ekv_backward_workspace(64, 96, 256, 4096, 1, 1)
+
+
 def test_lut_build_and_pack_reject_bad_arguments():
     lib = _hip.load()
     params = (ctypes.c_double * 4)(4.136, 0.0259, 7.5875e-7, 0.1)
