@@ -37,6 +37,10 @@ VALU_PEAK = 256 * 64 * 2.4e9
 # range-checked inner loops (4 log2 per cell forward; 4 log2 + 4 rcp backward, each with
 # the rounding correction of log2(1 + e)), so its fraction measures issue efficiency.
 INSTR_PER_CELL = {"lut": (12, 16), "exact": (32, 52)}
+# measured-codebook path (member mode): issued lane-instructions per cell of the forward
+# and dX inner loops (forward: two id-offset adds, the slope and intercept differences, fma,
+# accumulate; dX: slope gathers only)
+MEASURED_INSTR_PER_CELL = (6, 8)
 
 CONFIGS = {
     # name: (batch, tokens, d_model, d_ffn, physical fc2)
@@ -116,6 +120,84 @@ def measured_traffic(config: str):
     except OSError:
         pass
     return None
+
+
+def measured_fc1_step(args) -> int:
+    """The measured-codebook deployment of a Physical ViT-S fc1 (192 -> 768, measured
+    mode, forward and dX) over X[128, 65, 192] with a synthetic 24-state, 61-point codebook
+    (the FG50 centre-codebook shape). A step is one forward and backward; cell-evals count
+    M*K*O per pass as for the LUT path. Reports the measured kernels' HIP-event times."""
+    import torch
+
+    from isa.device_models.config import make_flash_transistor_ekv_config
+    from isa.kernels.transformer_ffn import _hip
+    from isa.measured_deployment.operator import DeploymentAwareCIMLinear
+
+    dev = torch.device("cuda", 0)
+    B, T, D, F = 128, 65, 192, 768
+    M = B * T
+    cfg = make_flash_transistor_ekv_config(default_lut_size=args.lut_size)
+    torch.manual_seed(0)
+    layer = DeploymentAwareCIMLinear(D, F, cfg).to(dev)
+    vg = torch.linspace(0.0, 4.0, 61)
+    vt = torch.linspace(0.4, 3.6, 24)
+    sp = torch.nn.functional.softplus((vg[None, :] - vt[:, None]) / 0.1)
+    layer.configure_codebook(vg, 2e-9 * sp * sp + 4e-10)
+    layer.set_assignment(torch.randint(0, 24, (F, D)), torch.randint(0, 24, (F, D)))
+    layer.set_forward_mode("measured")
+    x = (torch.randn(B, T, D, device=dev).clamp(0.0, 4.0)).requires_grad_(True)
+    g = torch.randn(B, T, F, device=dev)
+
+    def step():
+        x.grad = None
+        layer(x).backward(g)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with _hip.KernelTimer() as kt:
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    cells = float(M * D * F)
+    value = 2.0 * cells / (ms * 1e-3)
+    fwd_avg = kt.fwd_ms / max(kt.fwd_launches, 1)
+    bwd_avg = kt.bwd_ms / max(kt.bwd_launches, 1)
+    instr_f, instr_b = MEASURED_INSTR_PER_CELL
+    result = {
+        "metric": "measured-codebook CIM cell-evals/sec fwd+dX, ViT-S fc1, 1 GPU",
+        "value": value,
+        "unit": "cell-evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (24-state 61-point codebook, random assignment)",
+        "config": {"workload": "DeploymentAwareCIMLinear 192->768 measured mode, X[128,65,192], fwd+dX",
+                   "tokens": M, "parallelism": "single GPU"},
+        "roofline": {
+            "bound": "valu", "unit": "TOP/s", "peak": round(VALU_PEAK / 1e12, 3),
+            "kernel": "bwd_measured_kernel (dX)", "avg_launch_ms": round(bwd_avg, 4),
+            "achieved": round(cells * instr_b / (bwd_avg * 1e-3) / 1e12, 3),
+            "frac": round(cells * instr_b / (bwd_avg * 1e-3) / VALU_PEAK, 4),
+            "work": f"{instr_b} VALU lane-instr per cell x {cells:.4e} cells per launch",
+            "forward_kernel": {"kernel": "fwd_measured_kernel", "avg_launch_ms": round(fwd_avg, 4),
+                               "frac": round(cells * instr_f / (fwd_avg * 1e-3) / VALU_PEAK, 4)},
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+    log(f"[bench] measured fc1: {ms:.3f} ms/step, fwd {fwd_avg:.3f} ms, dX {bwd_avg:.3f} ms")
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def gpt_train_step(args) -> int:
@@ -221,7 +303,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="gptl_ffn", choices=sorted(CONFIGS) + ["gptl_train"])
+    ap.add_argument("--config", default="gptl_ffn", choices=sorted(CONFIGS) + ["gptl_train", "measured_fc1"])
     ap.add_argument("--lut-size", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -239,6 +321,8 @@ def main() -> int:
 
     if args.config == "gptl_train":
         return gpt_train_step(args)
+    if args.config == "measured_fc1":
+        return measured_fc1_step(args)
 
     import torch
     import torch.nn as nn

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 4
+#define ISA_EKV_ABI_VERSION 5
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -183,6 +183,54 @@ int isa_ekv_layer_backward(const float* x, const float* vth_pos, const float* vt
                            float delta_min, float delta_max, float v_sat, const isa_ekv_glue* glue, float* grad_x,
                            float* grad_vth_pos, float* grad_vth_neg, const isa_ekv_glue_grads* glue_grads,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Measured-codebook projection. Replaces the fused kernel of
+ * measured_deployment/kernels/measured_lut_triton.py:23-142 (fused_measured_forward,
+ * :159-267) and the segmented PyTorch path of DeploymentAwareCIMLinear.measured_forward
+ * (measured_deployment/operator.py:164-224), with its gradient for x. Each cell (o, k)
+ * holds int16 state ids a = ids_a[o][k] and, in member mode, b = ids_b[o][k] into a
+ * codebook of piecewise-linear curves (slopes/intercepts [n_rows][n_seg] fp32, device);
+ * with v = clamp(x, lookup_min, lookup_max) in segment s:
+ *   out_pre[m,o] = current_scale * sum_k ((S[a][s] - S[b][s]) v + (C[a][s] - C[b][s]))
+ *   out[m,o] = clamp(out_pre * r_tia[0], out_min, out_max)
+ * ids_b = null is pair mode (ids_a name difference curves; no b terms). Segments:
+ *   ISA_EKV_SEG_UNIFORM  s = int((v - voltage_min) * inverse_step)            (Triton kernel)
+ *   ISA_EKV_SEG_SEARCH   s = searchsorted(vg, v, right=True) - 1, vg [n_seg+1] (segmented path)
+ *   ISA_EKV_SEG_ROUND    s = rint((v - lookup_min) * inverse_step)            (vin_lut_bins)
+ * each clamped to [0, n_seg - 1]; ids are clamped into [0, n_rows - 1]. */
+#define ISA_EKV_SEG_UNIFORM 0
+#define ISA_EKV_SEG_SEARCH 1
+#define ISA_EKV_SEG_ROUND 2
+
+typedef struct isa_ekv_codebook {
+    const float* slopes;     /* [n_rows][n_seg] */
+    const float* intercepts; /* [n_rows][n_seg] */
+    int n_seg, n_rows;
+    int seg_mode;
+    const float* vg;         /* [n_seg + 1] for ISA_EKV_SEG_SEARCH, else may be null */
+    float voltage_min, inverse_step;
+    float lookup_min, lookup_max;
+} isa_ekv_codebook;
+
+size_t isa_ekv_measured_forward_workspace(int64_t M, int64_t K, int64_t O, int n_seg, int n_rows);
+size_t isa_ekv_measured_backward_workspace(int64_t M, int64_t K, int64_t O, int n_seg, int n_rows);
+
+/* out [M][O]; out_pre [M][O] (nullable) is kept for isa_ekv_measured_backward. r_tia is a
+ * device scalar. */
+int isa_ekv_measured_forward(const float* x, const int16_t* ids_a, const int16_t* ids_b, int64_t M, int64_t K,
+                             int64_t O, const isa_ekv_codebook* codebook, float current_scale, const float* r_tia,
+                             float out_min, float out_max, float* out_pre, float* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* grad_x[m,k] = [lookup_min <= x <= lookup_max] * current_scale * sum_o grad_out[m,o] * r_tia
+ *               * [out_min <= out_pre * r_tia <= out_max] * (S[a][s] - S[b][s]),
+ * the derivative of the piecewise-linear forward as autograd gives it through the
+ * reference's segmented path. The codebook, ids and r_tia get no gradient (the reference
+ * keeps them as fixed buffers / detached). */
+int isa_ekv_measured_backward(const float* x, const int16_t* ids_a, const int16_t* ids_b, int64_t M, int64_t K,
+                              int64_t O, const isa_ekv_codebook* codebook, float current_scale,
+                              const float* grad_out, const float* out_pre, const float* r_tia, float out_min,
+                              float out_max, float* grad_x, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Profiling aid, no reference counterpart: between begin and end, every forward and
  * backward call records HIP events on its stream (up to 4096 intervals). end synchronises

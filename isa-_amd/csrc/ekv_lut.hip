@@ -497,6 +497,10 @@ struct LutFwdCell {
         const float2 en = lut[(unsigned)cn];
         return fmaf(cp, ep.y, ep.x) - fmaf(cn, en.y, en.x);
     }
+    // token record {coordinate, r}; threshold record {+, -}
+    __device__ float accumulate(float acc, float2 xv, float2 w) const {
+        return fmaf((*this)(xv.x, w.x, w.y), xv.y, acc);
+    }
 };
 
 // Backward cells return a pair view whose dp()/dn() (derivative terms) and lp()/ln()
@@ -563,6 +567,9 @@ struct ExactFastFwdCell {
         return fmaf(l1, l1, -(l2 * l2));
     }
     __device__ float operator()(float ex, float ewp, float ewn) const { return one(ex, ewp) - one(ex, ewn); }
+    __device__ float accumulate(float acc, float2 xv, float2 w) const {
+        return fmaf((*this)(xv.x, w.x, w.y), xv.y, acc);
+    }
 };
 
 struct ExactFastBwdCell {
@@ -601,6 +608,9 @@ struct ExactGeneralFwdCell {
         return fmaf(l1, l1, -(l2 * l2));
     }
     __device__ float operator()(float tx, float twp, float twn) const { return one(tx, twp) - one(tx, twn); }
+    __device__ float accumulate(float acc, float2 xv, float2 w) const {
+        return fmaf((*this)(xv.x, w.x, w.y), xv.y, acc);
+    }
 };
 
 struct ExactGeneralBwdCell {
@@ -708,7 +718,7 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
                 const float2 xv = load_uniform2(xrow[i] + k0 + kk);
 #pragma unroll
                 for (int j = 0; j < ORR; ++j) {
-                    acc[i][j] = fmaf(cell(xv.x, w[kk][j].x, w[kk][j].y), xv.y, acc[i][j]);
+                    acc[i][j] = cell.accumulate(acc[i][j], xv, w[kk][j]);
                 }
             }
         }
@@ -1031,6 +1041,194 @@ __global__ __launch_bounds__(1024) void bwd_exact_kernel(BwdArgs a) {
         bwd_body<NEED_X, NEED_W>(a, ExactGeneralBwdCell{a.c2}, a.xrec_alt, a.wsT_alt, red, item);
 }
 
+// ----------------------------------------------------------------------------------
+// Measured-codebook projection (reference: measured_deployment/kernels/measured_lut_triton.py
+// and the segmented path of measured_deployment/operator.py:164-224). Every physical cell
+// (o, k) holds state ids a (positive) and b (negative) of a codebook of piecewise-linear
+// measured I-V curves; for the clamped input v = clamp(x, lookup_min, lookup_max) in
+// segment s,
+//   out[m,o] = clamp(sum_k ((S[s][a] - S[s][b]) v + (C[s][a] - C[s][b])) * scale * r_tia, lo, hi)
+// with S/C the segment slopes/intercepts; in pair mode the id names a precomputed
+// difference curve and the b terms are absent. The table is laid out [segment][state]
+// (float2 {S, C}) so the 64 lanes of one gather read one segment row; it is copied to LDS
+// when it fits (the 24-state codebook: 60 x 24 x 8 B), else read from global memory. A
+// zero record after the table serves padded inputs. The backward gives
+//   dX[m,k] = [lookup_min <= x <= lookup_max] sum_o G'[m,o] (S[s][a] - S[s][b])
+// with G' = G r_tia [lo <= out_pre <= hi] from glue_grad_kernel (no gradient for the
+// fixed codebook, ids or r_tia, as the reference's detached buffers).
+// ----------------------------------------------------------------------------------
+
+constexpr size_t kMeasuredLdsBytes = 128 * 1024;
+
+template <bool PAIR>
+struct MeasuredFwdCell {
+    const char* table;  // record byte offsets: segment row + state * 8
+    // token record {segment row byte offset (bits), v}; id record {a * 8, b * 8} (bits)
+    __device__ float accumulate(float acc, float2 xv, float2 w) const {
+        const unsigned row = __float_as_uint(xv.x);
+        const float2 ra = *reinterpret_cast<const float2*>(table + row + __float_as_uint(w.x));
+        if (PAIR) return acc + fmaf(ra.x, xv.y, ra.y);
+        const float2 rb = *reinterpret_cast<const float2*>(table + row + __float_as_uint(w.y));
+        return acc + fmaf(ra.x - rb.x, xv.y, ra.y - rb.y);
+    }
+};
+
+template <bool PAIR>
+struct MeasuredBwdCell {
+    const char* table;
+    // dp - dn is the cell's slope difference; the current terms do not reach dX
+    __device__ ValueBwdPair operator()(float row_bits, float wa, float wb) const {
+        const unsigned row = __float_as_uint(row_bits);
+        const float2 ra = *reinterpret_cast<const float2*>(table + row + __float_as_uint(wa));
+        ValueBwdPair q{0.0f, ra.x, 0.0f, 0.0f};
+        if (!PAIR) q.d_n = reinterpret_cast<const float2*>(table + row + __float_as_uint(wb))->x;
+        return q;
+    }
+};
+
+struct MeasuredPrepArgs {
+    const float* x;          // [M][K]
+    const short* ids_a;      // [O][K]
+    const short* ids_b;      // [O][K] or null (pair mode)
+    const float* slopes;     // [n_rows][n_seg]
+    const float* intercepts; // [n_rows][n_seg]
+    const float* vg;         // [n_seg + 1] (seg_mode 1)
+    int64_t M, K, O, Kp, Op;
+    int n_seg, n_rows;
+    int seg_mode;            // 0 uniform floor, 1 searchsorted on vg, 2 rounded bins
+    float voltage_min, inverse_step, lookup_min, lookup_max;
+    int rec_floats;          // 2 (forward) or 4 (backward)
+    float* xrec;             // [M][Kp][rec_floats]
+    float2* idT;             // [Kp][Op]
+    float2* table;           // [n_seg * n_rows + 1]
+};
+
+__device__ inline int measured_segment(const MeasuredPrepArgs& a, float v) {
+    if (v != v) return a.seg_mode == 0 ? 0 : a.n_seg - 1;  // NaN: as float->int conversion / sorted last
+    int s;
+    if (a.seg_mode == 0) {
+        s = (int)((v - a.voltage_min) * a.inverse_step);
+    } else if (a.seg_mode == 1) {
+        // searchsorted(vg, v, right=True) - 1: the number of grid points <= v, minus one
+        int lo = 0, hi = a.n_seg + 1;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (a.vg[mid] <= v)
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        s = lo - 1;
+    } else {
+        s = a.n_seg == 1 ? 0 : (int)rintf((v - a.lookup_min) * a.inverse_step);
+    }
+    return s < 0 ? 0 : (s > a.n_seg - 1 ? a.n_seg - 1 : s);
+}
+
+__global__ __launch_bounds__(256) void measured_prep_kernel(MeasuredPrepArgs a) {
+    const int64_t zero_row = (int64_t)a.n_seg * a.n_rows * 8;  // byte offset of the zero record
+    if (blockIdx.x < kPrepBlocksX) {
+        for (int64_t m = blockIdx.x; m < a.M; m += kPrepBlocksX) {
+            for (int k = threadIdx.x; k < (int)a.Kp; k += blockDim.x) {
+                float v = 0.0f;
+                unsigned row = (unsigned)zero_row;
+                if (k < a.K) {
+                    const float xv = a.x[m * a.K + k];
+                    v = xv != xv ? xv : fminf(fmaxf(xv, a.lookup_min), a.lookup_max);
+                    row = (unsigned)((int64_t)measured_segment(a, v) * a.n_rows * 8);
+                }
+                const int64_t e = m * a.Kp + k;
+                if (a.rec_floats == 2)
+                    reinterpret_cast<float2*>(a.xrec)[e] = make_float2(__uint_as_float(row), v);
+                else
+                    reinterpret_cast<float4*>(a.xrec)[e] = make_float4(__uint_as_float(row), 1.0f, 0.0f, v);
+            }
+        }
+        return;
+    }
+    if (blockIdx.x < kPrepBlocksX + kPrepBlocksW) {
+        // ids: 64(o) x 32(k) tiles transposed through LDS, ids clamped into the codebook
+        __shared__ int2 tile[32][65];
+        const int64_t n_ot = a.Op / 64, n_kt = (a.Kp + 31) / 32;
+        const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+        for (int64_t t = blockIdx.x - kPrepBlocksX; t < n_ot * n_kt; t += kPrepBlocksW) {
+            const int64_t ot = t % n_ot, kt = t / n_ot;
+            for (int rr = ty; rr < 64; rr += 8) {
+                int64_t o = ot * 64 + rr;
+                const int64_t k = kt * 32 + tx;
+                int2 v = make_int2(0, 0);  // padded inputs: state 0 on the zero record
+                if (k < a.K && a.O > 0) {
+                    if (o >= a.O) o = a.O - 1;  // padded outputs copy a real row; dropped
+                    int ia = a.ids_a[o * a.K + k], ib = a.ids_b ? a.ids_b[o * a.K + k] : 0;
+                    ia = ia < 0 ? 0 : (ia >= a.n_rows ? a.n_rows - 1 : ia);
+                    ib = ib < 0 ? 0 : (ib >= a.n_rows ? a.n_rows - 1 : ib);
+                    v = make_int2(ia * 8, ib * 8);
+                }
+                tile[tx][rr] = v;
+            }
+            __syncthreads();
+            for (int rr = ty; rr < 32; rr += 8) {
+                const int64_t k = kt * 32 + rr;
+                if (k < a.Kp) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int2 v = tile[rr][h * 32 + tx];
+                        a.idT[k * a.Op + ot * 64 + h * 32 + tx] = make_float2(__int_as_float(v.x), __int_as_float(v.y));
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    // codebook records [segment][state] {slope, intercept} and the zero record
+    const int64_t total = (int64_t)a.n_seg * a.n_rows;
+    for (int64_t e = (int64_t)(blockIdx.x - kPrepBlocksX - kPrepBlocksW) * blockDim.x + threadIdx.x; e <= total;
+         e += (int64_t)kPrepBlocksW * blockDim.x) {
+        if (e == total) {
+            a.table[e] = make_float2(0.0f, 0.0f);
+        } else {
+            const int64_t seg = e / a.n_rows, st = e - seg * a.n_rows;
+            a.table[e] = make_float2(a.slopes[st * a.n_seg + seg], a.intercepts[st * a.n_seg + seg]);
+        }
+    }
+}
+
+template <int MR, bool PAIR, bool LDS>
+__global__ __launch_bounds__(kFwdWaves * 64) void fwd_measured_kernel(FwdArgs a) {
+    extern __shared__ float2 s_tab[];
+    const float2* tab = reinterpret_cast<const float2*>(a.lut);
+    if constexpr (LDS) {
+        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_tab[i] = tab[i];
+        __syncthreads();
+        tab = s_tab;
+    }
+    int m0, o_lane;
+    if (!fwd_tile(a, MR, m0, o_lane)) return;
+    fwd_body<MR, kFwdORR, false>(a, MeasuredFwdCell<PAIR>{reinterpret_cast<const char*>(tab)}, a.xrec, a.wsT, m0,
+                                 o_lane);
+}
+
+template <bool PAIR, bool LDS>
+__global__ __launch_bounds__(1024) void bwd_measured_kernel(BwdArgs a) {
+    extern __shared__ float4 s_mtab[];
+    const float2* tab = reinterpret_cast<const float2*>(a.lut);
+    size_t table_floats4 = 0;
+    if constexpr (LDS) {
+        float2* s2 = reinterpret_cast<float2*>(s_mtab);
+        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s2[i] = tab[i];
+        __syncthreads();
+        tab = s2;
+        table_floats4 = (size_t)(a.NP + 1) / 2;
+    }
+    const int waves = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* red = reinterpret_cast<float*>(s_mtab + table_floats4) + wave * (kBwdMB * kBwdKR * kRedStride);
+    const int item = blockIdx.x * waves + wave;
+    if (item >= a.n_items) return;
+    bwd_body<true, false>(a, MeasuredBwdCell<PAIR>{reinterpret_cast<const char*>(tab)}, a.xrec, a.wsT, red, item);
+}
+
 // dX[m,k] = scale * sum over output blocks, in block order (deterministic); scale is 1 for
 // the LUT path and the derivative constant of the exact cells. With an input mapping
 // v = clamp(x * s + b) in front of the layer (in_affine), dX is the gradient for v and this
@@ -1039,10 +1237,13 @@ __global__ __launch_bounds__(1024) void bwd_exact_kernel(BwdArgs a) {
 // mask*dv*x (ds) and mask*dv (db) to aff_part[block] for glue_reduce_kernel.
 constexpr int kDxReduceBlocks = 1024;
 
+// range_mask (no in_affine): dx = dv where lo <= x <= hi, else 0 (torch.clamp's backward of
+// the measured path's input clamp).
 __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict__ part, int n_ob,
                                                         int64_t n, float scale, float* __restrict__ dx,
                                                         const float* __restrict__ x, const float* in_affine,
-                                                        float in_lo, float in_hi, float2* __restrict__ aff_part) {
+                                                        float in_lo, float in_hi, float2* __restrict__ aff_part,
+                                                        int range_mask = 0) {
     const float aff_s = in_affine ? in_affine[0] : 1.0f;
     const float aff_b = in_affine ? in_affine[1] : 0.0f;
     float ds = 0.0f, db = 0.0f;
@@ -1051,7 +1252,10 @@ __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict_
         float s = part[e];
         for (int b = 1; b < n_ob; ++b) s += part[(size_t)b * n + e];
         s *= scale;
-        if (in_affine) {
+        if (range_mask) {
+            const float xv = x[e];
+            s = (xv >= in_lo && xv <= in_hi) ? s : 0.0f;
+        } else if (in_affine) {
             const float xv = x[e];
             const float pre = mapped_pre(xv, aff_s, aff_b);
             const float g = (pre >= in_lo && pre <= in_hi) ? s : 0.0f;
@@ -1711,6 +1915,203 @@ int check_glue(const isa_ekv_glue* glue, const isa_ekv_glue_grads* gg, bool need
     return 0;
 }
 
+
+// ----------------------------------------------------------------------------------
+// Measured-codebook calls.
+// ----------------------------------------------------------------------------------
+
+constexpr size_t kMeasuredBwdLdsTableBytes = 88 * 1024;  // with 16 waves' dX buffers, within 160 KB
+
+size_t measured_table_bytes(int n_seg, int n_rows) {
+    return (size_t)round_up(((int64_t)n_seg * n_rows + 1) * 8, 256);
+}
+
+int check_codebook(const isa_ekv_codebook* cb, const short* ids_a) {
+    if (!cb) return fail(ISA_EKV_EINVAL, "codebook is null");
+    if (cb->n_seg < 1 || cb->n_rows < 1) return fail(ISA_EKV_EINVAL, "codebook needs n_seg >= 1 and n_rows >= 1");
+    if ((int64_t)cb->n_seg * cb->n_rows > (int64_t)INT32_MAX / 16)
+        return fail(ISA_EKV_EINVAL, "codebook too large (n_seg * n_rows records)");
+    if (!cb->slopes || !cb->intercepts) return fail(ISA_EKV_EINVAL, "codebook slopes/intercepts are null");
+    if (cb->seg_mode < ISA_EKV_SEG_UNIFORM || cb->seg_mode > ISA_EKV_SEG_ROUND)
+        return fail(ISA_EKV_EINVAL, "unknown segment mode %d", cb->seg_mode);
+    if (cb->seg_mode == ISA_EKV_SEG_SEARCH && !cb->vg) return fail(ISA_EKV_EINVAL, "segment search needs vg");
+    if (!(cb->lookup_max >= cb->lookup_min)) return fail(ISA_EKV_EINVAL, "lookup range needs lookup_max >= lookup_min");
+    if (!ids_a) return fail(ISA_EKV_EINVAL, "ids_a is null");
+    return 0;
+}
+
+MeasuredPrepArgs measured_prep(const isa_ekv_codebook* cb, const float* x, const short* ids_a, const short* ids_b,
+                               int64_t M, int64_t K, int64_t O, int64_t Kp, int64_t Op, int rec_floats, float* xrec,
+                               float2* idT, float2* table) {
+    MeasuredPrepArgs pa{};
+    pa.x = x;
+    pa.ids_a = ids_a;
+    pa.ids_b = ids_b;
+    pa.slopes = cb->slopes;
+    pa.intercepts = cb->intercepts;
+    pa.vg = cb->vg;
+    pa.M = M;
+    pa.K = K;
+    pa.O = O;
+    pa.Kp = Kp;
+    pa.Op = Op;
+    pa.n_seg = cb->n_seg;
+    pa.n_rows = cb->n_rows;
+    pa.seg_mode = cb->seg_mode;
+    pa.voltage_min = cb->voltage_min;
+    pa.inverse_step = cb->inverse_step;
+    pa.lookup_min = cb->lookup_min;
+    pa.lookup_max = cb->lookup_max;
+    pa.rec_floats = rec_floats;
+    pa.xrec = xrec;
+    pa.idT = idT;
+    pa.table = table;
+    return pa;
+}
+
+template <bool PAIR>
+void launch_fwd_measured(bool lds, int mr, dim3 grid, size_t lds_bytes, hipStream_t s, const FwdArgs& fa) {
+    const dim3 block(kFwdWaves * 64);
+    if (lds) {
+        if (mr == 8) hipLaunchKernelGGL((fwd_measured_kernel<8, PAIR, true>), grid, block, lds_bytes, s, fa);
+        else if (mr == 4) hipLaunchKernelGGL((fwd_measured_kernel<4, PAIR, true>), grid, block, lds_bytes, s, fa);
+        else hipLaunchKernelGGL((fwd_measured_kernel<2, PAIR, true>), grid, block, lds_bytes, s, fa);
+    } else {
+        if (mr == 8) hipLaunchKernelGGL((fwd_measured_kernel<8, PAIR, false>), grid, block, 0, s, fa);
+        else if (mr == 4) hipLaunchKernelGGL((fwd_measured_kernel<4, PAIR, false>), grid, block, 0, s, fa);
+        else hipLaunchKernelGGL((fwd_measured_kernel<2, PAIR, false>), grid, block, 0, s, fa);
+    }
+}
+
+int run_measured_forward(const float* x, const short* ids_a, const short* ids_b, int64_t M, int64_t K, int64_t O,
+                         const isa_ekv_codebook* cb, float current_scale, const float* r_tia, float out_min,
+                         float out_max, float* out_pre, float* out, void* workspace, size_t workspace_bytes,
+                         hipStream_t s) {
+    if (M == 0 || O == 0) return 0;
+    if (!out) return fail(ISA_EKV_EINVAL, "out is null");
+    const FwdPlan p = plan_forward(M, K, O, false);
+    const size_t tbytes = measured_table_bytes(cb->n_seg, cb->n_rows);
+    const size_t need = p.bytes + tbytes;
+    if (!workspace || workspace_bytes < need)
+        return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, need);
+    char* ws = static_cast<char*>(workspace);
+    CallTimer call_timer(s, 2);
+    float2* table = reinterpret_cast<float2*>(ws + p.bytes);
+    const MeasuredPrepArgs pa = measured_prep(cb, x, ids_a, ids_b, M, K, O, p.Kp, p.Op, 2,
+                                              reinterpret_cast<float*>(ws + p.off_xrec),
+                                              reinterpret_cast<float2*>(ws + p.off_wsT), table);
+    hipLaunchKernelGGL(measured_prep_kernel, dim3(kPrepBlocksX + 2 * kPrepBlocksW), dim3(256), 0, s, pa);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "measured prep launch");
+    FwdArgs fa{};
+    fa.xrec = reinterpret_cast<const float2*>(ws + p.off_xrec);
+    fa.wsT = reinterpret_cast<const float2*>(ws + p.off_wsT);
+    fa.lut = table;
+    fa.out = out;
+    fa.M = (int)M;
+    fa.O = (int)O;
+    fa.Kp = (int)p.Kp;
+    fa.Op = (int)p.Op;
+    fa.NP = cb->n_seg * cb->n_rows + 1;
+    fa.n_mt = p.n_mt;
+    fa.n_ot = p.n_ot;
+    fa.out_scale = current_scale;
+    fa.glue = 1;
+    fa.idiff = out_pre;
+    fa.r_tia = r_tia;
+    fa.y_lo = out_min;
+    fa.y_hi = out_max;
+    const size_t lds_bytes = (size_t)fa.NP * 8;
+    const bool lds = lds_bytes <= kMeasuredLdsBytes;
+    ProfiledLaunch* prof;
+    prof_start(s, 0, &prof);
+    if (ids_b)
+        launch_fwd_measured<false>(lds, p.mr, dim3(p.blocks), lds_bytes, s, fa);
+    else
+        launch_fwd_measured<true>(lds, p.mr, dim3(p.blocks), lds_bytes, s, fa);
+    err = hipGetLastError();
+    prof_stop(s, prof);
+    if (err != hipSuccess) return hip_fail(err, "measured forward launch");
+    return 0;
+}
+
+int run_measured_backward(const float* x, const short* ids_a, const short* ids_b, int64_t M, int64_t K, int64_t O,
+                          const isa_ekv_codebook* cb, float current_scale, const float* grad_out,
+                          const float* out_pre,
+                          const float* r_tia, float out_min, float out_max, float* grad_x, void* workspace,
+                          size_t workspace_bytes, hipStream_t s) {
+    if (!grad_x) return 0;
+    hipError_t err;
+    if (M == 0 || K == 0 || O == 0) {
+        zero_fill(grad_x, M * K, s);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "zero fill launch");
+        return 0;
+    }
+    if (!grad_out || !out_pre) return fail(ISA_EKV_EINVAL, "grad_out/out_pre is null");
+    BwdPlan p = plan_backward(M, K, O, 0, true, false, true);
+    const size_t tbytes = measured_table_bytes(cb->n_seg, cb->n_rows);
+    const size_t need = p.bytes + tbytes;
+    if (!workspace || workspace_bytes < need)
+        return fail(ISA_EKV_EINVAL, "backward workspace too small (%zu < %zu bytes)", workspace_bytes, need);
+    char* ws = static_cast<char*>(workspace);
+    CallTimer call_timer(s, 3);
+    float2* table = reinterpret_cast<float2*>(ws + p.bytes);
+    const MeasuredPrepArgs pa = measured_prep(cb, x, ids_a, ids_b, M, K, O, p.Kp, p.Op, 4,
+                                              reinterpret_cast<float*>(ws + p.off_xrec),
+                                              reinterpret_cast<float2*>(ws + p.off_wsT), table);
+    hipLaunchKernelGGL(measured_prep_kernel, dim3(kPrepBlocksX + 2 * kPrepBlocksW), dim3(256), 0, s, pa);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "measured prep launch");
+    float* col_part = reinterpret_cast<float*>(ws + p.off_glue);
+    float* r_part = col_part + (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) / 4;
+    GlueGradArgs ga{grad_out, out_pre, M, O, p.Op, r_tia, out_min, out_max, nullptr,
+                    reinterpret_cast<float*>(ws + p.off_gpad), col_part, r_part};
+    hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks), dim3(256), 0, s, ga);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "measured grad prep launch");
+    const int np = cb->n_seg * cb->n_rows + 1;
+    const bool lds = (size_t)np * 8 <= kMeasuredBwdLdsTableBytes;
+    BwdArgs ba{};
+    ba.xrec = reinterpret_cast<const float4*>(ws + p.off_xrec);
+    ba.wsT = reinterpret_cast<const float2*>(ws + p.off_wsT);
+    ba.grad = reinterpret_cast<const float*>(ws + p.off_gpad);
+    ba.lut = reinterpret_cast<const float4*>(table);
+    ba.dx_part = reinterpret_cast<float*>(ws + p.off_dx);
+    ba.M = (int)M;
+    ba.K = (int)K;
+    ba.O = (int)O;
+    ba.Kp = (int)p.Kp;
+    ba.Op = (int)p.Op;
+    ba.ldg = (int)p.Op;
+    ba.NP = np;
+    ba.n_ob = p.n_ob;
+    ba.n_kb = p.n_kb;
+    ba.n_split = p.n_split;
+    ba.m_chunk = p.m_chunk;
+    ba.n_items = p.n_items;
+    const size_t lds_bytes = (lds ? round_up((int64_t)np * 8, 16) : 0) + p.lds_bytes;
+    const dim3 grid(p.blocks), block(p.waves_per_block * 64);
+    ProfiledLaunch* prof;
+    prof_start(s, 1, &prof);
+    if (ids_b) {
+        if (lds) hipLaunchKernelGGL((bwd_measured_kernel<false, true>), grid, block, lds_bytes, s, ba);
+        else hipLaunchKernelGGL((bwd_measured_kernel<false, false>), grid, block, lds_bytes, s, ba);
+    } else {
+        if (lds) hipLaunchKernelGGL((bwd_measured_kernel<true, true>), grid, block, lds_bytes, s, ba);
+        else hipLaunchKernelGGL((bwd_measured_kernel<true, false>), grid, block, lds_bytes, s, ba);
+    }
+    err = hipGetLastError();
+    prof_stop(s, prof);
+    if (err != hipSuccess) return hip_fail(err, "measured backward launch");
+    hipLaunchKernelGGL(dx_reduce_kernel, dim3(kDxReduceBlocks), dim3(256), 0, s,
+                       reinterpret_cast<const float*>(ws + p.off_dx), p.n_ob, M * K, current_scale, grad_x, x,
+                       static_cast<const float*>(nullptr), cb->lookup_min, cb->lookup_max,
+                       static_cast<float2*>(nullptr), 1);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
+    return 0;
+}
 }  // namespace
 
 // ----------------------------------------------------------------------------------
@@ -1920,6 +2321,48 @@ int isa_ekv_layer_backward(const float* x, const float* vth_pos, const float* vt
     return run_backward(lut_setup(lut_bwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, grad_out, M, K,
                         O, v_sat, grad_x, grad_vth_pos, grad_vth_neg, workspace, workspace_bytes,
                         static_cast<hipStream_t>(stream), glue, idiff, glue_grads);
+}
+
+size_t isa_ekv_measured_forward_workspace(int64_t M, int64_t K, int64_t O, int n_seg, int n_rows) {
+    if (M < 0 || K < 0 || O < 0 || n_seg < 1 || n_rows < 1) return 0;
+    return plan_forward(M, K, O, false).bytes + measured_table_bytes(n_seg, n_rows);
+}
+
+size_t isa_ekv_measured_backward_workspace(int64_t M, int64_t K, int64_t O, int n_seg, int n_rows) {
+    if (M < 0 || K < 0 || O < 0 || n_seg < 1 || n_rows < 1) return 0;
+    return plan_backward(M, K, O, 0, true, false, true).bytes + measured_table_bytes(n_seg, n_rows);
+}
+
+int isa_ekv_measured_forward(const float* x, const int16_t* ids_a, const int16_t* ids_b, int64_t M, int64_t K,
+                             int64_t O, const isa_ekv_codebook* codebook, float current_scale, const float* r_tia,
+                             float out_min, float out_max, float* out_pre, float* out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    int rc = check_codebook(codebook, reinterpret_cast<const short*>(ids_a));
+    if (rc) return rc;
+    // the id arrays stand where the threshold arrays are checked
+    rc = check_shapes(x, reinterpret_cast<const float*>(ids_a), reinterpret_cast<const float*>(ids_a), M, K, O, 1.0f);
+    if (rc) return rc;
+    if (!r_tia) return fail(ISA_EKV_EINVAL, "r_tia is null");
+    if (!(out_max >= out_min)) return fail(ISA_EKV_EINVAL, "output range needs out_max >= out_min");
+    return run_measured_forward(x, reinterpret_cast<const short*>(ids_a), reinterpret_cast<const short*>(ids_b), M,
+                                K, O, codebook, current_scale, r_tia, out_min, out_max, out_pre, out, workspace,
+                                workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int isa_ekv_measured_backward(const float* x, const int16_t* ids_a, const int16_t* ids_b, int64_t M, int64_t K,
+                              int64_t O, const isa_ekv_codebook* codebook, float current_scale,
+                              const float* grad_out, const float* out_pre, const float* r_tia, float out_min,
+                              float out_max, float* grad_x, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_codebook(codebook, reinterpret_cast<const short*>(ids_a));
+    if (rc) return rc;
+    // the id arrays stand where the threshold arrays are checked
+    rc = check_shapes(x, reinterpret_cast<const float*>(ids_a), reinterpret_cast<const float*>(ids_a), M, K, O, 1.0f);
+    if (rc) return rc;
+    if (!r_tia) return fail(ISA_EKV_EINVAL, "r_tia is null");
+    if (!(out_max >= out_min)) return fail(ISA_EKV_EINVAL, "output range needs out_max >= out_min");
+    return run_measured_backward(x, reinterpret_cast<const short*>(ids_a), reinterpret_cast<const short*>(ids_b), M,
+                                 K, O, codebook, current_scale, grad_out, out_pre, r_tia, out_min, out_max, grad_x,
+                                 workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -41,6 +41,10 @@ EXPORTS = (
     "isa_ekv_layer_backward_workspace",
     "isa_ekv_layer_forward",
     "isa_ekv_layer_backward",
+    "isa_ekv_measured_forward_workspace",
+    "isa_ekv_measured_backward_workspace",
+    "isa_ekv_measured_forward",
+    "isa_ekv_measured_backward",
     "isa_ekv_profile_begin",
     "isa_ekv_profile_end",
 )
@@ -65,6 +69,28 @@ class Glue(ctypes.Structure):
         ("y_hi", ctypes.c_float),
         ("adc_scale", ctypes.c_void_p),
         ("adc_shift", ctypes.c_void_p),
+    ]
+
+
+SEG_UNIFORM = 0
+SEG_SEARCH = 1
+SEG_ROUND = 2
+
+
+class Codebook(ctypes.Structure):
+    """isa_ekv_codebook: measured-curve tables (device pointers) and the segment rule."""
+
+    _fields_ = [
+        ("slopes", ctypes.c_void_p),
+        ("intercepts", ctypes.c_void_p),
+        ("n_seg", ctypes.c_int),
+        ("n_rows", ctypes.c_int),
+        ("seg_mode", ctypes.c_int),
+        ("vg", ctypes.c_void_p),
+        ("voltage_min", ctypes.c_float),
+        ("inverse_step", ctypes.c_float),
+        ("lookup_min", ctypes.c_float),
+        ("lookup_max", ctypes.c_float),
     ]
 
 
@@ -125,6 +151,16 @@ def _declare(lib) -> None:
     lib.isa_ekv_layer_backward.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32,
                                            ctypes.POINTER(Glue), vp, vp, vp, ctypes.POINTER(GlueGrads), vp, sz, vp]
     lib.isa_ekv_layer_backward.restype = ci
+    lib.isa_ekv_measured_forward_workspace.argtypes = [i64, i64, i64, ci, ci]
+    lib.isa_ekv_measured_forward_workspace.restype = sz
+    lib.isa_ekv_measured_backward_workspace.argtypes = [i64, i64, i64, ci, ci]
+    lib.isa_ekv_measured_backward_workspace.restype = sz
+    lib.isa_ekv_measured_forward.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.POINTER(Codebook), f32, vp, f32, f32,
+                                             vp, vp, vp, sz, vp]
+    lib.isa_ekv_measured_forward.restype = ci
+    lib.isa_ekv_measured_backward.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.POINTER(Codebook), f32, vp, vp, vp,
+                                              f32, f32, vp, vp, sz, vp]
+    lib.isa_ekv_measured_backward.restype = ci
     lib.isa_ekv_profile_begin.argtypes = []
     lib.isa_ekv_profile_begin.restype = ci
     lib.isa_ekv_profile_end.argtypes = [ctypes.POINTER(f64), ctypes.POINTER(ci)]

@@ -303,3 +303,101 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
     if not need_grad_x:
         res["dx"] = None
     return res
+
+
+def _ids16(t: torch.Tensor, name: str, shape, device) -> torch.Tensor:
+    _require_cuda(t, name)
+    if tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if t.device != device:
+        raise RuntimeError(f"{name} must be on {device}")
+    return t.to(dtype=torch.int16).contiguous()
+
+
+def _codebook(slopes, intercepts, seg_mode, vg, voltage_min, inverse_step, lookup_min, lookup_max, device):
+    for t, name in ((slopes, "slopes"), (intercepts, "intercepts")):
+        _require_cuda(t, name)
+        if t.device != device:
+            raise RuntimeError(f"{name} must be on {device}")
+    if slopes.dim() != 2 or intercepts.shape != slopes.shape:
+        raise RuntimeError("slope/intercept tables must have matching 2-D shapes [curves, segments]")
+    if slopes.shape[0] > 32767:
+        raise RuntimeError("the codebook holds at most 32767 curves (int16 state ids)")
+    sl, ic = as_kernel_f32(slopes), as_kernel_f32(intercepts)
+    v = None
+    if seg_mode == _hip.SEG_SEARCH:
+        v = as_kernel_f32(vg.reshape(-1))
+        if v.numel() != sl.shape[1] + 1:
+            raise RuntimeError("vg must have one more point than the tables have segments")
+    cb = _hip.Codebook()
+    cb.slopes, cb.intercepts = sl.data_ptr(), ic.data_ptr()
+    cb.n_seg, cb.n_rows = int(sl.shape[1]), int(sl.shape[0])
+    cb.seg_mode = int(seg_mode)
+    cb.vg = _ptr(v)
+    cb.voltage_min, cb.inverse_step = float(voltage_min), float(inverse_step)
+    cb.lookup_min, cb.lookup_max = float(lookup_min), float(lookup_max)
+    return cb, (sl, ic, v)  # keep the tensors alive for the call
+
+
+def measured_forward(x: torch.Tensor, ids_a: torch.Tensor, ids_b: Optional[torch.Tensor], slopes: torch.Tensor,
+                     intercepts: torch.Tensor, *, seg_mode: int, vg: Optional[torch.Tensor] = None,
+                     voltage_min: float = 0.0, inverse_step: float = 1.0, lookup_min: float = 0.0,
+                     lookup_max: float = 4.0, current_scale: float = 1.0, r_tia: torch.Tensor,
+                     out_min: float = -4.0, out_max: float = 4.0):
+    """(out, out_pre) of the measured-codebook projection, fp32 [M, O]."""
+    lib = _hip.load()
+    _require_cuda(x, "x")
+    if x.dim() != 2:
+        raise RuntimeError(f"x must be 2-D [M, K], got shape {tuple(x.shape)}")
+    dev = x.device
+    M, K = int(x.shape[0]), int(x.shape[1])
+    if ids_a.dim() != 2 or ids_a.shape[1] != K:
+        raise RuntimeError(f"ids_a must be [O, {K}], got {tuple(ids_a.shape)}")
+    O = int(ids_a.shape[0])
+    a16 = _ids16(ids_a, "ids_a", (O, K), dev)
+    b16 = None if ids_b is None else _ids16(ids_b, "ids_b", (O, K), dev)
+    cb, keep = _codebook(slopes, intercepts, seg_mode, vg, voltage_min, inverse_step, lookup_min, lookup_max, dev)
+    r = _glue_operand(r_tia, 1, "r_tia", dev)
+    out = torch.empty((M, O), dtype=torch.float32, device=dev)
+    pre = torch.empty((M, O), dtype=torch.float32, device=dev)
+    if M == 0 or O == 0:
+        return out, pre
+    x32 = as_kernel_f32(x)
+    ws = _workspace(lib.isa_ekv_measured_forward_workspace(M, K, O, cb.n_seg, cb.n_rows), dev)
+    with torch.cuda.device(dev):
+        rc = lib.isa_ekv_measured_forward(_ptr(x32), a16.data_ptr(), _ptr(b16), M, K, O, ctypes.byref(cb),
+                                          float(current_scale), r.data_ptr(), float(out_min), float(out_max),
+                                          pre.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          _hip.stream_handle(dev))
+    _hip.check(rc, "isa_ekv_measured_forward")
+    del keep
+    return out, pre
+
+
+def measured_backward(x: torch.Tensor, ids_a: torch.Tensor, ids_b: Optional[torch.Tensor], slopes: torch.Tensor,
+                      intercepts: torch.Tensor, grad_out: torch.Tensor, out_pre: torch.Tensor, *, seg_mode: int,
+                      vg: Optional[torch.Tensor] = None, voltage_min: float = 0.0, inverse_step: float = 1.0,
+                      lookup_min: float = 0.0, lookup_max: float = 4.0, current_scale: float = 1.0,
+                      r_tia: torch.Tensor, out_min: float = -4.0, out_max: float = 4.0) -> torch.Tensor:
+    """dX [M, K] fp32 of the measured-codebook projection's output."""
+    lib = _hip.load()
+    dev = x.device
+    M, K = int(x.shape[0]), int(x.shape[1])
+    O = int(ids_a.shape[0])
+    a16 = _ids16(ids_a, "ids_a", (O, K), dev)
+    b16 = None if ids_b is None else _ids16(ids_b, "ids_b", (O, K), dev)
+    if tuple(grad_out.shape) != (M, O) or tuple(out_pre.shape) != (M, O):
+        raise RuntimeError(f"grad_out and out_pre must be [{M}, {O}]")
+    cb, keep = _codebook(slopes, intercepts, seg_mode, vg, voltage_min, inverse_step, lookup_min, lookup_max, dev)
+    r = _glue_operand(r_tia, 1, "r_tia", dev)
+    gx = torch.empty((M, K), dtype=torch.float32, device=dev)
+    x32, g32, p32 = as_kernel_f32(x), as_kernel_f32(grad_out), as_kernel_f32(out_pre)
+    ws = _workspace(lib.isa_ekv_measured_backward_workspace(M, K, O, cb.n_seg, cb.n_rows), dev)
+    with torch.cuda.device(dev):
+        rc = lib.isa_ekv_measured_backward(_ptr(x32), a16.data_ptr(), _ptr(b16), M, K, O, ctypes.byref(cb),
+                                           float(current_scale), _ptr(g32), _ptr(p32), r.data_ptr(),
+                                           float(out_min), float(out_max), gx.data_ptr(), ws.data_ptr(), ws.numel(),
+                                           _hip.stream_handle(dev))
+    _hip.check(rc, "isa_ekv_measured_backward")
+    del keep
+    return gx

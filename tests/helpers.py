@@ -60,3 +60,22 @@ def oracle_all(x, vp, vn, grad, cfg, out_min=-4.0, out_max=4.0):
 def errs(actual: torch.Tensor, expected: np.ndarray):
     a = actual.detach().double().cpu().numpy()
     return oracle.normwise_error(a, expected), oracle.elementwise_error(a, expected, 1e-3)
+
+
+def make_codebook(n_states: int = 24, n_points: int = 61, lo: float = 0.0, hi: float = 4.0, seed: int = 0,
+                  uniform: bool = True):
+    """Synthetic measured I-V codebook: vg [n_points] (uniform, or strictly increasing with
+    jittered steps) and monotone curves [n_states, n_points] in amperes (EKV-like turn-on
+    at state-dependent thresholds, nA to uA), fp32 CPU tensors."""
+    g = torch.Generator().manual_seed(seed)
+    if uniform:
+        vg = torch.linspace(lo, hi, n_points)
+    else:
+        steps = torch.rand(n_points - 1, generator=g) + 0.5
+        vg = torch.cat([torch.zeros(1), torch.cumsum(steps, 0)])
+        vg = (lo + (hi - lo) * vg / vg[-1]).float()
+    vt = torch.linspace(0.4, 3.6, n_states)[torch.randperm(n_states, generator=g)]
+    slope = 0.08 + 0.04 * torch.rand(n_states, generator=g)
+    sp = torch.nn.functional.softplus((vg[None, :] - vt[:, None]) / slope[:, None])
+    currents = (2e-9 * sp * sp + 4e-10).float()
+    return vg.float(), currents

@@ -159,6 +159,35 @@ def test_layer_entry_points_reject_bad_glue_before_launch():
         lib.isa_ekv_backward_workspace(64, 96, 256, 4096, 1, 1)
 
 
+def test_measured_entry_points_reject_bad_codebooks_before_launch():
+    lib = _hip.load()
+    fake = ctypes.c_void_p(16)
+
+    def fwd(cb, r=fake, ids=fake):
+        return lib.isa_ekv_measured_forward(fake, ids, None, 4, 4, 4, cb, 1.0, r, -4.0, 4.0, fake, fake, fake, 0,
+                                            None)
+
+    assert fwd(None) == -1 and "codebook is null" in _err(lib)
+    cb = _hip.Codebook()
+    assert fwd(ctypes.byref(cb)) == -1 and "n_seg" in _err(lib)
+    cb.n_seg, cb.n_rows = 60, 24
+    assert fwd(ctypes.byref(cb)) == -1 and "slopes" in _err(lib)
+    cb.slopes = cb.intercepts = 16
+    cb.seg_mode = 7
+    assert fwd(ctypes.byref(cb)) == -1 and "segment mode" in _err(lib)
+    cb.seg_mode = _hip.SEG_SEARCH
+    assert fwd(ctypes.byref(cb)) == -1 and "vg" in _err(lib)
+    cb.seg_mode, cb.lookup_min, cb.lookup_max = _hip.SEG_UNIFORM, 0.0, 4.0
+    assert fwd(ctypes.byref(cb), ids=None) == -1 and "ids_a" in _err(lib)
+    assert fwd(ctypes.byref(cb), r=None) == -1 and "r_tia" in _err(lib)
+    assert fwd(ctypes.byref(cb)) == -1 and "workspace too small" in _err(lib)
+    assert lib.isa_ekv_measured_forward_workspace(8, 8, 8, 60, 24) > lib.isa_ekv_forward_workspace(8, 8, 8)
+    assert lib.isa_ekv_measured_backward_workspace(8, 8, 8, 0, 24) == 0
+    rc = lib.isa_ekv_measured_backward(fake, fake, None, 4, 4, 4, ctypes.byref(cb), 1.0, fake, fake, fake, -4.0, 4.0,
+                                       None, fake, 0, None)
+    assert rc == 0  # no grad_x requested: nothing to do
+
+
 def test_lut_build_and_pack_reject_bad_arguments():
     lib = _hip.load()
     params = (ctypes.c_double * 4)(4.136, 0.0259, 7.5875e-7, 0.1)
