@@ -40,6 +40,7 @@
 
 #include <type_traits>
 
+#include <algorithm>
 #include <cmath>
 #include <math.h>
 #include <stdarg.h>
@@ -97,6 +98,7 @@ constexpr int kSplitRecords = 4096 + 2 * kPad;
 
 __host__ __device__ inline int lut_records(int n) { return n + 2 * kPad; }
 constexpr int kLdsBytes = 160 * 1024;
+constexpr int64_t kCUs = 256;  // MI355X compute units (a fixed plan input: workspace sizes must not depend on the device)
 
 thread_local char g_last_error[512] = "";
 
@@ -1484,14 +1486,26 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     while (wpb > 1 && lut_bytes + wpb * red_bytes > (size_t)kLdsBytes) wpb /= 2;
     p.waves_per_block = wpb;
     p.lds_bytes = lut_bytes + (size_t)wpb * red_bytes;
-    // token splits: enough wave items to cover the chip several times over
+    // Token splits. One block runs per CU at a time (the LDS table), and blocks of equal
+    // work finish together, so the launch takes ceil(blocks / CUs) rounds. Among the split
+    // counts from ~2 rounds up, take the smallest whose block count fills its rounds to
+    // within 2% of the best fill (each split adds a dVth partial plane and per-item setup).
     const int64_t base_items = (int64_t)p.n_ob * p.n_kb;
-    const int64_t target = 3 * 256 * 16;
-    int64_t splits = (target + base_items - 1) / base_items;
-    const int64_t max_splits = (M + 63) / 64;  // keep at least 64 tokens per split
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-    p.m_chunk = (int)round_up((M + splits - 1) / splits, kBwdMB);
+    const int64_t max_splits = (M + 63) / 64 > 0 ? (M + 63) / 64 : 1;  // >= 64 tokens per split
+    const int64_t min_splits = std::min<int64_t>(max_splits, (2 * kCUs * wpb + base_items - 1) / base_items);
+    const int64_t top_splits = std::min<int64_t>(max_splits, 4 * min_splits + 8);
+    auto fill_of = [&](int64_t sp) {
+        const int64_t chunk = round_up((M + sp - 1) / sp, kBwdMB);
+        const int64_t n_sp = (M + chunk - 1) / chunk;
+        const int64_t blocks = (base_items * n_sp + wpb - 1) / wpb;
+        const int64_t rounds = (blocks + kCUs - 1) / kCUs;
+        return (double)blocks / (double)(rounds * kCUs);
+    };
+    double best_fill = 0.0;
+    for (int64_t sp = min_splits; sp <= top_splits; ++sp) best_fill = std::max(best_fill, fill_of(sp));
+    int64_t best_splits = min_splits;
+    while (best_splits < top_splits && fill_of(best_splits) < best_fill - 0.02) ++best_splits;
+    p.m_chunk = (int)round_up((M + best_splits - 1) / best_splits, kBwdMB);
     if (p.m_chunk < kBwdMB) p.m_chunk = kBwdMB;
     p.n_split = (int)((M + p.m_chunk - 1) / p.m_chunk);
     if (p.n_split < 1) p.n_split = 1;
