@@ -1489,7 +1489,8 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     // Token splits. One block runs per CU at a time (the LDS table), and blocks of equal
     // work finish together, so the launch takes ceil(blocks / CUs) rounds. Among the split
     // counts from ~2 rounds up, take the smallest whose block count fills its rounds to
-    // within 2% of the best fill (each split adds a dVth partial plane and per-item setup).
+    // within 0.5% of the best fill (each split adds a dVth partial plane and per-item
+    // setup, measured at well under the 1.6% a 98.4%-filled last round costs).
     const int64_t base_items = (int64_t)p.n_ob * p.n_kb;
     const int64_t max_splits = (M + 63) / 64 > 0 ? (M + 63) / 64 : 1;  // >= 64 tokens per split
     const int64_t min_splits = std::min<int64_t>(max_splits, (2 * kCUs * wpb + base_items - 1) / base_items);
@@ -1504,7 +1505,7 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     double best_fill = 0.0;
     for (int64_t sp = min_splits; sp <= top_splits; ++sp) best_fill = std::max(best_fill, fill_of(sp));
     int64_t best_splits = min_splits;
-    while (best_splits < top_splits && fill_of(best_splits) < best_fill - 0.02) ++best_splits;
+    while (best_splits < top_splits && fill_of(best_splits) < best_fill - 0.005) ++best_splits;
     p.m_chunk = (int)round_up((M + best_splits - 1) / best_splits, kBwdMB);
     if (p.m_chunk < kBwdMB) p.m_chunk = kBwdMB;
     p.n_split = (int)((M + p.m_chunk - 1) / p.m_chunk);
