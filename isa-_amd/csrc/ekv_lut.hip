@@ -1249,23 +1249,45 @@ __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict_
     const float aff_s = in_affine ? in_affine[0] : 1.0f;
     const float aff_b = in_affine ? in_affine[1] : 0.0f;
     float ds = 0.0f, db = 0.0f;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
-         e += (int64_t)gridDim.x * blockDim.x) {
-        float s = part[e];
-        for (int b = 1; b < n_ob; ++b) s += part[(size_t)b * n + e];
+    auto finish = [&](float s, float xv) {
         s *= scale;
         if (range_mask) {
-            const float xv = x[e];
             s = (xv >= in_lo && xv <= in_hi) ? s : 0.0f;
         } else if (in_affine) {
-            const float xv = x[e];
             const float pre = mapped_pre(xv, aff_s, aff_b);
             const float g = (pre >= in_lo && pre <= in_hi) ? s : 0.0f;
             ds = fmaf(g, xv, ds);
             db += g;
             s = g * aff_s;
         }
-        dx[e] = s;
+        return s;
+    };
+    const bool need_x = range_mask || in_affine;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const bool vec4 = (n & 3) == 0 && (((uintptr_t)part | (uintptr_t)dx) & 15) == 0 &&
+                      (!need_x || ((uintptr_t)x & 15) == 0);
+    if (vec4) {  // 16-byte vectors
+        const int64_t n4 = n >> 2;
+        const float4* p4 = reinterpret_cast<const float4*>(part);
+        for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n4; e += stride) {
+            float4 s = p4[e];
+            for (int b = 1; b < n_ob; ++b) {
+                const float4 v = p4[(size_t)b * n4 + e];
+                s.x += v.x;
+                s.y += v.y;
+                s.z += v.z;
+                s.w += v.w;
+            }
+            const float4 xv = need_x ? reinterpret_cast<const float4*>(x)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+            reinterpret_cast<float4*>(dx)[e] =
+                make_float4(finish(s.x, xv.x), finish(s.y, xv.y), finish(s.z, xv.z), finish(s.w, xv.w));
+        }
+    } else {
+        for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride) {
+            float s = part[e];
+            for (int b = 1; b < n_ob; ++b) s += part[(size_t)b * n + e];
+            dx[e] = finish(s, need_x ? x[e] : 0.0f);
+        }
     }
     if (in_affine) {
         __shared__ float s_ds[4], s_db[4];
@@ -1285,36 +1307,46 @@ __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict_
     }
 }
 
-// dVth+[o,k] = -scale * sum_s P[s][0][k][o], dVth-[o,k] = +scale * sum_s P[s][1][k][o];
-// 32x32 transpose tiles
+// dVth+[o,k] = -scale * sum_s P[s][0][k][o], dVth-[o,k] = +scale * sum_s P[s][1][k][o]
+// (splits summed in order s = 0, 1, ...). Tiles of 64 outputs x 32 inputs: 16-byte loads
+// along o (a wave reads four 256-byte row segments per plane and split), transposed through
+// LDS, stores along k.
 __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict__ part, int n_split,
                                                         int K, int O, int Kp, int Op, float scale,
                                                         float* __restrict__ dvp, float* __restrict__ dvn) {
-    __shared__ float tile[2][32][33];
-    const int n_ot = (O + 31) / 32, n_kt = (K + 31) / 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    __shared__ float tile[2][32][65];
+    const int n_ot = (O + 63) / 64, n_kt = (K + 31) / 32;
+    const int t = threadIdx.x;
+    const int c4 = t & 15, row = t >> 4;  // loads: 16 float4 columns x 16 rows
+    const int kl = t & 31, orow = t >> 5;  // stores: 32 inputs x 8 output rows
     const size_t plane = (size_t)Kp * Op;
-    for (int t = blockIdx.x; t < n_ot * n_kt; t += gridDim.x) {
-        const int ot = t % n_ot, kt = t / n_ot;
-        for (int rr = ty; rr < 32; rr += 8) {
-            const int k = kt * 32 + rr, o = ot * 32 + tx;
-            float sp = 0.0f, sn = 0.0f;
-            if (k < K && o < O) {
-                const size_t e = (size_t)k * Op + o;
-                for (int s = 0; s < n_split; ++s) {
-                    sp += part[(size_t)s * 2 * plane + e];
-                    sn += part[(size_t)s * 2 * plane + plane + e];
+    for (int tile_id = blockIdx.x; tile_id < n_ot * n_kt; tile_id += gridDim.x) {
+        const int ot = tile_id % n_ot, kt = tile_id / n_ot;
+        for (int rr = row; rr < 32; rr += 16) {
+            const int k = kt * 32 + rr;
+            float4 sp = make_float4(0.f, 0.f, 0.f, 0.f), sn = sp;
+            if (k < K) {  // ot * 64 + 63 < Op: Op is O rounded up to 256
+                const float4* src = reinterpret_cast<const float4*>(part + (size_t)k * Op + ot * 64 + c4 * 4);
+                const size_t plane4 = plane / 4;
+#pragma unroll 4
+                for (int sidx = 0; sidx < n_split; ++sidx) {
+                    const float4 a = src[(size_t)sidx * 2 * plane4];
+                    const float4 b = src[(size_t)sidx * 2 * plane4 + plane4];
+                    sp.x += a.x; sp.y += a.y; sp.z += a.z; sp.w += a.w;
+                    sn.x += b.x; sn.y += b.y; sn.z += b.z; sn.w += b.w;
                 }
             }
-            tile[0][rr][tx] = -sp * scale;
-            tile[1][rr][tx] = sn * scale;
+            float* tp = &tile[0][rr][c4 * 4];
+            float* tn = &tile[1][rr][c4 * 4];
+            tp[0] = -sp.x * scale; tp[1] = -sp.y * scale; tp[2] = -sp.z * scale; tp[3] = -sp.w * scale;
+            tn[0] = sn.x * scale; tn[1] = sn.y * scale; tn[2] = sn.z * scale; tn[3] = sn.w * scale;
         }
         __syncthreads();
-        for (int rr = ty; rr < 32; rr += 8) {
-            const int o = ot * 32 + rr, k = kt * 32 + tx;
+        for (int orr = orow; orr < 64; orr += 8) {
+            const int o = ot * 64 + orr, k = kt * 32 + kl;
             if (o < O && k < K) {
-                dvp[(size_t)o * K + k] = tile[0][tx][rr];
-                dvn[(size_t)o * K + k] = tile[1][tx][rr];
+                dvp[(size_t)o * K + k] = tile[0][kl][orr];
+                dvn[(size_t)o * K + k] = tile[1][kl][orr];
             }
         }
         __syncthreads();
@@ -1328,12 +1360,14 @@ __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict_
 //   y0 = idiff * r_tia, mask = lo <= y0 <= hi    (torch.clamp's backward mask)
 //   G_eff[m, o] = mask * gy * r_tia               (the CIM backward's upstream gradient)
 //   d r_tia   += mask * gy * idiff,   d adc_scale[o] += G * clamp(y0),   d adc_shift[o] += G
-// Blocks own fixed row sets; per-block partials are combined in block order by
-// glue_reduce_kernel, so every result is reproducible. G_eff is written [M][Op] with zeros
-// in the padded outputs.
+// A block owns a contiguous row range (one of kGlueBlocks) and 256 padded outputs (one of
+// Op / 256): 4 row lanes x 64 output lanes, each thread 4 outputs 64 apart so every load
+// instruction of a wave reads 64 consecutive floats. Per-block partials are combined in
+// block order by glue_reduce_kernel, so every result is reproducible. G_eff is written
+// [M][Op] with zeros in the padded outputs.
 // ----------------------------------------------------------------------------------
 
-constexpr int kGlueBlocks = 256;
+constexpr int kGlueBlocks = 256;  // row ranges
 
 struct GlueGradArgs {
     const float* g;          // [M][O]
@@ -1344,80 +1378,128 @@ struct GlueGradArgs {
     const float* adc_scale;  // [O] or null
     float* geff;             // [M][Op]
     float* col_part;         // [kGlueBlocks][2][Op] (d adc_scale, d adc_shift)
-    float* r_part;           // [kGlueBlocks]
+    float* r_part;           // [kGlueBlocks * (Op / 256)]
 };
 
 __global__ __launch_bounds__(256) void glue_grad_kernel(GlueGradArgs a) {
     const bool has_r = a.r_tia != nullptr;
     const float r = has_r ? *a.r_tia : 1.0f;
+    const int rg = blockIdx.x, ob = blockIdx.y;
+    const int lane_o = threadIdx.x & 63, row_lane = threadIdx.x >> 6;
+    const int64_t rows = (a.M + kGlueBlocks - 1) / kGlueBlocks;
+    const int64_t m_begin = (int64_t)rg * rows, m_end = m_begin + rows < a.M ? m_begin + rows : a.M;
+    float da[4] = {0.0f, 0.0f, 0.0f, 0.0f}, dc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, as[4];
+    int64_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        o[c] = (int64_t)ob * 256 + c * 64 + lane_o;
+        as[c] = (a.adc_scale && o[c] < a.O) ? a.adc_scale[o[c]] : 1.0f;
+    }
     float racc = 0.0f;
-    for (int64_t o = threadIdx.x; o < a.Op; o += blockDim.x) {
-        float da = 0.0f, dc = 0.0f;
-        const float as = (a.adc_scale && o < a.O) ? a.adc_scale[o] : 1.0f;
-        for (int64_t m = blockIdx.x; m < a.M; m += gridDim.x) {
+    for (int64_t m = m_begin + row_lane; m < m_end; m += 4) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
             float ge = 0.0f;
-            if (o < a.O) {
-                const float gz = a.g[m * a.O + o];
-                const float id = a.idiff[m * a.O + o];
+            if (o[c] < a.O) {
+                const float gz = a.g[m * a.O + o[c]];
+                const float id = a.idiff[m * a.O + o[c]];
                 const float y0 = id * r;
                 const bool pass = !has_r || (y0 >= a.y_lo && y0 <= a.y_hi);
                 if (a.adc_scale) {
                     const float y = !has_r ? id : (y0 != y0 ? y0 : fminf(fmaxf(y0, a.y_lo), a.y_hi));
-                    da = fmaf(gz, y, da);
-                    dc += gz;
+                    da[c] = fmaf(gz, y, da[c]);
+                    dc[c] += gz;
                 }
-                const float gy = a.adc_scale ? gz * as : gz;
+                const float gy = a.adc_scale ? gz * as[c] : gz;
                 const float gm = pass ? gy : 0.0f;
                 racc = fmaf(gm, id, racc);
                 ge = gm * r;
             }
-            a.geff[m * a.Op + o] = ge;
-        }
-        if (a.adc_scale) {
-            a.col_part[(size_t)blockIdx.x * 2 * a.Op + o] = da;
-            a.col_part[(size_t)blockIdx.x * 2 * a.Op + a.Op + o] = dc;
+            a.geff[m * a.Op + o[c]] = ge;
         }
     }
-    if (has_r) {
-        __shared__ float s_r[4];
-        for (int off = 32; off > 0; off >>= 1) racc += __shfl_xor(racc, off);
-        if ((threadIdx.x & 63) == 0) s_r[threadIdx.x >> 6] = racc;
-        __syncthreads();
-        if (threadIdx.x == 0) a.r_part[blockIdx.x] = (s_r[0] + s_r[1]) + (s_r[2] + s_r[3]);
+    __shared__ float s_da[4][256], s_dc[4][256], s_r[4];
+    if (a.adc_scale) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            s_da[row_lane][c * 64 + lane_o] = da[c];
+            s_dc[row_lane][c * 64 + lane_o] = dc[c];
+        }
     }
+    for (int off = 32; off > 0; off >>= 1) racc += __shfl_xor(racc, off);
+    if (lane_o == 0) s_r[row_lane] = racc;
+    __syncthreads();
+    if (a.adc_scale) {
+        const int t = threadIdx.x;  // one output of the block each
+        const float sa = (s_da[0][t] + s_da[1][t]) + (s_da[2][t] + s_da[3][t]);
+        const float sc = (s_dc[0][t] + s_dc[1][t]) + (s_dc[2][t] + s_dc[3][t]);
+        const int64_t oo = (int64_t)ob * 256 + (t & 63) + (t >> 6) * 64;
+        a.col_part[(size_t)rg * 2 * a.Op + oo] = sa;
+        a.col_part[(size_t)rg * 2 * a.Op + a.Op + oo] = sc;
+    }
+    if (has_r && threadIdx.x == 0) a.r_part[(size_t)rg * gridDim.y + ob] = (s_r[0] + s_r[1]) + (s_r[2] + s_r[3]);
 }
 
 // Final sums of the glue partials in fixed order: d adc_scale/shift[o] over glue blocks,
-// d r_tia over glue blocks, d {scale, shift} of the input mapping over dx_reduce blocks.
+// d r_tia over glue blocks and output blocks, d {scale, shift} of the input mapping over
+// dx_reduce blocks. Grid: ceil(O / 64) column blocks (64 outputs x 4 quarters of the glue
+// blocks each, quarters combined in LDS), then one block for the three scalars (strided
+// partial sums per thread, then a tree in LDS).
 __global__ __launch_bounds__(256) void glue_reduce_kernel(const float* __restrict__ col_part,
                                                           const float* __restrict__ r_part,
                                                           const float2* __restrict__ aff_part, int64_t O,
                                                           int64_t Op, float* d_adc_scale, float* d_adc_shift,
                                                           float* d_r_tia, float* d_affine) {
-    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < O; o += (int64_t)gridDim.x * blockDim.x) {
-        if (!d_adc_scale && !d_adc_shift) break;
+    __shared__ float red[3][256];
+    const int t = threadIdx.x;
+    const int64_t n_col_blocks = (O + 63) / 64;
+    if ((int64_t)blockIdx.x < n_col_blocks) {
+        if (!d_adc_scale && !d_adc_shift) return;
+        const int64_t o = (int64_t)blockIdx.x * 64 + (t & 63);
+        constexpr int kQuarter = kGlueBlocks / 4;
+        const int b0 = (t >> 6) * kQuarter;
         float sa = 0.0f, sc = 0.0f;
-        for (int b = 0; b < kGlueBlocks; ++b) {
-            sa += col_part[(size_t)b * 2 * Op + o];
-            sc += col_part[(size_t)b * 2 * Op + Op + o];
-        }
-        if (d_adc_scale) d_adc_scale[o] = sa;
-        if (d_adc_shift) d_adc_shift[o] = sc;
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        if (d_r_tia) {
-            float sr = 0.0f;
-            for (int b = 0; b < kGlueBlocks; ++b) sr += r_part[b];
-            d_r_tia[0] = sr;
-        }
-        if (d_affine) {
-            float ss = 0.0f, sb = 0.0f;
-            for (int b = 0; b < kDxReduceBlocks; ++b) {
-                ss += aff_part[b].x;
-                sb += aff_part[b].y;
+        if (o < O) {
+            for (int b = b0; b < b0 + kQuarter; ++b) {
+                sa += col_part[(size_t)b * 2 * Op + o];
+                sc += col_part[(size_t)b * 2 * Op + Op + o];
             }
-            d_affine[0] = ss;
-            d_affine[1] = sb;
+        }
+        red[0][t] = sa;
+        red[1][t] = sc;
+        __syncthreads();
+        if (t < 64 && o < O) {
+            if (d_adc_scale) d_adc_scale[o] = (red[0][t] + red[0][t + 64]) + (red[0][t + 128] + red[0][t + 192]);
+            if (d_adc_shift) d_adc_shift[o] = (red[1][t] + red[1][t + 64]) + (red[1][t + 128] + red[1][t + 192]);
+        }
+        return;
+    }
+    const int n_rpart = kGlueBlocks * (int)(Op / 256);
+    float sr = 0.0f, ss = 0.0f, sb = 0.0f;
+    if (d_r_tia)
+        for (int b = t; b < n_rpart; b += 256) sr += r_part[b];
+    if (d_affine)
+        for (int b = t; b < kDxReduceBlocks; b += 256) {
+            ss += aff_part[b].x;
+            sb += aff_part[b].y;
+        }
+    red[0][t] = sr;
+    red[1][t] = ss;
+    red[2][t] = sb;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w) {
+            red[0][t] += red[0][t + w];
+            red[1][t] += red[1][t + w];
+            red[2][t] += red[2][t + w];
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        if (d_r_tia) d_r_tia[0] = red[0][0];
+        if (d_affine) {
+            d_affine[0] = red[1][0];
+            d_affine[1] = red[2][0];
         }
     }
 }
@@ -1532,9 +1614,10 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     if (need_x) off += (size_t)round_up((int64_t)p.n_ob * M * (K > 0 ? K : 1) * 4, 256);
     p.off_dv = off;
     if (need_w) off += (size_t)round_up((int64_t)p.n_split * 2 * p.Kp * p.Op * 4, 256);
-    p.off_glue = off;  // col_part [kGlueBlocks][2][Op], r_part [kGlueBlocks], aff_part [kDxReduceBlocks]
+    p.off_glue = off;  // col_part [kGlueBlocks][2][Op], r_part [kGlueBlocks][Op/256], aff_part [kDxReduceBlocks]
     if (glue)
-        off += (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) + round_up(kGlueBlocks * 4, 256) +
+        off += (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) +
+               (size_t)round_up((int64_t)kGlueBlocks * (p.Op / 256) * 4, 256) +
                (size_t)round_up(kDxReduceBlocks * 8, 256);
     p.bytes = round_up((int64_t)off, 256);
     return p;
@@ -1817,17 +1900,18 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     CallTimer call_timer(s, 3);
     float* col_part = reinterpret_cast<float*>(ws + p.off_glue);
     float* r_part = col_part + (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) / 4;
-    float2* aff_part = reinterpret_cast<float2*>(r_part + (size_t)round_up(kGlueBlocks * 4, 256) / 4);
+    float2* aff_part =
+        reinterpret_cast<float2*>(r_part + (size_t)round_up((int64_t)kGlueBlocks * (p.Op / 256) * 4, 256) / 4);
     if (glue) {
         GlueGradArgs ga{grad_out, idiff, M, O, p.Op, glue->r_tia, glue->y_lo, glue->y_hi, glue->adc_scale,
                         reinterpret_cast<float*>(ws + p.off_gpad), col_part, r_part};
-        hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks), dim3(256), 0, s, ga);
+        hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks, (unsigned)(p.Op / 256)), dim3(256), 0, s, ga);
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "glue grad launch");
         if (K == 0) {  // nothing reaches x or the thresholds
             if (gg) zero_fill(gg->in_affine, 2, s);
             if (gg && (gg->r_tia || gg->adc_scale || gg->adc_shift))
-                hipLaunchKernelGGL(glue_reduce_kernel, dim3((O + 255) / 256), dim3(256), 0, s, col_part, r_part,
+                hipLaunchKernelGGL(glue_reduce_kernel, dim3((unsigned)((O + 63) / 64 + 1)), dim3(256), 0, s, col_part, r_part,
                                    aff_part, O, p.Op, gg->adc_scale, gg->adc_shift, gg->r_tia, nullptr);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "glue reduce launch");
@@ -1899,13 +1983,13 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
     }
     if (need_w) {
-        hipLaunchKernelGGL(dv_reduce_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dv),
+        hipLaunchKernelGGL(dv_reduce_kernel, dim3(2048), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dv),
                            p.n_split, (int)K, (int)O, (int)p.Kp, (int)p.Op, scale, grad_vth_pos, grad_vth_neg);
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "dv reduce launch");
     }
     if (need_glue) {
-        hipLaunchKernelGGL(glue_reduce_kernel, dim3((O + 255) / 256), dim3(256), 0, s, col_part, r_part, aff_part, O,
+        hipLaunchKernelGGL(glue_reduce_kernel, dim3((unsigned)((O + 63) / 64 + 1)), dim3(256), 0, s, col_part, r_part, aff_part, O,
                            p.Op, gg->adc_scale, gg->adc_shift, gg->r_tia, gg->in_affine);
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "glue reduce launch");
@@ -2082,7 +2166,7 @@ int run_measured_backward(const float* x, const short* ids_a, const short* ids_b
     float* r_part = col_part + (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) / 4;
     GlueGradArgs ga{grad_out, out_pre, M, O, p.Op, r_tia, out_min, out_max, nullptr,
                     reinterpret_cast<float*>(ws + p.off_gpad), col_part, r_part};
-    hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks), dim3(256), 0, s, ga);
+    hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks, (unsigned)(p.Op / 256)), dim3(256), 0, s, ga);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "measured grad prep launch");
     const int np = cb->n_seg * cb->n_rows + 1;
