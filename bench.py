@@ -298,6 +298,45 @@ def gpt_train_step(args) -> int:
     return 0
 
 
+def lds_roofline(model, cfg: dict, cells_launch: float, fwd_ms: float, bwd_ms: float, dev) -> dict:
+    """The table kernels' second bound: their LDS gathers. Each cell-eval gathers 2 records
+    (forward: the + and - branch, ds_read_b64) or 4 (backward: the I and D halves of both
+    branches, ds_read_b64 each); the 64 lanes of a gather share the token and input, so
+    their indices spread over the window the thresholds of the wave's outputs span,
+    (max - min of vth) / LUT step records. isa_ekv_probe_lds_gather measures the time per
+    random b64 gather at that window on this GPU (bank conflicts included), which gives
+    the kernels' LDS-bound launch times."""
+    import math
+
+    import torch
+
+    from isa.approximations.delta_lut import lut_range
+    from isa.kernels.transformer_ffn import ops
+
+    dmin, dmax, n = lut_range(cfg)
+    step = (dmax - dmin) / (n - 1)
+    spans = []
+    for name, p in model.named_parameters():
+        if name.endswith("vth_pos") or name.endswith("vth_neg"):
+            spans.append(float(p.detach().max() - p.detach().min()))
+    window = max(1, min(8192, int(math.ceil(max(spans) / step)) + 1))
+    ns = ops.probe_lds_gather(window, 8, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    waves_per_launch = cells_launch / 64.0
+    fwd_roof = 2 * waves_per_launch * ns / cus * 1e-6  # ms
+    bwd_roof = 4 * waves_per_launch * ns / cus * 1e-6
+    return {
+        "bound": "lds",
+        "window_records": window,
+        "ns_per_gather_per_cu": round(ns, 4),
+        "forward_roof_ms": round(fwd_roof, 4),
+        "forward_frac": round(fwd_roof / fwd_ms, 4) if fwd_ms else None,
+        "backward_roof_ms": round(bwd_roof, 4),
+        "backward_frac": round(bwd_roof / bwd_ms, 4) if bwd_ms else None,
+        "work": "forward 2, backward 4 random ds_read_b64 gathers per cell-eval (wave-level: per 64 cells)",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -420,6 +459,11 @@ def main() -> int:
     }
     log(f"[bench] fwd kernel {fwd_avg:.3f} ms/launch ({roofline['forward_kernel']['frac']:.3f} of VALU peak), "
         f"bwd kernel {bwd_avg:.3f} ms/launch ({roofline['frac']:.3f})")
+    if not exact:
+        roofline["lds"] = lds_roofline(model, cfg, cells_launch, fwd_avg, bwd_avg, dev)
+        log(f"[bench] LDS gather roofline (window {roofline['lds']['window_records']} records, "
+            f"{roofline['lds']['ns_per_gather_per_cu']:.3f} ns per gather per CU): fwd "
+            f"{roofline['lds']['forward_frac']:.3f}, bwd {roofline['lds']['backward_frac']:.3f}")
 
     cpu = None
     if not args.no_cpu_baseline:

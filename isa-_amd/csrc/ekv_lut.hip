@@ -338,45 +338,94 @@ __device__ inline void block_minmax(float lo, float hi, float2* out) {
     }
 }
 
-__device__ inline void store_token(float* dst, int rec_floats, int64_t e, float c, float r, float z) {
-    if (rec_floats == 2)
-        reinterpret_cast<float2*>(dst)[e] = make_float2(c, r);
-    else
-        reinterpret_cast<float4*>(dst)[e] = make_float4(c, r, z, 0.0f);
+// Four consecutive token records from m * Kp + k0 (k0 a multiple of 4): {c, r} pairs
+// (REC 2) or {c, r, z, 0} (REC 4), as 16-byte stores.
+template <int REC>
+__device__ inline void store_tokens4(float* dst, int64_t e, const float* c, const float* r, const float* z) {
+    float4* d = reinterpret_cast<float4*>(dst + e * REC);
+    if constexpr (REC == 2) {
+        d[0] = make_float4(c[0], r[0], c[1], r[1]);
+        d[1] = make_float4(c[2], r[2], c[3], r[3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[i] = make_float4(c[i], r[i], z[i], 0.0f);
+    }
+}
+
+// Token side of the prep: each thread builds the records of four consecutive inputs of one
+// row (16-byte loads of x where K % 4 == 0), walking the flattened (m, k / 4) index space
+// with a grid stride.
+template <int REC, bool EXACT>
+__device__ inline void prep_tokens(const PrepArgs& a, float& lo, float& hi) {
+    const float aff_s = a.in_affine ? a.in_affine[0] : 1.0f;
+    const float aff_b = a.in_affine ? a.in_affine[1] : 0.0f;
+    const int64_t kq = a.Kp >> 2;  // Kp: a multiple of 8
+    const int64_t total = a.M * kq;
+    const int64_t stride = (int64_t)kPrepBlocksX * blockDim.x;
+    int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= total) return;
+    int64_t m = q / kq, k4 = q - m * kq;
+    const int64_t dm = stride / kq, dk = stride - dm * kq;
+    const bool vec_x = (a.K & 3) == 0 && ((uintptr_t)a.x & 15) == 0;
+    for (; q < total; q += stride) {
+        const int64_t k0 = k4 * 4;
+        const float* xrow = a.x + m * a.K;
+        float xv[4];
+        if (vec_x && k0 < a.K) {
+            const float4 v = *reinterpret_cast<const float4*>(xrow + k0);
+            xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = k0 + i < a.K ? xrow[k0 + i] : 0.0f;
+        }
+        float c[4], r[4], f[4], z[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[i] = 1.0f;
+            if (k0 + i < a.K) {
+                float x = xv[i];
+                if (a.in_affine) x = input_map(x, aff_s, aff_b, a.in_lo, a.in_hi);
+                c[i] = fmaf(x - a.xoff, a.scale, a.xadd);
+                r[i] = 1.0f / (1.0f + x / a.v_sat);
+                if (EXACT) f[i] = (float)exp2((double)x * a.scale_d);
+                const bool bad = c[i] != c[i];
+                lo = fminf(lo, bad ? -INFINITY : c[i]);
+                hi = fmaxf(hi, bad ? INFINITY : c[i]);
+            } else {
+                c[i] = a.pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
+                r[i] = 0.0f;
+            }
+            z[i] = -r[i] / a.z_div;
+        }
+        const int64_t e = m * a.Kp + k0;
+        if (EXACT) {
+            store_tokens4<REC>(a.xrec, e, f, r, z);
+            store_tokens4<REC>(a.xrec_slow, e, c, r, z);
+        } else {
+            store_tokens4<REC>(a.xrec, e, c, r, z);
+        }
+        k4 += dk;
+        m += dm;
+        if (k4 >= kq) {
+            k4 -= kq;
+            ++m;
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     float lo = INFINITY, hi = -INFINITY;
     if (blockIdx.x < kPrepBlocksX) {
-        // rows m are strided over the token-side blocks; threads walk k (coalesced)
-        const float aff_s = a.in_affine ? a.in_affine[0] : 1.0f;
-        const float aff_b = a.in_affine ? a.in_affine[1] : 0.0f;
-        for (int64_t m = blockIdx.x; m < a.M; m += kPrepBlocksX) {
-            const float* xrow = a.x + m * a.K;
-            for (int k = threadIdx.x; k < (int)a.Kp; k += blockDim.x) {
-                float c, r, f = 1.0f;
-                if (k < a.K) {
-                    float xv = xrow[k];
-                    if (a.in_affine) xv = input_map(xv, aff_s, aff_b, a.in_lo, a.in_hi);
-                    c = fmaf(xv - a.xoff, a.scale, a.xadd);
-                    r = 1.0f / (1.0f + xv / a.v_sat);
-                    if (a.exact) f = (float)exp2((double)xv * a.scale_d);
-                    const bool bad = c != c;
-                    lo = fminf(lo, bad ? -INFINITY : c);
-                    hi = fmaxf(hi, bad ? INFINITY : c);
-                } else {
-                    c = a.pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
-                    r = 0.0f;
-                }
-                const int64_t e = m * a.Kp + k;
-                const float z = -r / a.z_div;
-                if (a.exact) {
-                    store_token(a.xrec, a.rec_floats, e, f, r, z);
-                    store_token(a.xrec_slow, a.rec_floats, e, c, r, z);
-                } else {
-                    store_token(a.xrec, a.rec_floats, e, c, r, z);
-                }
-            }
+        if (a.exact) {
+            if (a.rec_floats == 2)
+                prep_tokens<2, true>(a, lo, hi);
+            else
+                prep_tokens<4, true>(a, lo, hi);
+        } else {
+            if (a.rec_floats == 2)
+                prep_tokens<2, false>(a, lo, hi);
+            else
+                prep_tokens<4, false>(a, lo, hi);
         }
         block_minmax(lo, hi, &a.partials[blockIdx.x]);
         return;
@@ -1505,6 +1554,78 @@ __global__ __launch_bounds__(256) void glue_reduce_kernel(const float* __restric
 }
 
 // ----------------------------------------------------------------------------------
+// LDS gather probe (measurement aid for the LDS roofline of the table kernels). One
+// 1024-thread block per CU holds a 64 KB table; every lane issues gathers of REC-byte
+// records (ds_read_b64 or ds_read_b128, the instructions the table kernels use) at 8 fixed
+// indices drawn uniformly from [0, window) per lane, i.e. the pattern of one table gather
+// whose lanes see thresholds spread over `window` records. Eight gathers are in flight per
+// wave between waits; 16 waves per CU overlap them. The results are summed into out so the
+// reads stay live. Indices are < window <= 65536 / REC, inside the table.
+// ----------------------------------------------------------------------------------
+
+typedef float probe_f2 __attribute__((ext_vector_type(2)));
+typedef float probe_f4 __attribute__((ext_vector_type(4)));
+
+template <int REC>
+__global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int iters, unsigned seed, float* out) {
+    __shared__ float4 table[4096];
+    for (int i = threadIdx.x; i < 4096; i += blockDim.x) table[i] = make_float4(i, 0.5f * i, 0.25f * i, 1.0f);
+    __syncthreads();
+    unsigned h = (threadIdx.x + 1) * 2654435761u ^ seed ^ blockIdx.x * 40503u;
+    unsigned addr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        h ^= h << 13;
+        h ^= h >> 17;
+        h ^= h << 5;
+        addr[i] = (h % (unsigned)window) * REC;
+    }
+    float acc = 0.0f;
+    for (int it = 0; it < iters; ++it) {
+        if constexpr (REC == 8) {
+            probe_f2 v0, v1, v2, v3, v4, v5, v6, v7;
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v0) : "v"(addr[0]));
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v1) : "v"(addr[1]));
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v2) : "v"(addr[2]));
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v3) : "v"(addr[3]));
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v4) : "v"(addr[4]));
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v5) : "v"(addr[5]));
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v6) : "v"(addr[6]));
+            asm volatile("ds_read_b64 %0, %1" : "=v"(v7) : "v"(addr[7]));
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v0));
+            asm volatile("" : "+v"(v1));
+            asm volatile("" : "+v"(v2));
+            asm volatile("" : "+v"(v3));
+            asm volatile("" : "+v"(v4));
+            asm volatile("" : "+v"(v5));
+            asm volatile("" : "+v"(v6));
+            asm volatile("" : "+v"(v7));
+            acc += ((v0.x + v1.x) + (v2.x + v3.x)) + ((v4.x + v5.x) + (v6.x + v7.x));
+        } else {
+            probe_f4 v0, v1, v2, v3, v4, v5, v6, v7;
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v0) : "v"(addr[0]));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v1) : "v"(addr[1]));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v2) : "v"(addr[2]));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v3) : "v"(addr[3]));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v4) : "v"(addr[4]));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v5) : "v"(addr[5]));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v6) : "v"(addr[6]));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v7) : "v"(addr[7]));
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v0));
+            asm volatile("" : "+v"(v1));
+            asm volatile("" : "+v"(v2));
+            asm volatile("" : "+v"(v3));
+            asm volatile("" : "+v"(v4));
+            asm volatile("" : "+v"(v5));
+            asm volatile("" : "+v"(v6));
+            asm volatile("" : "+v"(v7));
+            acc += ((v0.x + v1.x) + (v2.x + v3.x)) + ((v4.x + v5.x) + (v6.x + v7.x));
+        }
+    }
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+// ----------------------------------------------------------------------------------
 // Host-side planning shared by the workspace queries and the launches.
 // ----------------------------------------------------------------------------------
 
@@ -2462,6 +2583,34 @@ int isa_ekv_measured_backward(const float* x, const int16_t* ids_a, const int16_
     return run_measured_backward(x, reinterpret_cast<const short*>(ids_a), reinterpret_cast<const short*>(ids_b), M,
                                  K, O, codebook, current_scale, grad_out, out_pre, r_tia, out_min, out_max, grad_x,
                                  workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iterations, float* out, int64_t out_floats,
+                             int* gathers_per_cu, void* stream) {
+    if (record_bytes != 8 && record_bytes != 16)
+        return fail(ISA_EKV_EINVAL, "record_bytes must be 8 or 16 (got %d)", record_bytes);
+    if (window_records < 1 || window_records > 65536 / record_bytes)
+        return fail(ISA_EKV_EINVAL, "window_records must be in [1, %d] (got %d)", 65536 / record_bytes,
+                    window_records);
+    if (iterations < 1 || iterations > (1 << 20))
+        return fail(ISA_EKV_EINVAL, "iterations must be in [1, 2^20] (got %d)", iterations);
+    int dev = 0, cus = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return hip_fail(err, "device query");
+    if (!out || out_floats < (int64_t)cus * 1024)
+        return fail(ISA_EKV_EINVAL, "out needs %lld floats (one per thread of %d blocks)", (long long)cus * 1024, cus);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (record_bytes == 8)
+        hipLaunchKernelGGL(lds_gather_probe_kernel<8>, dim3(cus), dim3(1024), 0, s, window_records, iterations,
+                           12345u, out);
+    else
+        hipLaunchKernelGGL(lds_gather_probe_kernel<16>, dim3(cus), dim3(1024), 0, s, window_records, iterations,
+                           12345u, out);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "lds probe launch");
+    if (gathers_per_cu) *gathers_per_cu = 16 * 8 * iterations;
+    return 0;
 }
 
 }  // extern "C"

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -47,6 +47,7 @@ EXPORTS = (
     "isa_ekv_measured_backward",
     "isa_ekv_profile_begin",
     "isa_ekv_profile_end",
+    "isa_ekv_probe_lds_gather",
 )
 
 _lock = threading.Lock()
@@ -165,6 +166,8 @@ def _declare(lib) -> None:
     lib.isa_ekv_profile_begin.restype = ci
     lib.isa_ekv_profile_end.argtypes = [ctypes.POINTER(f64), ctypes.POINTER(ci)]
     lib.isa_ekv_profile_end.restype = ci
+    lib.isa_ekv_probe_lds_gather.argtypes = [ci, ci, ci, vp, i64, ctypes.POINTER(ci), vp]
+    lib.isa_ekv_probe_lds_gather.restype = ci
 
 
 def load(path: Path | None = None):

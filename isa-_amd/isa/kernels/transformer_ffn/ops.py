@@ -401,3 +401,33 @@ def measured_backward(x: torch.Tensor, ids_a: torch.Tensor, ids_b: Optional[torc
     _hip.check(rc, "isa_ekv_measured_backward")
     del keep
     return gx
+
+
+def probe_lds_gather(window_records: int, record_bytes: int = 8, iterations: int = 2048,
+                     device: Optional[torch.device] = None, repeats: int = 5) -> float:
+    """Average nanoseconds per wave-level LDS gather per CU for random `record_bytes`
+    gathers whose 64 lanes draw indices uniformly from `window_records` entries (one
+    `isa_ekv_probe_lds_gather` launch per repeat, after one untimed launch, timed with HIP
+    events on the current stream). A measurement aid for the table kernels' LDS bound."""
+    lib = _hip.load()
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = torch.empty(cus * 1024, dtype=torch.float32, device=dev)
+    per_cu = ctypes.c_int(0)
+    with torch.cuda.device(dev):
+        stream = _hip.stream_handle(dev)
+
+        def launch():
+            rc = lib.isa_ekv_probe_lds_gather(int(window_records), int(record_bytes), int(iterations),
+                                              out.data_ptr(), out.numel(), ctypes.byref(per_cu), stream)
+            _hip.check(rc, "isa_ekv_probe_lds_gather")
+
+        launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(repeats):
+            launch()
+        e1.record()
+        torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / repeats
+    return ms * 1e6 / per_cu.value

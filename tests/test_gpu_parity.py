@@ -178,3 +178,18 @@ def test_bf16_table_mode(cuda_device):
     out, gx, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device)
     assert errs(out, ref)[0] <= FWD_TOL
     assert errs(gx, dx)[0] <= BWD_TOL
+
+
+def test_lds_gather_probe(cuda_device):
+    """The LDS roofline's probe runs and orders as bank conflicts predict: gathers whose
+    lanes spread over a wide window cost at least as much as a 32-record window (one
+    8-byte record per bank pair, conflict-free) and 16-byte records more than 8-byte ones."""
+    from isa.kernels.transformer_ffn import ops
+
+    print("[case] lds gather probe", flush=True)
+    narrow = ops.probe_lds_gather(32, 8, iterations=256, device=cuda_device)
+    wide = ops.probe_lds_gather(1024, 8, iterations=256, device=cuda_device)
+    wide16 = ops.probe_lds_gather(1024, 16, iterations=256, device=cuda_device)
+    assert 0.0 < narrow < 1e3
+    assert wide >= 0.95 * narrow
+    assert wide16 >= 0.95 * wide
