@@ -338,77 +338,72 @@ __device__ inline void block_minmax(float lo, float hi, float2* out) {
     }
 }
 
-// Four consecutive token records from m * Kp + k0 (k0 a multiple of 4): {c, r} pairs
-// (REC 2) or {c, r, z, 0} (REC 4), as 16-byte stores.
+// Token side of the prep: the flattened [M][Kp] record space is walked in chunks of four
+// block widths; each thread builds four records a block width apart, so every load and
+// store instruction of a wave covers consecutive records (4-byte loads of x, 8- or
+// 16-byte record stores).
 template <int REC>
-__device__ inline void store_tokens4(float* dst, int64_t e, const float* c, const float* r, const float* z) {
-    float4* d = reinterpret_cast<float4*>(dst + e * REC);
-    if constexpr (REC == 2) {
-        d[0] = make_float4(c[0], r[0], c[1], r[1]);
-        d[1] = make_float4(c[2], r[2], c[3], r[3]);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = make_float4(c[i], r[i], z[i], 0.0f);
-    }
+__device__ inline void store_token(float* dst, int64_t e, float c, float r, float z) {
+    if constexpr (REC == 2)
+        reinterpret_cast<float2*>(dst)[e] = make_float2(c, r);
+    else
+        reinterpret_cast<float4*>(dst)[e] = make_float4(c, r, z, 0.0f);
 }
 
-// Token side of the prep: each thread builds the records of four consecutive inputs of one
-// row (16-byte loads of x where K % 4 == 0), walking the flattened (m, k / 4) index space
-// with a grid stride.
 template <int REC, bool EXACT>
 __device__ inline void prep_tokens(const PrepArgs& a, float& lo, float& hi) {
     const float aff_s = a.in_affine ? a.in_affine[0] : 1.0f;
     const float aff_b = a.in_affine ? a.in_affine[1] : 0.0f;
-    const int64_t kq = a.Kp >> 2;  // Kp: a multiple of 8
-    const int64_t total = a.M * kq;
-    const int64_t stride = (int64_t)kPrepBlocksX * blockDim.x;
-    int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= total) return;
-    int64_t m = q / kq, k4 = q - m * kq;
-    const int64_t dm = stride / kq, dk = stride - dm * kq;
-    const bool vec_x = (a.K & 3) == 0 && ((uintptr_t)a.x & 15) == 0;
-    for (; q < total; q += stride) {
-        const int64_t k0 = k4 * 4;
-        const float* xrow = a.x + m * a.K;
-        float xv[4];
-        if (vec_x && k0 < a.K) {
-            const float4 v = *reinterpret_cast<const float4*>(xrow + k0);
-            xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+    const int64_t total = a.M * a.Kp;
+    const int64_t chunk = 4 * (int64_t)blockDim.x;
+    for (int64_t base = (int64_t)blockIdx.x * chunk; base < total; base += (int64_t)kPrepBlocksX * chunk) {
+        int64_t q = base + threadIdx.x;
+        int64_t m, k;
+        if (total <= 0xffffffffll) {
+            m = (uint32_t)q / (uint32_t)a.Kp;
         } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xv[i] = k0 + i < a.K ? xrow[k0 + i] : 0.0f;
+            m = q / a.Kp;
         }
-        float c[4], r[4], f[4], z[4];
+        k = q - m * a.Kp;
+        float xv[4];  // loads first: four independent requests in flight
+        int64_t mj[4], kj[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[i] = 1.0f;
-            if (k0 + i < a.K) {
-                float x = xv[i];
-                if (a.in_affine) x = input_map(x, aff_s, aff_b, a.in_lo, a.in_hi);
-                c[i] = fmaf(x - a.xoff, a.scale, a.xadd);
-                r[i] = 1.0f / (1.0f + x / a.v_sat);
-                if (EXACT) f[i] = (float)exp2((double)x * a.scale_d);
-                const bool bad = c[i] != c[i];
-                lo = fminf(lo, bad ? -INFINITY : c[i]);
-                hi = fmaxf(hi, bad ? INFINITY : c[i]);
-            } else {
-                c[i] = a.pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
-                r[i] = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+            mj[j] = m;
+            kj[j] = k;
+            xv[j] = (q < total && k < a.K) ? a.x[m * a.K + k] : 0.0f;
+            q += blockDim.x;
+            k += blockDim.x;
+            while (k >= a.Kp) {
+                k -= a.Kp;
+                ++m;
             }
-            z[i] = -r[i] / a.z_div;
         }
-        const int64_t e = m * a.Kp + k0;
-        if (EXACT) {
-            store_tokens4<REC>(a.xrec, e, f, r, z);
-            store_tokens4<REC>(a.xrec_slow, e, c, r, z);
-        } else {
-            store_tokens4<REC>(a.xrec, e, c, r, z);
-        }
-        k4 += dk;
-        m += dm;
-        if (k4 >= kq) {
-            k4 -= kq;
-            ++m;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t e = mj[j] * a.Kp + kj[j];
+            if (e >= total) break;
+            float c, r, f = 1.0f;
+            if (kj[j] < a.K) {
+                float x = xv[j];
+                if (a.in_affine) x = input_map(x, aff_s, aff_b, a.in_lo, a.in_hi);
+                c = fmaf(x - a.xoff, a.scale, a.xadd);
+                r = 1.0f / (1.0f + x / a.v_sat);
+                if (EXACT) f = (float)exp2((double)x * a.scale_d);
+                const bool bad = c != c;
+                lo = fminf(lo, bad ? -INFINITY : c);
+                hi = fmaxf(hi, bad ? INFINITY : c);
+            } else {
+                c = a.pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
+                r = 0.0f;
+            }
+            const float z = -r / a.z_div;
+            if (EXACT) {
+                store_token<REC>(a.xrec, e, f, r, z);
+                store_token<REC>(a.xrec_slow, e, c, r, z);
+            } else {
+                store_token<REC>(a.xrec, e, c, r, z);
+            }
         }
     }
 }
@@ -552,7 +547,39 @@ struct LutFwdCell {
     __device__ float accumulate(float acc, float2 xv, float2 w) const {
         return fmaf((*this)(xv.x, w.x, w.y), xv.y, acc);
     }
+    // two-phase form of accumulate (same arithmetic): fetch issues the gathers of one cell,
+    // finish consumes them, so a loop can keep several cells' gathers in flight
+    struct Pending {
+        float cp, cn;
+        float2 ep, en;
+    };
+    __device__ Pending fetch(float xs, float2 w) const {
+        Pending q;
+        q.cp = coord<CLAMP>(xs, w.x, cmin, cmax);
+        q.cn = coord<CLAMP>(xs, w.y, cmin, cmax);
+        q.ep = lut[(unsigned)q.cp];
+        q.en = lut[(unsigned)q.cn];
+        return q;
+    }
+    __device__ float finish(float acc, const Pending& q, float r) const {
+        return fmaf(fmaf(q.cp, q.ep.y, q.ep.x) - fmaf(q.cn, q.en.y, q.en.x), r, acc);
+    }
 };
+
+#ifndef ISA_EKV_FWD_TOKOPS
+#define ISA_EKV_FWD_TOKOPS 16  // forward: token records (MR tokens x KU inputs) loaded per step
+#endif
+#ifndef ISA_EKV_FWD_WT
+#define ISA_EKV_FWD_WT 3  // forward plan: target waves = WT x 256 CUs x 16
+#endif
+#ifndef ISA_EKV_FWD_FB
+#define ISA_EKV_FWD_FB 4  // LUT forward: cells whose gathers are issued together
+#endif
+
+template <class Cell>
+struct TwoPhaseCell : std::false_type {};
+template <bool CLAMP>
+struct TwoPhaseCell<LutFwdCell<CLAMP>> : std::true_type {};
 
 // Backward cells return a pair view whose dp()/dn() (derivative terms) and lp()/ln()
 // (current terms) the loop reads where it uses them; the LUT view holds the two gathered
@@ -750,7 +777,7 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
     const float4* wcol = reinterpret_cast<const float4*>(wsT + o_lane);
     const size_t wstride = (size_t)a.Op / 2;  // float4 per k row
 
-    constexpr int KU = 16 / MR;  // 32 SGPRs of token operands per step
+    constexpr int KU = ISA_EKV_FWD_TOKOPS / MR >= 1 ? ISA_EKV_FWD_TOKOPS / MR : 1;  // token records per step
     static_assert(KU >= 1 && 8 % KU == 0, "Kp is a multiple of 8");
     for (int k0 = 0; k0 < a.Kp; k0 += KU) {
         float2 w[KU][ORR];
@@ -767,9 +794,19 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
 #pragma unroll
             for (int i = 0; i < MR; ++i) {
                 const float2 xv = load_uniform2(xrow[i] + k0 + kk);
+                if constexpr (TwoPhaseCell<Cell>::value && ISA_EKV_FWD_FB > 0) {
+                    constexpr int FB = ISA_EKV_FWD_FB < ORR ? ISA_EKV_FWD_FB : ORR;
 #pragma unroll
-                for (int j = 0; j < ORR; ++j) {
-                    acc[i][j] = cell.accumulate(acc[i][j], xv, w[kk][j]);
+                    for (int j0 = 0; j0 < ORR; j0 += FB) {
+                        typename Cell::Pending q[FB];
+#pragma unroll
+                        for (int jj = 0; jj < FB; ++jj) q[jj] = cell.fetch(xv.x, w[kk][j0 + jj]);
+#pragma unroll
+                        for (int jj = 0; jj < FB; ++jj) acc[i][j0 + jj] = cell.finish(acc[i][j0 + jj], q[jj], xv.y);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < ORR; ++j) acc[i][j] = cell.accumulate(acc[i][j], xv, w[kk][j]);
                 }
             }
         }
@@ -1641,7 +1678,7 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
     p.Op = round_up(O > 0 ? O : 1, 64 * kFwdORR);
     p.n_ot = (int)(p.Op / (64 * kFwdORR));
     // choose tokens per wave so the grid covers the chip several times over
-    const int64_t waves_target = 3 * 256 * 16;
+    const int64_t waves_target = (int64_t)ISA_EKV_FWD_WT * 256 * 16;
     p.mr = 8;
     while (p.mr > 2 && ((M + p.mr - 1) / p.mr) * p.n_ot < waves_target) p.mr /= 2;
     const int64_t tokens_per_block = (int64_t)kFwdWaves * p.mr;
