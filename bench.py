@@ -348,6 +348,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ekv-approx", default="lut", choices=["lut", "exact"],
                     help="CIMLinear projection: the LUT kernels (headline) or the exact-formula kernels")
+    ap.add_argument("--lut-dtype", default=None, choices=["float32", "bfloat16"],
+                    help="LUT table precision (default: the config's, float32); bfloat16 reproduces the "
+                         "reference's bf16 tables")
+    ap.add_argument("--vth-spread", default="init", choices=["init", "full"],
+                    help="thresholds: the reference's initialisation U(2.5 +- 0.5*2nU_T) (headline), or "
+                         "U[V_TH_MIN, V_TH_MAX] as a stand-in for trained thresholds (wider table windows)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -377,6 +383,8 @@ def main() -> int:
     cfg = make_flash_transistor_ekv_config(default_lut_size=args.lut_size)
     cfg["LUT_DELTA_SIZE"] = args.lut_size
     cfg["ekv_approx"] = args.ekv_approx
+    if args.lut_dtype:
+        cfg["LUT_DTYPE"] = args.lut_dtype
     fwd_instr, bwd_instr = INSTR_PER_CELL[args.ekv_approx]
 
     torch.manual_seed(0)
@@ -390,6 +398,11 @@ def main() -> int:
         model = CIMLinear(D, F, cfg)
         layers = [(M, D, F)]
     model = model.to(dev)
+    if args.vth_spread == "full":
+        with torch.no_grad():
+            for name, p in model.named_parameters():
+                if name.endswith(("vth_pos", "vth_neg")):
+                    p.uniform_(float(cfg["V_TH_MIN"]), float(cfg["V_TH_MAX"]))
     x = torch.randn(B, T, D, device=dev)
     if physical is None:
         x = x.clamp(0.0, 4.0)  # VoltageMapping defaults, applied once up front
@@ -490,7 +503,9 @@ def main() -> int:
                 "vitm_ffn": "Physical ViT-M FFN: CIMLinear 256->1024->256, X[128,65,256] fp32, fwd+bwd",
                 "gptm_hybrid": "Hybrid GPT-M FFN: CIMLinear 384->1536 + Linear 1536->384, X[16,1024,384], fwd+bwd",
                 "vits_up": "ViT-S up-projection: CIMLinear 192->768, X[8,65,192] fp32, fwd+bwd",
-            }[args.config] + (" (exact-formula kernels, ekv_approx='exact')" if exact else ""),
+            }[args.config] + (" (exact-formula kernels, ekv_approx='exact')" if exact else "")
+              + (f" (LUT_DTYPE={cfg['LUT_DTYPE']})" if args.lut_dtype else "")
+              + (" (thresholds U[V_TH_MIN, V_TH_MAX])" if args.vth_spread == "full" else ""),
             "tokens": M,
             "lut_entries": args.lut_size,
             "cell_evals_per_step": cells_step,

@@ -1597,16 +1597,22 @@ __global__ __launch_bounds__(256) void glue_reduce_kernel(const float* __restric
 // indices drawn uniformly from [0, window) per lane, i.e. the pattern of one table gather
 // whose lanes see thresholds spread over `window` records. Eight gathers are in flight per
 // wave between waits; 16 waves per CU overlap them. The results are summed into out so the
-// reads stay live. Indices are < window <= 65536 / REC, inside the table.
+// reads stay live. Indices are < window <= kProbeLdsBytes / REC, inside the table.
 // ----------------------------------------------------------------------------------
 
 typedef float probe_f2 __attribute__((ext_vector_type(2)));
 typedef float probe_f4 __attribute__((ext_vector_type(4)));
 
+// The table is dynamic LDS sized at launch (kProbeLdsBytes): a static array that only the
+// inline-asm reads use would be removed by the compiler, leaving the reads outside the
+// workgroup's allocation.
+constexpr int kProbeLdsBytes = 65536;
+
 template <int REC>
 __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int iters, unsigned seed, float* out) {
-    __shared__ float4 table[4096];
-    for (int i = threadIdx.x; i < 4096; i += blockDim.x) table[i] = make_float4(i, 0.5f * i, 0.25f * i, 1.0f);
+    extern __shared__ float4 probe_table[];
+    for (int i = threadIdx.x; i < kProbeLdsBytes / 16; i += blockDim.x)
+        probe_table[i] = make_float4(i, 0.5f * i, 0.25f * i, 1.0f);
     __syncthreads();
     unsigned h = (threadIdx.x + 1) * 2654435761u ^ seed ^ blockIdx.x * 40503u;
     unsigned addr[8];
@@ -2626,8 +2632,8 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
                              int* gathers_per_cu, void* stream) {
     if (record_bytes != 8 && record_bytes != 16)
         return fail(ISA_EKV_EINVAL, "record_bytes must be 8 or 16 (got %d)", record_bytes);
-    if (window_records < 1 || window_records > 65536 / record_bytes)
-        return fail(ISA_EKV_EINVAL, "window_records must be in [1, %d] (got %d)", 65536 / record_bytes,
+    if (window_records < 1 || window_records > kProbeLdsBytes / record_bytes)
+        return fail(ISA_EKV_EINVAL, "window_records must be in [1, %d] (got %d)", kProbeLdsBytes / record_bytes,
                     window_records);
     if (iterations < 1 || iterations > (1 << 20))
         return fail(ISA_EKV_EINVAL, "iterations must be in [1, 2^20] (got %d)", iterations);
@@ -2639,11 +2645,11 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
         return fail(ISA_EKV_EINVAL, "out needs %lld floats (one per thread of %d blocks)", (long long)cus * 1024, cus);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (record_bytes == 8)
-        hipLaunchKernelGGL(lds_gather_probe_kernel<8>, dim3(cus), dim3(1024), 0, s, window_records, iterations,
-                           12345u, out);
+        hipLaunchKernelGGL(lds_gather_probe_kernel<8>, dim3(cus), dim3(1024), kProbeLdsBytes, s, window_records,
+                           iterations, 12345u, out);
     else
-        hipLaunchKernelGGL(lds_gather_probe_kernel<16>, dim3(cus), dim3(1024), 0, s, window_records, iterations,
-                           12345u, out);
+        hipLaunchKernelGGL(lds_gather_probe_kernel<16>, dim3(cus), dim3(1024), kProbeLdsBytes, s, window_records,
+                           iterations, 12345u, out);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "lds probe launch");
     if (gathers_per_cu) *gathers_per_cu = 16 * 8 * iterations;
