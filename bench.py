@@ -109,6 +109,40 @@ def cpu_baseline(d_model: int, d_ffn: int, target_s: float) -> dict:
     }
 
 
+def cpu_lut_oracle(d_model: int, d_ffn: int, target_s: float) -> dict:
+    """For information: the CPU LUT oracle (oracle/ekv_oracle.c, one thread, fp32 cells with
+    double sums) timed on fc1 fwd+bwd over a token sample sized to about target_s seconds."""
+    import numpy as np
+
+    from oracle import oracle
+
+    cfg = dict(oracle.FLASH_PARAMS)
+    cfg["LUT_DELTA_SIZE"] = 4096
+    dmin, dmax, _ = oracle.lut_range(cfg)
+    ti, td = oracle.lut_tables(cfg)
+    rng = np.random.default_rng(0)
+    lo, hi = 2.5 - 0.5 * 2 * cfg["n"] * cfg["U_T"], 2.5 + 0.5 * 2 * cfg["n"] * cfg["U_T"]
+    vp = rng.uniform(lo, hi, (d_ffn, d_model)).astype(np.float32)
+    vn = rng.uniform(lo, hi, (d_ffn, d_model)).astype(np.float32)
+
+    def run(tokens: int) -> float:
+        x = np.clip(rng.standard_normal((tokens, d_model)), 0.0, 4.0).astype(np.float32)
+        g = rng.standard_normal((tokens, d_ffn)).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.forward(x, vp, vn, ti, dmin, dmax, cfg["V_sat"])
+        oracle.backward(x, vp, vn, g, ti, td, dmin, dmax, cfg["V_sat"])
+        return time.perf_counter() - t0
+
+    run(1)  # warm-up
+    dt = run(8)
+    want = max(1, min(1024, int(8 * target_s / max(dt, 1e-4))))
+    dt = run(want)
+    cells = 2.0 * want * d_model * d_ffn
+    return {"value": cells / dt, "unit": "cell-evals/s", "cores": 1, "kind": "oracle (LUT, C)",
+            "sample": f"oracle/ekv_oracle.c LUT forward + dX + dVth, fc1 {d_model}->{d_ffn} on {want} tokens "
+                      f"({cells:.3e} cell-evals, {dt:.1f} s)"}
+
+
 def measured_traffic(config: str):
     """HBM bytes per backward main-kernel launch from the committed rocprofv3 counter summary
     (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel), or None if absent."""
@@ -479,10 +513,13 @@ def main() -> int:
             f"{roofline['lds']['forward_frac']:.3f}, bwd {roofline['lds']['backward_frac']:.3f}")
 
     cpu = None
+    lut_cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline ...")
         cpu = cpu_baseline(D, F, args.cpu_seconds)
         log(f"[bench] cpu {cpu['value']:.4e} cell-evals/s on {cpu['cores']} threads")
+        lut_cpu = cpu_lut_oracle(D, F, 4.0)
+        log(f"[bench] cpu LUT oracle {lut_cpu['value']:.4e} cell-evals/s on 1 thread")
 
     result = {
         "metric": "CIM cell-evals/sec fwd+bwd, Physical GPT-L FFN, 1 GPU; % of VALU roofline",
@@ -513,6 +550,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_lut_oracle": lut_cpu,
     }
     print(json.dumps(result), flush=True)
     return 0
