@@ -15,8 +15,12 @@
 // MI355X design (one process, one device, caller-owned memory):
 //  * The table lives in LDS as padded records in intercept form: record i holds
 //    {T[i] - i*dT[i], dT[i]} with dT[i] = T[i+1] - T[i], so L(c) = fma(c, dT, A) on the raw
-//    coordinate c. Forward records {A_I, dI} (8 B, one ds_read_b64 per branch), backward
-//    {A_I, dI, A_D, dD} (16 B, one ds_read_b128).
+//    coordinate c. Forward records {A_I, dI} (8 B, one ds_read_b64 per branch); backward
+//    records as an I half {A_I, dI} and a D half {A_D, dD} kSplitRecords records apart (two
+//    ds_read_b64 per branch from one address), or interleaved 16-byte records read with
+//    one ds_read_b128 when the split table does not fit. The random gathers of a wave
+//    collide in the LDS banks once its thresholds span more than 32 records; those bank
+//    conflicts, not VALU work, set the kernels' speed.
 //    kPad replicated end records on each side reproduce the reference's coordinate clamp
 //    exactly for coordinates within kPad-1 entries of the table range, so a kernel whose
 //    operand ranges fit (checked on device from the prep kernel's range partials) runs a
