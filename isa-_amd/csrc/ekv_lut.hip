@@ -93,6 +93,9 @@ constexpr int kPrepBlocksX = 1024; // prep blocks for the token side
 constexpr int kPrepBlocksW = 256; // prep blocks for the threshold side
 constexpr int kMaxEntriesFwd = 16384;
 constexpr int kMaxEntriesBwd = 8192;
+#ifndef ISA_EKV_BWD_LANE_RED
+#define ISA_EKV_BWD_LANE_RED 1  // dX reduction: 0 LDS buffers, 1 lane exchanges, 2 lane exchanges when the table crowds LDS
+#endif
 #ifndef ISA_EKV_BWD_SPLIT
 #define ISA_EKV_BWD_SPLIT 1
 #endif
@@ -940,10 +943,49 @@ struct BwdTableSplit {
     }
 };
 
-template <bool NEED_X, bool NEED_W, class Cell>
+// Cross-lane dX reduction without LDS (gfx950 lane exchanges): the wave's four per-lane
+// partials v0..v3 (one per input of the wave) are summed over all 64 lanes so that every
+// lane of 16-lane row r ends with the total of one input. permlane32_swap exchanges a
+// register's upper half with another register's lower half, so adding the two results
+// pairs lanes l and l+32 of one input; permlane16_swap does the same across adjacent
+// 16-lane rows; four row rotations finish each row. The order of the additions is fixed,
+// so the result is reproducible. wave_rows_input() gives, per lane, which input its row
+// holds: the same exchanges applied to the labels 0..3 (both outputs of an exchange carry
+// one label at every lane).
+template <int N>
+__device__ inline float dpp_row_rotate(float v) {  // row_ror:N within each 16-lane row
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xf, 0xf, false));
+}
+
+__device__ inline float wave_sum_rows4(float v0, float v1, float v2, float v3) {
+    const auto p01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v1), false, false);
+    const auto p23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v2), __float_as_uint(v3), false, false);
+    const float t01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);
+    const float t23 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(t01), __float_as_uint(t23), false, false);
+    float u = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    u += dpp_row_rotate<8>(u);
+    u += dpp_row_rotate<4>(u);
+    u += dpp_row_rotate<2>(u);
+    u += dpp_row_rotate<1>(u);
+    return u;
+}
+
+__device__ inline int wave_rows_input() {
+    const auto p01 = __builtin_amdgcn_permlane32_swap(0u, 1u, false, false);
+    const auto p23 = __builtin_amdgcn_permlane32_swap(2u, 3u, false, false);
+    const auto q = __builtin_amdgcn_permlane16_swap(p01[0], p23[0], false, false);
+    return (int)q[0];
+}
+
+// LANE_RED: reduce each token's dX partials across the wave with lane exchanges
+// (wave_sum_rows4) instead of the LDS transpose buffer (red unused), freeing LDS for
+// tables too large to leave room for the buffers of 16 waves.
+template <bool NEED_X, bool NEED_W, class Cell, bool LANE_RED = false>
 __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4* xrec, const float2* wsT,
                                 float* red, int item) {
     constexpr int ORR = kBwdORR, KR = kBwdKR, MB = kBwdMB;
+    static_assert(!LANE_RED || KR == 4, "the lane-exchange reduction sums four inputs per wave");
     const int lane = threadIdx.x & 63;
     // inputs vary fastest: the waves of a block share (output block, token split), so the
     // G row slices they stream are fetched once into the CU's L1 and reused
@@ -976,6 +1018,7 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
     // transpose-buffer reduction role of this lane: slot = lane / 4, quarter = lane % 4
     const int my_slot = lane >> 2;
     const int my_quarter = lane & 3;
+    const int row_kk = LANE_RED ? wave_rows_input() : 0;  // input whose dX total this lane's row holds
 
     // token m's operands are prefetched one step ahead (scalar token records, vector grads)
     const float4* xbase = xrec + k0;
@@ -1039,11 +1082,19 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
                 for (int kk = 0; kk < KR; ++kk) tv[kk] = 0.0f;
             }
             if (NEED_X) {
+                if constexpr (LANE_RED) {
+                    if (m < m_end) {  // wave-uniform: every lane takes part in the exchanges
+                        const float sum = wave_sum_rows4(tv[0], tv[1], tv[2], tv[3]);
+                        const int k = k0 + row_kk;
+                        if ((lane & 15) == 0 && k < a.K) a.dx_part[((size_t)ob * a.M + m) * a.K + k] = sum;
+                    }
+                } else {
 #pragma unroll
-                for (int kk = 0; kk < KR; ++kk) red[(s * KR + kk) * kRedStride + lane] = tv[kk];
+                    for (int kk = 0; kk < KR; ++kk) red[(s * KR + kk) * kRedStride + lane] = tv[kk];
+                }
             }
         }
-        if (NEED_X) {
+        if (NEED_X && !LANE_RED) {
             // all 64 lanes of this wave wrote MB*KR slots; LDS ops of one wave complete in
             // order, so only a compiler barrier is needed before reading other lanes' values
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1083,7 +1134,7 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
     }
 }
 
-template <bool NEED_X, bool NEED_W, bool SPLIT>
+template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false>
 __global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
@@ -1101,7 +1152,9 @@ __global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int table_records = SPLIT ? kSplitRecords : a.NP;
-    float* red = reinterpret_cast<float*>(s_lut_bwd + table_records) + wave * (kBwdMB * kBwdKR * kRedStride);
+    float* red = LANE_RED ? nullptr
+                          : reinterpret_cast<float*>(s_lut_bwd + table_records) +
+                                wave * (kBwdMB * kBwdKR * kRedStride);
     const int item = blockIdx.x * waves + wave;
     if (item >= a.n_items) return;
     using Table = typename std::conditional<SPLIT, BwdTableSplit, BwdTableInterleaved>::type;
@@ -1111,9 +1164,11 @@ __global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
     else
         t = BwdTableInterleaved{s_lut_bwd};
     if (fast)
-        bwd_body<NEED_X, NEED_W>(a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+        bwd_body<NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(a, LutBwdCell<false, Table>{t, a.cmin, a.cmax},
+                                                                     a.xrec, a.wsT, red, item);
     else
-        bwd_body<NEED_X, NEED_W>(a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+        bwd_body<NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(a, LutBwdCell<true, Table>{t, a.cmin, a.cmax},
+                                                                    a.xrec, a.wsT, red, item);
 }
 
 // Exact-formula backward (reference: ekv_triton.py:94-169): same work decomposition; LDS
@@ -1714,7 +1769,7 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
 struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
-    bool grad_padded, split;
+    bool grad_padded, split, lane_red;
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_gpad, off_dx, off_dv, off_glue, bytes,
         lds_bytes;
 };
@@ -1732,10 +1787,17 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     const size_t red_bytes = (size_t)kBwdMB * kBwdKR * kRedStride * 4;
     p.split = !exact && ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
     const size_t lut_bytes = exact ? 0 : (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
+    // dX reduction across the wave: lane exchanges (no LDS; measured 5% faster at N = 4096
+    // and, with the 8192-entry table, the only way to keep 16 waves per block), or the LDS
+    // transpose buffers
+    p.lane_red = !exact && need_x &&
+                 (ISA_EKV_BWD_LANE_RED == 1 ||
+                  (ISA_EKV_BWD_LANE_RED == 2 && lut_bytes + 16 * red_bytes > (size_t)kLdsBytes));
+    const size_t per_wave = p.lane_red ? 0 : red_bytes;
     int wpb = 16;
-    while (wpb > 1 && lut_bytes + wpb * red_bytes > (size_t)kLdsBytes) wpb /= 2;
+    while (wpb > 1 && lut_bytes + wpb * per_wave > (size_t)kLdsBytes) wpb /= 2;
     p.waves_per_block = wpb;
-    p.lds_bytes = lut_bytes + (size_t)wpb * red_bytes;
+    p.lds_bytes = lut_bytes + (size_t)wpb * per_wave;
     // Token splits. One block runs per CU at a time (the LDS table), and blocks of equal
     // work finish together, so the launch takes ceil(blocks / CUs) rounds. Among the split
     // counts from ~2 rounds up, take the smallest whose block count fills its rounds to
@@ -1826,19 +1888,19 @@ void launch_forward(bool exact, int mr, dim3 grid, size_t lds, hipStream_t s, co
         hipLaunchKernelGGL(fwd_kernel<2>, grid, block, lds, s, fa);
 }
 
-template <bool SPLIT>
+template <bool SPLIT, bool LANE_RED>
 void launch_backward_layout(bool need_x, bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s,
                             const BwdArgs& ba) {
     if (need_x && need_w)
-        hipLaunchKernelGGL((bwd_kernel<true, true, SPLIT>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<true, true, SPLIT, LANE_RED>), grid, block, lds, s, ba);
     else if (need_x)
-        hipLaunchKernelGGL((bwd_kernel<true, false, SPLIT>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<true, false, SPLIT, LANE_RED>), grid, block, lds, s, ba);
     else
-        hipLaunchKernelGGL((bwd_kernel<false, true, SPLIT>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<false, true, SPLIT, false>), grid, block, lds, s, ba);
 }
 
-void launch_backward(bool exact, bool need_x, bool need_w, bool split, dim3 grid, dim3 block, size_t lds,
-                     hipStream_t s, const BwdArgs& ba) {
+void launch_backward(bool exact, bool need_x, bool need_w, bool split, bool lane_red, dim3 grid, dim3 block,
+                     size_t lds, hipStream_t s, const BwdArgs& ba) {
     if (exact) {
         if (need_x && need_w)
             hipLaunchKernelGGL((bwd_exact_kernel<true, true>), grid, block, lds, s, ba);
@@ -1847,9 +1909,15 @@ void launch_backward(bool exact, bool need_x, bool need_w, bool split, dim3 grid
         else
             hipLaunchKernelGGL((bwd_exact_kernel<false, true>), grid, block, lds, s, ba);
     } else if (split) {
-        launch_backward_layout<true>(need_x, need_w, grid, block, lds, s, ba);
+        if (lane_red)
+            launch_backward_layout<true, true>(need_x, need_w, grid, block, lds, s, ba);
+        else
+            launch_backward_layout<true, false>(need_x, need_w, grid, block, lds, s, ba);
     } else {
-        launch_backward_layout<false>(need_x, need_w, grid, block, lds, s, ba);
+        if (lane_red)
+            launch_backward_layout<false, true>(need_x, need_w, grid, block, lds, s, ba);
+        else
+            launch_backward_layout<false, false>(need_x, need_w, grid, block, lds, s, ba);
     }
 }
 
@@ -2138,7 +2206,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
     ProfiledLaunch* prof;
     prof_start(s, 1, &prof);
-    launch_backward(cs.exact, need_x, need_w, p.split, grid, block, p.lds_bytes, s, ba);
+    launch_backward(cs.exact, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
     err = hipGetLastError();
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "backward launch");
