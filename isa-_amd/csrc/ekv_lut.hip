@@ -1360,20 +1360,19 @@ template <bool PAIR, bool LDS>
 __global__ __launch_bounds__(1024) void bwd_measured_kernel(BwdArgs a) {
     extern __shared__ float4 s_mtab[];
     const float2* tab = reinterpret_cast<const float2*>(a.lut);
-    size_t table_floats4 = 0;
     if constexpr (LDS) {
         float2* s2 = reinterpret_cast<float2*>(s_mtab);
         for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s2[i] = tab[i];
         __syncthreads();
         tab = s2;
-        table_floats4 = (size_t)(a.NP + 1) / 2;
     }
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float* red = reinterpret_cast<float*>(s_mtab + table_floats4) + wave * (kBwdMB * kBwdKR * kRedStride);
     const int item = blockIdx.x * waves + wave;
     if (item >= a.n_items) return;
-    bwd_body<true, false>(a, MeasuredBwdCell<PAIR>{reinterpret_cast<const char*>(tab)}, a.xrec, a.wsT, red, item);
+    // dX partials reduced with lane exchanges: the LDS holds only the codebook
+    bwd_body<true, false, MeasuredBwdCell<PAIR>, true>(a, MeasuredBwdCell<PAIR>{reinterpret_cast<const char*>(tab)},
+                                                       a.xrec, a.wsT, nullptr, item);
 }
 
 // dX[m,k] = scale * sum over output blocks, in block order (deterministic); scale is 1 for
@@ -2255,7 +2254,7 @@ int check_glue(const isa_ekv_glue* glue, const isa_ekv_glue_grads* gg, bool need
 // Measured-codebook calls.
 // ----------------------------------------------------------------------------------
 
-constexpr size_t kMeasuredBwdLdsTableBytes = 88 * 1024;  // with 16 waves' dX buffers, within 160 KB
+constexpr size_t kMeasuredBwdLdsTableBytes = 128 * 1024;  // the dX reduction needs no LDS
 
 size_t measured_table_bytes(int n_seg, int n_rows) {
     return (size_t)round_up(((int64_t)n_seg * n_rows + 1) * 8, 256);
@@ -2425,7 +2424,7 @@ int run_measured_backward(const float* x, const short* ids_a, const short* ids_b
     ba.n_split = p.n_split;
     ba.m_chunk = p.m_chunk;
     ba.n_items = p.n_items;
-    const size_t lds_bytes = (lds ? round_up((int64_t)np * 8, 16) : 0) + p.lds_bytes;
+    const size_t lds_bytes = lds ? round_up((int64_t)np * 8, 16) : 0;
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
     ProfiledLaunch* prof;
     prof_start(s, 1, &prof);
