@@ -79,20 +79,24 @@ constexpr int kFwdORR = 4;        // outputs per lane, forward
 #define ISA_EKV_BWD_ORR 4
 #endif
 #ifndef ISA_EKV_BWD_KR
-#define ISA_EKV_BWD_KR 4
+#define ISA_EKV_BWD_KR 2
 #endif
 #ifndef ISA_EKV_BWD_SCHED
 #define ISA_EKV_BWD_SCHED 1
 #endif
 constexpr int kBwdORR = ISA_EKV_BWD_ORR;  // outputs per lane, backward (2 or 4)
-constexpr int kBwdKR = ISA_EKV_BWD_KR;    // inputs per wave, backward (2 or 4)
-constexpr int kBwdMB = 16 / kBwdKR;       // tokens per dX transpose batch: 16 slots per batch
+constexpr int kBwdKR = ISA_EKV_BWD_KR;    // inputs per wave, table backward (2 or 4)
+constexpr int kBwdKRExact = 4;            // inputs per wave, exact and measured backward
+constexpr int kRedSlots = 16;             // dX transpose buffer: tokens x inputs slots per batch
 static_assert((kBwdORR == 2 || kBwdORR == 4) && (kBwdKR == 2 || kBwdKR == 4), "backward tile");
 constexpr int kRedStride = 68;    // floats per slot row in the transpose buffer (64 + pad)
 constexpr int kPrepBlocksX = 1024; // prep blocks for the token side
 constexpr int kPrepBlocksW = 256; // prep blocks for the threshold side
 constexpr int kMaxEntriesFwd = 16384;
 constexpr int kMaxEntriesBwd = 8192;
+#ifndef ISA_EKV_BWD_MIN_BLOCKS
+#define ISA_EKV_BWD_MIN_BLOCKS 2  // table-backward blocks per CU the VGPR budget is held to (64 VGPRs at 2)
+#endif
 #ifndef ISA_EKV_BWD_LANE_RED
 #define ISA_EKV_BWD_LANE_RED 1  // dX reduction: 0 LDS buffers, 1 lane exchanges, 2 lane exchanges when the table crowds LDS
 #endif
@@ -978,14 +982,34 @@ __device__ inline int wave_rows_input() {
     return (int)q[0];
 }
 
+// Two inputs per wave: after the half exchange each 32-lane half holds one input's
+// pair sums; the row exchange of that register with itself folds rows 0+1 and 2+3.
+__device__ inline float wave_sum_rows2(float v0, float v1) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v1), false, false);
+    const float t = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+    float u = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    u += dpp_row_rotate<8>(u);
+    u += dpp_row_rotate<4>(u);
+    u += dpp_row_rotate<2>(u);
+    u += dpp_row_rotate<1>(u);
+    return u;
+}
+
+__device__ inline int wave_rows_input2() {
+    const auto p = __builtin_amdgcn_permlane32_swap(0u, 1u, false, false);
+    const auto q = __builtin_amdgcn_permlane16_swap(p[0], p[0], false, false);
+    return (int)q[0];
+}
+
 // LANE_RED: reduce each token's dX partials across the wave with lane exchanges
 // (wave_sum_rows4) instead of the LDS transpose buffer (red unused), freeing LDS for
 // tables too large to leave room for the buffers of 16 waves.
-template <bool NEED_X, bool NEED_W, class Cell, bool LANE_RED = false>
+template <int KR, bool NEED_X, bool NEED_W, class Cell, bool LANE_RED = false>
 __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4* xrec, const float2* wsT,
                                 float* red, int item) {
-    constexpr int ORR = kBwdORR, KR = kBwdKR, MB = kBwdMB;
-    static_assert(!LANE_RED || KR == 4, "the lane-exchange reduction sums four inputs per wave");
+    constexpr int ORR = kBwdORR, MB = kRedSlots / KR;
+    static_assert(!LANE_RED || KR == 4 || KR == 2, "the lane-exchange reduction sums two or four inputs per wave");
     const int lane = threadIdx.x & 63;
     // inputs vary fastest: the waves of a block share (output block, token split), so the
     // G row slices they stream are fetched once into the CU's L1 and reused
@@ -1018,7 +1042,7 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
     // transpose-buffer reduction role of this lane: slot = lane / 4, quarter = lane % 4
     const int my_slot = lane >> 2;
     const int my_quarter = lane & 3;
-    const int row_kk = LANE_RED ? wave_rows_input() : 0;  // input whose dX total this lane's row holds
+    const int row_kk = !LANE_RED ? 0 : (KR == 4 ? wave_rows_input() : wave_rows_input2());  // input of this row's dX total
 
     // token m's operands are prefetched one step ahead (scalar token records, vector grads)
     const float4* xbase = xrec + k0;
@@ -1084,9 +1108,14 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
             if (NEED_X) {
                 if constexpr (LANE_RED) {
                     if (m < m_end) {  // wave-uniform: every lane takes part in the exchanges
-                        const float sum = wave_sum_rows4(tv[0], tv[1], tv[2], tv[3]);
+                        float sum;
+                        if constexpr (KR == 4)
+                            sum = wave_sum_rows4(tv[0], tv[1], tv[2], tv[3]);
+                        else
+                            sum = wave_sum_rows2(tv[0], tv[1]);
                         const int k = k0 + row_kk;
-                        if ((lane & 15) == 0 && k < a.K) a.dx_part[((size_t)ob * a.M + m) * a.K + k] = sum;
+                        const bool writer = (lane & (KR == 4 ? 15 : 31)) == 0;  // one lane per input
+                        if (writer && k < a.K) a.dx_part[((size_t)ob * a.M + m) * a.K + k] = sum;
                     }
                 } else {
 #pragma unroll
@@ -1135,7 +1164,7 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
 }
 
 template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false>
-__global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
+__global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdArgs a) {
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
     for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
@@ -1153,8 +1182,7 @@ __global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int table_records = SPLIT ? kSplitRecords : a.NP;
     float* red = LANE_RED ? nullptr
-                          : reinterpret_cast<float*>(s_lut_bwd + table_records) +
-                                wave * (kBwdMB * kBwdKR * kRedStride);
+                          : reinterpret_cast<float*>(s_lut_bwd + table_records) + wave * (kRedSlots * kRedStride);
     const int item = blockIdx.x * waves + wave;
     if (item >= a.n_items) return;
     using Table = typename std::conditional<SPLIT, BwdTableSplit, BwdTableInterleaved>::type;
@@ -1164,11 +1192,11 @@ __global__ __launch_bounds__(1024) void bwd_kernel(BwdArgs a) {
     else
         t = BwdTableInterleaved{s_lut_bwd};
     if (fast)
-        bwd_body<NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(a, LutBwdCell<false, Table>{t, a.cmin, a.cmax},
-                                                                     a.xrec, a.wsT, red, item);
+        bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(
+            a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
     else
-        bwd_body<NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(a, LutBwdCell<true, Table>{t, a.cmin, a.cmax},
-                                                                    a.xrec, a.wsT, red, item);
+        bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(
+            a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
 }
 
 // Exact-formula backward (reference: ekv_triton.py:94-169): same work decomposition; LDS
@@ -1179,13 +1207,13 @@ __global__ __launch_bounds__(1024) void bwd_exact_kernel(BwdArgs a) {
     const bool fast = exact_operands_in_fast_range(a.partials);
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float* red = reinterpret_cast<float*>(s_red_exact) + wave * (kBwdMB * kBwdKR * kRedStride);
+    float* red = reinterpret_cast<float*>(s_red_exact) + wave * (kRedSlots * kRedStride);
     const int item = blockIdx.x * waves + wave;
     if (item >= a.n_items) return;
     if (fast)
-        bwd_body<NEED_X, NEED_W>(a, ExactFastBwdCell{a.k2}, a.xrec, a.wsT, red, item);
+        bwd_body<kBwdKRExact, NEED_X, NEED_W>(a, ExactFastBwdCell{a.k2}, a.xrec, a.wsT, red, item);
     else
-        bwd_body<NEED_X, NEED_W>(a, ExactGeneralBwdCell{a.c2}, a.xrec_alt, a.wsT_alt, red, item);
+        bwd_body<kBwdKRExact, NEED_X, NEED_W>(a, ExactGeneralBwdCell{a.c2}, a.xrec_alt, a.wsT_alt, red, item);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1371,7 +1399,7 @@ __global__ __launch_bounds__(1024) void bwd_measured_kernel(BwdArgs a) {
     const int item = blockIdx.x * waves + wave;
     if (item >= a.n_items) return;
     // dX partials reduced with lane exchanges: the LDS holds only the codebook
-    bwd_body<true, false, MeasuredBwdCell<PAIR>, true>(a, MeasuredBwdCell<PAIR>{reinterpret_cast<const char*>(tab)},
+    bwd_body<kBwdKRExact, true, false, MeasuredBwdCell<PAIR>, true>(a, MeasuredBwdCell<PAIR>{reinterpret_cast<const char*>(tab)},
                                                        a.xrec, a.wsT, nullptr, item);
 }
 
@@ -1782,8 +1810,12 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     p.Kp = round_up(K > 0 ? K : 1, 8);
     p.Op = round_up(O > 0 ? O : 1, 64 * kBwdORR);
     p.n_ob = (int)(p.Op / (64 * kBwdORR));
-    p.n_kb = (int)(p.Kp / kBwdKR);
-    const size_t red_bytes = (size_t)kBwdMB * kBwdKR * kRedStride * 4;
+    // inputs per wave: the table kernels take kBwdKR, the exact and measured kernels (planned
+    // with n_entries = 0) kBwdKRExact
+    const int kr = exact ? kBwdKRExact : kBwdKR;
+    const int mb = kRedSlots / kr;  // tokens per dX batch
+    p.n_kb = (int)(p.Kp / kr);
+    const size_t red_bytes = (size_t)kRedSlots * kRedStride * 4;
     p.split = !exact && ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
     const size_t lut_bytes = exact ? 0 : (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
     // dX reduction across the wave: lane exchanges (no LDS; measured 5% faster at N = 4096
@@ -1802,23 +1834,29 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     // counts from ~2 rounds up, take the smallest whose block count fills its rounds to
     // within 0.5% of the best fill (each split adds a dVth partial plane and per-item
     // setup, measured at well under the 1.6% a 98.4%-filled last round costs).
+    // blocks resident per CU: the table kernels fit ISA_EKV_BWD_MIN_BLOCKS 16-wave blocks in
+    // their VGPR budget when the LDS holds that many tables; the exact kernels fit one
+    const int64_t resident =
+        exact ? 1 : std::max<int64_t>(1, std::min<int64_t>(ISA_EKV_BWD_MIN_BLOCKS, (int64_t)(kLdsBytes / p.lds_bytes)));
     const int64_t base_items = (int64_t)p.n_ob * p.n_kb;
     const int64_t max_splits = (M + 63) / 64 > 0 ? (M + 63) / 64 : 1;  // >= 64 tokens per split
-    const int64_t min_splits = std::min<int64_t>(max_splits, (2 * kCUs * wpb + base_items - 1) / base_items);
+    const int64_t min_splits =
+        std::min<int64_t>(max_splits, (2 * kCUs * resident * wpb + base_items - 1) / base_items);
     const int64_t top_splits = std::min<int64_t>(max_splits, 4 * min_splits + 8);
     auto fill_of = [&](int64_t sp) {
-        const int64_t chunk = round_up((M + sp - 1) / sp, kBwdMB);
+        const int64_t chunk = round_up((M + sp - 1) / sp, mb);
         const int64_t n_sp = (M + chunk - 1) / chunk;
         const int64_t blocks = (base_items * n_sp + wpb - 1) / wpb;
-        const int64_t rounds = (blocks + kCUs - 1) / kCUs;
-        return (double)blocks / (double)(rounds * kCUs);
+        const int64_t slots = kCUs * resident;  // blocks resident per round
+        const int64_t rounds = (blocks + slots - 1) / slots;
+        return (double)blocks / (double)(rounds * slots);
     };
     double best_fill = 0.0;
     for (int64_t sp = min_splits; sp <= top_splits; ++sp) best_fill = std::max(best_fill, fill_of(sp));
     int64_t best_splits = min_splits;
     while (best_splits < top_splits && fill_of(best_splits) < best_fill - 0.005) ++best_splits;
-    p.m_chunk = (int)round_up((M + best_splits - 1) / best_splits, kBwdMB);
-    if (p.m_chunk < kBwdMB) p.m_chunk = kBwdMB;
+    p.m_chunk = (int)round_up((M + best_splits - 1) / best_splits, mb);
+    if (p.m_chunk < mb) p.m_chunk = mb;
     p.n_split = (int)((M + p.m_chunk - 1) / p.m_chunk);
     if (p.n_split < 1) p.n_split = 1;
     p.n_items = (int)(base_items * p.n_split);
