@@ -241,12 +241,12 @@ int isa_ekv_measured_backward(const float* x, const int16_t* ids_a, const int16_
 int isa_ekv_profile_begin(void);
 int isa_ekv_profile_end(double* ms, int* launches);
 
-/* Measurement aid, no reference counterpart: launches one 1024-thread block per CU, each
+/* Measurement aid, no reference counterpart: launches two 1024-thread blocks per CU, each
  * issuing 16 waves x 8 x `iterations` random LDS gathers of `record_bytes` (8: ds_read_b64,
  * 16: ds_read_b128) with per-lane indices uniform in [0, window_records), the access pattern
  * of the table kernels' gathers when a wave's thresholds span window_records table entries.
  * The caller times the launch on `stream` (asynchronous) to get the LDS gather rate that
- * bounds those kernels. out: device buffer of >= (CU count x 1024) floats (scratch results).
+ * bounds those kernels. out: device buffer of >= (2 x CU count x 1024) floats (scratch results).
  * *gathers_per_cu (nullable) receives the wave-level gathers each CU issues. */
 int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iterations, float* out, int64_t out_floats,
                              int* gathers_per_cu, void* stream);

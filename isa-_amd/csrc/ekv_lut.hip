@@ -1677,12 +1677,12 @@ __global__ __launch_bounds__(256) void glue_reduce_kernel(const float* __restric
 }
 
 // ----------------------------------------------------------------------------------
-// LDS gather probe (measurement aid for the LDS roofline of the table kernels). One
-// 1024-thread block per CU holds a 64 KB table; every lane issues gathers of REC-byte
+// LDS gather probe (measurement aid for the LDS roofline of the table kernels). Two
+// 1024-thread blocks per CU each hold a 64 KB table; every lane issues gathers of REC-byte
 // records (ds_read_b64 or ds_read_b128, the instructions the table kernels use) at 8 fixed
 // indices drawn uniformly from [0, window) per lane, i.e. the pattern of one table gather
 // whose lanes see thresholds spread over `window` records. Eight gathers are in flight per
-// wave between waits; 16 waves per CU overlap them. The results are summed into out so the
+// wave between waits; 32 waves per CU overlap them. The results are summed into out so the
 // reads stay live. Indices are < window <= kProbeLdsBytes / REC, inside the table.
 // ----------------------------------------------------------------------------------
 
@@ -1693,6 +1693,7 @@ typedef float probe_f4 __attribute__((ext_vector_type(4)));
 // inline-asm reads use would be removed by the compiler, leaving the reads outside the
 // workgroup's allocation.
 constexpr int kProbeLdsBytes = 65536;
+constexpr int kProbeBlocksPerCU = 2;  // 32 waves per CU, as the table kernels run
 
 template <int REC>
 __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int iters, unsigned seed, float* out) {
@@ -2750,18 +2751,20 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
     hipError_t err = hipGetDevice(&dev);
     if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (err != hipSuccess) return hip_fail(err, "device query");
-    if (!out || out_floats < (int64_t)cus * 1024)
-        return fail(ISA_EKV_EINVAL, "out needs %lld floats (one per thread of %d blocks)", (long long)cus * 1024, cus);
+    const int blocks = kProbeBlocksPerCU * cus;
+    if (!out || out_floats < (int64_t)blocks * 1024)
+        return fail(ISA_EKV_EINVAL, "out needs %lld floats (one per thread of %d blocks)", (long long)blocks * 1024,
+                    blocks);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (record_bytes == 8)
-        hipLaunchKernelGGL(lds_gather_probe_kernel<8>, dim3(cus), dim3(1024), kProbeLdsBytes, s, window_records,
+        hipLaunchKernelGGL(lds_gather_probe_kernel<8>, dim3(blocks), dim3(1024), kProbeLdsBytes, s, window_records,
                            iterations, 12345u, out);
     else
-        hipLaunchKernelGGL(lds_gather_probe_kernel<16>, dim3(cus), dim3(1024), kProbeLdsBytes, s, window_records,
+        hipLaunchKernelGGL(lds_gather_probe_kernel<16>, dim3(blocks), dim3(1024), kProbeLdsBytes, s, window_records,
                            iterations, 12345u, out);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "lds probe launch");
-    if (gathers_per_cu) *gathers_per_cu = 16 * 8 * iterations;
+    if (gathers_per_cu) *gathers_per_cu = kProbeBlocksPerCU * 16 * 8 * iterations;
     return 0;
 }
 

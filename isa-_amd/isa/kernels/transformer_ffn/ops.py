@@ -412,7 +412,7 @@ def probe_lds_gather(window_records: int, record_bytes: int = 8, iterations: int
     lib = _hip.load()
     dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    out = torch.empty(cus * 1024, dtype=torch.float32, device=dev)
+    out = torch.empty(2 * cus * 1024, dtype=torch.float32, device=dev)
     per_cu = ctypes.c_int(0)
     with torch.cuda.device(dev):
         stream = _hip.stream_handle(dev)
