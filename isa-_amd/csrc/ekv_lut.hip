@@ -82,7 +82,7 @@ constexpr int kFwdORR = 4;        // outputs per lane, forward
 #define ISA_EKV_BWD_KR 2
 #endif
 #ifndef ISA_EKV_BWD_SCHED
-#define ISA_EKV_BWD_SCHED 1
+#define ISA_EKV_BWD_SCHED 0
 #endif
 constexpr int kBwdORR = ISA_EKV_BWD_ORR;  // outputs per lane, backward (2 or 4)
 constexpr int kBwdKR = ISA_EKV_BWD_KR;    // inputs per wave, table backward (2 or 4)
@@ -1097,8 +1097,8 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
                         }
                     }
                     tv[kk] = fmaf(x2, xv.z, x1);  // r*sum(G L_D) - r^2/V_sat*sum(G L_I), in d units
-                    // keep one input's gathers in flight at a time: bounds register pressure
-                    // to the 128 VGPRs of a 16-wave block; other waves hide the LDS latency
+                    // optionally keep one input's gathers in flight at a time (a scheduling
+                    // fence); at two inputs per wave the compiler's own schedule is as fast
                     if (ISA_EKV_BWD_SCHED) __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
