@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 6
+#define ISA_EKV_ABI_VERSION 7
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -141,6 +141,10 @@ int isa_ekv_exact_backward(const float* x, const float* vth_pos, const float* vt
  *           idiff = isa_ekv_forward(v, ...)                               (clamped to idiff_min/max)
  *           y = clamp(idiff * r_tia[0], y_lo, y_hi)                       (if r_tia)
  *           out = y * adc_scale[o] + adc_shift[o]                         (if adc_scale)
+ * Output statistics of CIMLinear.forward's GPU branch (cim.py:194-198), on y (y = idiff
+ * without r_tia), after the forward in stream order:
+ *           stat_abs_max[0] = maximum(stat_abs_max[0], max |y|)          (NaN propagates)
+ *           stat_total[0] += M * O
  * All glue pointers are device memory and may be null (that step is skipped). */
 typedef struct isa_ekv_glue {
     const float* in_affine; /* [2] {scale, shift} */
@@ -149,6 +153,8 @@ typedef struct isa_ekv_glue {
     float y_lo, y_hi;
     const float* adc_scale; /* [O] */
     const float* adc_shift; /* [O], required with adc_scale */
+    float* stat_abs_max;    /* [1] fp32, forward only */
+    double* stat_total;     /* [1] fp64, forward only */
 } isa_ekv_glue;
 
 /* Gradients of the glue parameters written by isa_ekv_layer_backward (device memory; each

@@ -311,6 +311,7 @@ struct PrepArgs {
     float2* partials;         // [kPrepBlocksX + kPrepBlocksW]
     const float* in_affine;   // optional device {scale, shift}: the layer input is clamp(x*scale + shift)
     float in_lo, in_hi;
+    unsigned* stat_bits;      // optional: the forward's output-statistics word, cleared here
 };
 
 // Input voltage mapping clamp(x * scale + shift, lo, hi) (cim.py:37-39): product and sum
@@ -420,6 +421,7 @@ __device__ inline void prep_tokens(const PrepArgs& a, float& lo, float& hi) {
 }
 
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
+    if (a.stat_bits && blockIdx.x == 0 && threadIdx.x == 0) *a.stat_bits = 0u;
     float lo = INFINITY, hi = -INFINITY;
     if (blockIdx.x < kPrepBlocksX) {
         if (a.exact) {
@@ -751,24 +753,34 @@ struct FwdArgs {
     float y_lo, y_hi;
     const float* adc_scale; // device [O]: out = y * adc_scale[o] + adc_shift[o]
     const float* adc_shift;
+    unsigned* stat_bits;    // optional: atomic max of the |y| bit patterns (see layer_stat_bits)
     int glue;
 };
 
-// TIA gain, output clamp and ADC affine of cim.py:190-193 and :243, applied to one output
-// value: each tensor op's rounding kept (no contraction), NaN kept as torch.clamp does.
-__device__ inline float layer_glue(float v, float r, bool has_r, float lo, float hi, const float* a_scale,
-                                   const float* a_shift, int o) {
+// TIA gain and output clamp (cim.py:190-193) and the ADC affine (cim.py:243), applied to one
+// output value: each tensor op's rounding kept (no contraction), NaN kept as torch.clamp does.
+__device__ inline float layer_tia(float v, float r, bool has_r, float lo, float hi) {
 #pragma clang fp contract(off)
     if (has_r) {
         v = v * r;
         v = v != v ? v : fminf(fmaxf(v, lo), hi);
     }
+    return v;
+}
+
+__device__ inline float layer_adc(float v, const float* a_scale, const float* a_shift, int o) {
+#pragma clang fp contract(off)
     if (a_scale) {
         const float prod = v * a_scale[o];
         v = prod + a_shift[o];
     }
     return v;
 }
+
+// |y| as an unsigned bit pattern: non-negative floats order as their bits, and every NaN
+// pattern lies above +inf, so an unsigned max over them is the NaN-propagating max of
+// torch.maximum / Tensor.max (cim.py:194-198).
+__device__ inline unsigned layer_stat_bits(float y) { return __float_as_uint(y) & 0x7fffffffu; }
 
 template <int MR, int ORR, bool CLAMP_OUT, class Cell>
 __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2* xrec, const float2* wsT,
@@ -825,6 +837,7 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
     if (a.glue) {
         const bool has_r = a.r_tia != nullptr;
         const float r = has_r ? load_uniform1(a.r_tia) : 1.0f;
+        unsigned ymax = 0;
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
             const int m = m0 + i;
@@ -837,8 +850,15 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
                 if (o >= a.O) continue;
                 const float id = CLAMP_OUT ? fminf(fmaxf(acc[i][j], a.out_min), a.out_max) : acc[i][j] * a.out_scale;
                 if (irow) irow[o] = id;
-                orow[o] = layer_glue(id, r, has_r, a.y_lo, a.y_hi, a.adc_scale, a.adc_shift, o);
+                const float y = layer_tia(id, r, has_r, a.y_lo, a.y_hi);
+                ymax = max(ymax, layer_stat_bits(y));
+                orow[o] = layer_adc(y, a.adc_scale, a.adc_shift, o);
             }
+        }
+        if (a.stat_bits) {  // wave-uniform; every lane of the wave is here (m0 is wave-uniform)
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) ymax = max(ymax, (unsigned)__shfl_xor((int)ymax, d, 64));
+            if ((threadIdx.x & 63) == 0) atomicMax(a.stat_bits, ymax);
         }
         return;
     }
@@ -1526,7 +1546,8 @@ __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict_
 }
 
 // ----------------------------------------------------------------------------------
-// Layer glue backward (the reverse of layer_glue, cim.py:190-193 and :243 under autograd).
+// Layer glue backward (the reverse of layer_tia and layer_adc, cim.py:190-193 and :243 under
+// autograd).
 // For every (m, o) with G the gradient of the layer output:
 //   gy = G * adc_scale[o]                        (G without an ADC affine)
 //   y0 = idiff * r_tia, mask = lo <= y0 <= hi    (torch.clamp's backward mask)
@@ -1762,7 +1783,7 @@ __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int 
 struct FwdPlan {
     int64_t Kp, Op;
     int mr, n_mt, n_ot, blocks;
-    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, bytes;
+    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_stat, bytes;
 };
 
 FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
@@ -1789,7 +1810,9 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
     p.off_wsT_alt = off;
     if (exact) off += wsT_bytes;
     p.off_part = off;
-    off += (size_t)(kPrepBlocksX + kPrepBlocksW) * 8;
+    off += (size_t)round_up((kPrepBlocksX + kPrepBlocksW) * 8, 256);
+    p.off_stat = off;
+    off += 256;
     p.bytes = round_up((int64_t)off, 256);
     return p;
 }
@@ -2069,6 +2092,18 @@ PrepArgs make_prep(const CallSetup& cs, const float* x, const float* wp, const f
     return pa;
 }
 
+// Folds one forward's max |y| (bit pattern from the epilogue's atomic max) into the caller's
+// running statistics as cim.py:194-198 does: abs_max = maximum(abs_max, max|y|), NaN
+// propagating like torch.maximum; total += count.
+__global__ void stat_merge_kernel(const unsigned* bits, float* abs_max, double* total, double count) {
+    if (threadIdx.x != 0) return;
+    if (abs_max) {
+        const float m = __uint_as_float(*bits), cur = *abs_max;
+        *abs_max = cur != cur ? cur : (m != m || m > cur) ? m : cur;
+    }
+    if (total) *total += count;
+}
+
 int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg, int64_t M,
                 int64_t K, int64_t O, float v_sat, float out_min, float out_max, float* out, void* workspace,
                 size_t workspace_bytes, hipStream_t s, const isa_ekv_glue* glue = nullptr,
@@ -2080,8 +2115,11 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
     char* ws = static_cast<char*>(workspace);
     CallTimer call_timer(s, 2);
-    const PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 2, ws, p.off_xrec, p.off_wsT,
-                                  p.off_xrec_alt, p.off_wsT_alt, p.off_part, glue);
+    PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 2, ws, p.off_xrec, p.off_wsT,
+                            p.off_xrec_alt, p.off_wsT_alt, p.off_part, glue);
+    const bool stats = glue && (glue->stat_abs_max || glue->stat_total);
+    unsigned* stat_bits = stats ? reinterpret_cast<unsigned*>(ws + p.off_stat) : nullptr;
+    pa.stat_bits = stat_bits;
     hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "forward prep launch");
@@ -2108,6 +2146,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.y_hi = glue->y_hi;
         fa.adc_scale = glue->adc_scale;
         fa.adc_shift = glue->adc_shift;
+        fa.stat_bits = stat_bits;
     }
     size_t lds = 0;
     if (cs.exact) {
@@ -2128,6 +2167,12 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
     err = hipGetLastError();
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "forward launch");
+    if (stats) {
+        hipLaunchKernelGGL(stat_merge_kernel, dim3(1), dim3(64), 0, s, stat_bits, glue->stat_abs_max,
+                           glue->stat_total, (double)M * (double)O);
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "output statistics launch");
+    }
     return 0;
 }
 

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -70,6 +70,8 @@ class Glue(ctypes.Structure):
         ("y_hi", ctypes.c_float),
         ("adc_scale", ctypes.c_void_p),
         ("adc_shift", ctypes.c_void_p),
+        ("stat_abs_max", ctypes.c_void_p),
+        ("stat_total", ctypes.c_void_p),
     ]
 
 

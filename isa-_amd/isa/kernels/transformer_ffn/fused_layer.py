@@ -3,8 +3,9 @@
 No reference counterpart as a module: the reference runs the projection
 (`triton_lut_ekv_matmul`) and then separate PyTorch ops for the input voltage mapping
 (`cim.py:37-39`), the learnable TIA gain and output clamp (`cim.py:190-193`) and
-PhysicalFFN's ADC affine (`cim.py:243`). Here one library call does all of them in the
-forward (prep prologue, kernel epilogue) and one call the backward (a gradient prep pass
+PhysicalFFN's ADC affine (`cim.py:243`), and CIMLinear's optional output statistics
+(`cim.py:194-198`). Here one library call does all of them in the forward (prep prologue,
+kernel epilogue) and one call the backward (a gradient prep pass
 for the clamp mask, TIA and ADC gradients, and the mapping's backward inside the dX
 reduction). Values and gradients equal the unfused composition's up to the order of the
 parameter-gradient sums.
@@ -22,12 +23,13 @@ from isa.kernels.transformer_ffn import ops
 
 class FusedCIMLayerFn(torch.autograd.Function):
     """out = adc(clamp(clamp(Idiff(map(x)), lo, hi) * r_tia, lo, hi)); the optional pieces
-    (in_affine, r_tia, adc_scale/adc_shift) may be None."""
+    (in_affine, r_tia, adc_scale/adc_shift) may be None. stats: None or the (abs_max fp32,
+    total fp64) buffers the forward updates in place."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, in_affine: Optional[torch.Tensor],
                 r_tia: Optional[torch.Tensor], adc_scale: Optional[torch.Tensor], adc_shift: Optional[torch.Tensor],
-                cfg: Dict[str, Any], in_range: Tuple[float, float]):
+                cfg: Dict[str, Any], in_range: Tuple[float, float], stats=None):
         delta_min, delta_max, size = lut_range(cfg)
         lo = float(cfg.get("V_signed_min", -4.0))
         hi = float(cfg.get("V_signed_max", 4.0))
@@ -35,7 +37,8 @@ class FusedCIMLayerFn(torch.autograd.Function):
         out, idiff = ops.lut_layer_forward(
             x, wpos, wneg, fwd_records, size, delta_min, delta_max, float(cfg["V_sat"]), lo, hi,
             in_affine=in_affine, in_range=in_range, r_tia=r_tia, y_range=(lo, hi),
-            adc_scale=adc_scale, adc_shift=adc_shift)
+            adc_scale=adc_scale, adc_shift=adc_shift,
+            stat_abs_max=stats[0] if stats else None, stat_total=stats[1] if stats else None)
         ctx.save_for_backward(x, wpos, wneg, idiff, in_affine, r_tia, adc_scale, adc_shift)
         ctx.bwd_records = bwd_records
         ctx.meta = (delta_min, delta_max, size, float(cfg["V_sat"]), lo, hi, tuple(in_range))
@@ -68,13 +71,16 @@ class FusedCIMLayerFn(torch.autograd.Function):
             cast(res["d_adc_shift"], adc_shift) if need[6] else None,
             None,
             None,
+            None,
         )
 
 
 def fused_cim_layer(x2d: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, cfg: Dict[str, Any], *,
                     in_affine: Optional[torch.Tensor] = None, in_range: Tuple[float, float] = (0.0, 4.0),
                     r_tia: Optional[torch.Tensor] = None, adc_scale: Optional[torch.Tensor] = None,
-                    adc_shift: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """[M, K] -> [M, O] fp32 through FusedCIMLayerFn."""
+                    adc_shift: Optional[torch.Tensor] = None,
+                    stats: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+    """[M, K] -> [M, O] fp32 through FusedCIMLayerFn; stats = (abs_max, total) buffers to
+    update with the layer's output statistics, or None."""
     return FusedCIMLayerFn.apply(x2d, wpos, wneg, in_affine, r_tia, adc_scale, adc_shift, cfg,
-                                 (float(in_range[0]), float(in_range[1])))
+                                 (float(in_range[0]), float(in_range[1])), stats)

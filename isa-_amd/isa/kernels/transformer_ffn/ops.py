@@ -193,7 +193,8 @@ def exact_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad
     return gx, gp, gn
 
 
-def _glue_struct(in_affine, in_range, r_tia, y_range, adc_scale, adc_shift) -> "_hip.Glue":
+def _glue_struct(in_affine, in_range, r_tia, y_range, adc_scale, adc_shift, stat_abs_max=None,
+                 stat_total=None) -> "_hip.Glue":
     g = _hip.Glue()
     g.in_affine = _ptr(in_affine)
     g.in_lo, g.in_hi = (float(v) for v in in_range)
@@ -201,7 +202,19 @@ def _glue_struct(in_affine, in_range, r_tia, y_range, adc_scale, adc_shift) -> "
     g.y_lo, g.y_hi = (float(v) for v in y_range)
     g.adc_scale = _ptr(adc_scale)
     g.adc_shift = _ptr(adc_shift)
+    g.stat_abs_max = _ptr(stat_abs_max)
+    g.stat_total = _ptr(stat_total)
     return g
+
+
+def _stat_buffer(t: Optional[torch.Tensor], dtype: torch.dtype, name: str, device) -> Optional[torch.Tensor]:
+    """An output-statistics buffer the library updates in place: one contiguous element."""
+    if t is None:
+        return None
+    _require_cuda(t, name)
+    if t.device != device or t.dtype != dtype or t.numel() != 1 or not t.is_contiguous():
+        raise RuntimeError(f"{name} must be one contiguous {dtype} element on {device}")
+    return t
 
 
 def _glue_operand(t: Optional[torch.Tensor], numel: int, name: str, device) -> Optional[torch.Tensor]:
@@ -220,9 +233,12 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
                       n_entries: int, delta_min: float, delta_max: float, v_sat: float, idiff_min: float,
                       idiff_max: float, *, in_affine: Optional[torch.Tensor] = None, in_range=(0.0, 4.0),
                       r_tia: Optional[torch.Tensor] = None, y_range=(-4.0, 4.0),
-                      adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None):
+                      adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None,
+                      stat_abs_max: Optional[torch.Tensor] = None, stat_total: Optional[torch.Tensor] = None):
     """(out, idiff) of the LUT projection with its glue fused: x -> clamp(x*s + b) ->
-    Idiff (clamped to [idiff_min, idiff_max]) -> clamp(Idiff * r_tia) -> * adc_scale + adc_shift."""
+    Idiff (clamped to [idiff_min, idiff_max]) -> y = clamp(Idiff * r_tia) -> y * adc_scale +
+    adc_shift. stat_abs_max (fp32) and stat_total (fp64), one element each, are CIMLinear's
+    output statistics (cim.py:194-198), updated in place: maximum with max|y|, plus M * O."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
     if n_entries > MAX_ENTRIES_FORWARD:
@@ -234,12 +250,14 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
     a_c = _glue_operand(adc_shift, O, "adc_shift", dev)
     if (a_s is None) != (a_c is None):
         raise RuntimeError("adc_scale and adc_shift go together")
+    s_max = _stat_buffer(stat_abs_max, torch.float32, "stat_abs_max", dev)
+    s_tot = _stat_buffer(stat_total, torch.float64, "stat_total", dev)
     out = torch.empty((M, O), dtype=torch.float32, device=dev)
     idiff = torch.empty((M, O), dtype=torch.float32, device=dev)
     if M == 0 or O == 0:
         return out, idiff
     x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
-    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c)
+    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c, s_max, s_tot)
     ws = _workspace(lib.isa_ekv_layer_forward_workspace(M, K, O), dev)
     with torch.cuda.device(dev):
         rc = lib.isa_ekv_layer_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), fwd_records.data_ptr(), M, K, O,

@@ -14,8 +14,9 @@ exact-formula PyTorch path, `cim.py:201-214`).
 On the LUT path the elementwise glue around each projection (TIA gain and output clamp,
 and in `PhysicalFFN`/`HybridFFN` the input voltage mapping and the ADC affine) runs fused
 into the library's kernels (`fused_layer.py`); `ISA_EKV_FUSE_GLUE=0` (or setting
-`FUSE_GLUE = False` here) keeps it as separate PyTorch ops. Output-statistics tracking
-and non-fp32 inputs to the voltage mapping use the separate ops.
+`FUSE_GLUE = False` here) keeps it as separate PyTorch ops; output-statistics tracking
+(`cim.py:194-198`) is fused too. Non-fp32 inputs to the voltage mapping use the separate
+ops.
 """
 
 from __future__ import annotations
@@ -175,7 +176,7 @@ class CIMLinear(nn.Module):
     def fusable(self, x: torch.Tensor) -> bool:
         """Whether the fused LUT layer (projection + glue in the library) serves this input."""
         return (FUSE_GLUE and x.is_cuda and bool(self.cfg.get("use_triton", False))
-                and str(self.cfg.get("ekv_approx", "lut")).lower() == "lut" and not self.track_output_stats)
+                and str(self.cfg.get("ekv_approx", "lut")).lower() == "lut")
 
     def fused_forward(self, x: torch.Tensor, in_affine: Optional[torch.Tensor] = None,
                       in_range=(0.0, 4.0), adc_scale: Optional[torch.Tensor] = None,
@@ -185,9 +186,10 @@ class CIMLinear(nn.Module):
         b, n, in_f = x.shape
         assert in_f == self.in_features
         flat = x.reshape(b * n, in_f)
+        stats = (self._stat_abs_max, self._stat_total) if self.track_output_stats else None
         out = fused_cim_layer(flat, self.vth_pos, self.vth_neg, self.cfg, in_affine=in_affine, in_range=in_range,
                               r_tia=self.r_tia.to(device=x.device, dtype=torch.float32).reshape(1),
-                              adc_scale=adc_scale, adc_shift=adc_shift)
+                              adc_scale=adc_scale, adc_shift=adc_shift, stats=stats)
         return out.reshape(b, n, self.out_features)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -129,3 +129,53 @@ def test_fused_layer_direct_call_and_degenerate_k(cuda_device):
     out.backward(gz)
     assert torch.allclose(c.grad, gz.sum(0)) and float(a.grad.abs().max()) == 0.0
     assert float(r.grad.abs().max()) == 0.0 and float(aff.grad.abs().max()) == 0.0
+
+
+def test_output_stats_fused_equal_unfused(cuda_device):
+    """Output-statistics tracking (cim.py:194-198) in the fused epilogue: after two forwards
+    the counts and running max |y| equal the separate-op path's; a larger running max is
+    kept; NaN outputs (a NaN TIA gain) make the max NaN as torch.maximum does."""
+    import math
+
+    from isa.operators.cim import PhysicalFFN
+
+    print("[case] fused output statistics", flush=True)
+    torch.manual_seed(14)
+    ffn = PhysicalFFN(64, 200, flash_cfg(4096)).to(cuda_device)
+    with torch.no_grad():
+        ffn.fc1.r_tia_base.fill_(4e6)  # |idiff| reaches ~2e-6 A: some outputs clamp at +-4
+    xs = [torch.randn(2, 37, 64, device=cuda_device) * 2.0, torch.randn(1, 23, 64, device=cuda_device)]
+    gain = float(ffn.fc2.r_tia_base)
+
+    def stats(fused, preset=0.0, nan_gain=False):
+        from isa.operators import cim
+
+        saved = cim.FUSE_GLUE
+        cim.FUSE_GLUE = fused
+        try:
+            for layer in (ffn.fc1, ffn.fc2):
+                layer.set_output_stats_tracking(True, reset=True)
+                layer._stat_abs_max.fill_(preset)
+            with torch.no_grad():
+                ffn.fc2.r_tia_base.fill_(float("nan") if nan_gain else gain)
+                for x in xs:
+                    ffn(x)
+            torch.cuda.synchronize()
+            return [layer.output_stats() for layer in (ffn.fc1, ffn.fc2)]
+        finally:
+            cim.FUSE_GLUE = saved
+            with torch.no_grad():
+                ffn.fc2.r_tia_base.fill_(gain)
+            for layer in (ffn.fc1, ffn.fc2):
+                layer.set_output_stats_tracking(False)
+
+    fused, plain = stats(True), stats(False)
+    assert fused == plain, (fused, plain)
+    assert fused[0]["total"] == (2 * 37 + 23) * 200 and fused[1]["total"] == (2 * 37 + 23) * 64
+    assert fused[0]["preclamp_abs_max"] == 4.0  # clamped outputs reached the bound
+    assert stats(True, preset=100.0) == stats(False, preset=100.0)
+    assert stats(True, preset=100.0)[1]["preclamp_abs_max"] == 100.0
+    nan_fused, nan_plain = stats(True, nan_gain=True), stats(False, nan_gain=True)
+    assert nan_fused[0] == nan_plain[0] == fused[0]
+    assert math.isnan(nan_fused[1]["preclamp_abs_max"]) and math.isnan(nan_plain[1]["preclamp_abs_max"])
+    assert nan_fused[1]["total"] == nan_plain[1]["total"]
