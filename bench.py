@@ -494,7 +494,7 @@ def main() -> int:
         "unit": "TOP/s",
         "frac": round(achieved / peak, 4),
         "traffic": None if exact else measured_traffic(args.config),
-        "kernel": ("bwd_exact_kernel<true,true>" if exact else "bwd_kernel<true,true,true>")
+        "kernel": ("bwd_exact_kernel<true,true>" if exact else "bwd_kernel<true,true,true,true>")
                   + " (backward main kernel, dominant)",
         "work": f"{bwd_instr} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
         "avg_launch_ms": round(bwd_avg, 4),
