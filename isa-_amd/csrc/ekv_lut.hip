@@ -884,12 +884,19 @@ constexpr int kFwdWaves = 8;
 // XCD-aware order: consecutive hardware block ids go round-robin over 8 XCDs; remap so
 // the blocks of one XCD walk consecutive token tiles of the same output block and share
 // that output block's threshold columns in their L2. Returns false for waves past M.
-__device__ inline bool fwd_tile(const FwdArgs& a, int MR, int& m0, int& o_lane) {
+// Block index -> work index so that consecutive work indices run on one XCD: the hardware
+// hands workgroups to the 8 XCDs round-robin by block index, so XCD x gets blocks x, x + 8,
+// ...; they are given the contiguous work range [x * per_xcd, (x + 1) * per_xcd) (the blocks
+// past 8 * per_xcd keep their index). Work that shares operands then shares that XCD's L2.
+__device__ inline int xcd_work_index() {
     const int nb = gridDim.x;
     const int bid = blockIdx.x;
     const int per_xcd = nb / 8;
-    int t = bid;
-    if (per_xcd > 0 && bid < per_xcd * 8) t = (bid % 8) * per_xcd + bid / 8;
+    return (per_xcd > 0 && bid < per_xcd * 8) ? (bid % 8) * per_xcd + bid / 8 : bid;
+}
+
+__device__ inline bool fwd_tile(const FwdArgs& a, int MR, int& m0, int& o_lane) {
+    const int t = xcd_work_index();
     const int tile_m = t % a.n_mt;
     const int tile_o = t / a.n_mt;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1032,7 +1039,9 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
     static_assert(!LANE_RED || KR == 4 || KR == 2, "the lane-exchange reduction sums two or four inputs per wave");
     const int lane = threadIdx.x & 63;
     // inputs vary fastest: the waves of a block share (output block, token split), so the
-    // G row slices they stream are fetched once into the CU's L1 and reused
+    // G row slices they stream are fetched once into the CU's L1 and reused (blocks keep the
+    // hardware's round-robin XCD order: grouping one (output block, token split) on one XCD
+    // halves fc1's HBM reads of G but slows fc2 as much as it speeds fc1)
     const int kb = item % a.n_kb;
     const int rest = item / a.n_kb;
     const int ob = rest % a.n_ob;
