@@ -881,9 +881,6 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
 
 constexpr int kFwdWaves = 8;
 
-// XCD-aware order: consecutive hardware block ids go round-robin over 8 XCDs; remap so
-// the blocks of one XCD walk consecutive token tiles of the same output block and share
-// that output block's threshold columns in their L2. Returns false for waves past M.
 // Block index -> work index so that consecutive work indices run on one XCD: the hardware
 // hands workgroups to the 8 XCDs round-robin by block index, so XCD x gets blocks x, x + 8,
 // ...; they are given the contiguous work range [x * per_xcd, (x + 1) * per_xcd) (the blocks
@@ -895,6 +892,9 @@ __device__ inline int xcd_work_index() {
     return (per_xcd > 0 && bid < per_xcd * 8) ? (bid % 8) * per_xcd + bid / 8 : bid;
 }
 
+// Forward tile of this wave, in XCD-aware order: the blocks of one XCD walk consecutive token
+// tiles of the same output block and share that output block's threshold columns in their
+// L2. Returns false for waves past M.
 __device__ inline bool fwd_tile(const FwdArgs& a, int MR, int& m0, int& o_lane) {
     const int t = xcd_work_index();
     const int tile_m = t % a.n_mt;
