@@ -755,6 +755,17 @@ struct FwdArgs {
     const float* adc_shift;
     unsigned* stat_bits;    // optional: atomic max of the |y| bit patterns (see layer_stat_bits)
     int glue;
+    // K split (small problems): n_split > 1 ranges of k_chunk padded inputs; each writes its
+    // raw partial sums to split_part[s][M][O] and split_reduce_kernel finishes the outputs
+    int n_split, k_chunk;
+    float* split_part;
+};
+
+// The work of one forward wave.
+struct FwdTile {
+    int m0, o_lane;    // first token of the wave, first output of the lane
+    int k_lo, k_hi;    // padded-input range summed by this wave
+    float* split_out;  // K split: this split's [M][O] partial sums (null: full sums, epilogue here)
 };
 
 // TIA gain and output clamp (cim.py:190-193) and the ADC affine (cim.py:243), applied to one
@@ -784,7 +795,8 @@ __device__ inline unsigned layer_stat_bits(float y) { return __float_as_uint(y) 
 
 template <int MR, int ORR, bool CLAMP_OUT, class Cell>
 __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2* xrec, const float2* wsT,
-                                int m0, int o_lane) {
+                                const FwdTile& tile) {
+    const int m0 = tile.m0, o_lane = tile.o_lane;
     float acc[MR][ORR];
 #pragma unroll
     for (int i = 0; i < MR; ++i)
@@ -801,8 +813,8 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
     const size_t wstride = (size_t)a.Op / 2;  // float4 per k row
 
     constexpr int KU = ISA_EKV_FWD_TOKOPS / MR >= 1 ? ISA_EKV_FWD_TOKOPS / MR : 1;  // token records per step
-    static_assert(KU >= 1 && 8 % KU == 0, "Kp is a multiple of 8");
-    for (int k0 = 0; k0 < a.Kp; k0 += KU) {
+    static_assert(KU >= 1 && 8 % KU == 0, "Kp and the K-split ranges are multiples of 8");
+    for (int k0 = tile.k_lo; k0 < tile.k_hi; k0 += KU) {
         float2 w[KU][ORR];
 #pragma unroll
         for (int kk = 0; kk < KU; ++kk)
@@ -833,6 +845,18 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
                 }
             }
         }
+    }
+    if (tile.split_out) {  // partial sums over this K range; split_reduce_kernel does the rest
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+            const int m = m0 + i;
+            if (m >= a.M) break;
+            float* prow = tile.split_out + (size_t)m * a.O;
+#pragma unroll
+            for (int j = 0; j < ORR; ++j)
+                if (o_lane + j < a.O) prow[o_lane + j] = acc[i][j];
+        }
+        return;
     }
     if (a.glue) {
         const bool has_r = a.r_tia != nullptr;
@@ -893,43 +917,57 @@ __device__ inline int xcd_work_index() {
 }
 
 // Forward tile of this wave, in XCD-aware order: the blocks of one XCD walk consecutive token
-// tiles of the same output block and share that output block's threshold columns in their
-// L2. Returns false for waves past M.
-__device__ inline bool fwd_tile(const FwdArgs& a, int MR, int& m0, int& o_lane) {
-    const int t = xcd_work_index();
-    const int tile_m = t % a.n_mt;
-    const int tile_o = t / a.n_mt;
+// tiles of the same output block (and K split) and share that output block's threshold
+// columns in their L2. Returns false for waves past M. Launches planned without a K split
+// use SPLITS = false, which compiles them as if the split did not exist.
+template <bool SPLITS>
+__device__ inline bool fwd_tile(const FwdArgs& a, int MR, FwdTile& t) {
+    int w = xcd_work_index();
+    const int tiles = a.n_mt * a.n_ot;
+    const int split = SPLITS && a.n_split > 1 ? w / tiles : 0;
+    w -= split * tiles;
+    const int tile_m = w % a.n_mt;
+    const int tile_o = w / a.n_mt;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    m0 = (tile_m * kFwdWaves + wave) * MR;
-    o_lane = tile_o * 64 * kFwdORR + lane * kFwdORR;
-    return m0 < a.M;
+    t.m0 = (tile_m * kFwdWaves + wave) * MR;
+    t.o_lane = tile_o * 64 * kFwdORR + lane * kFwdORR;
+    if (SPLITS && a.n_split > 1) {
+        t.k_lo = split * a.k_chunk;
+        t.k_hi = min(a.Kp, t.k_lo + a.k_chunk);
+        t.split_out = a.split_part + (size_t)split * a.M * a.O;
+    } else {
+        t.k_lo = 0;
+        t.k_hi = a.Kp;
+        t.split_out = nullptr;
+    }
+    return t.m0 < a.M;
 }
 
-template <int MR>
+template <int MR, bool SPLITS>
 __global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
     for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
     const bool fast = coords_in_padded_range(a.partials, a.NP);
     __syncthreads();
-    int m0, o_lane;
-    if (!fwd_tile(a, MR, m0, o_lane)) return;
+    FwdTile t;
+    if (!fwd_tile<SPLITS>(a, MR, t)) return;
     if (fast)
-        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, m0, o_lane);
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, t);
     else
-        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, m0, o_lane);
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, t);
 }
 
 // Exact-formula forward (reference: ekv_triton.py:69-91): same tiling, no table.
-template <int MR>
+template <int MR, bool SPLITS>
 __global__ __launch_bounds__(kFwdWaves * 64) void fwd_exact_kernel(FwdArgs a) {
     const bool fast = exact_operands_in_fast_range(a.partials);
-    int m0, o_lane;
-    if (!fwd_tile(a, MR, m0, o_lane)) return;
+    FwdTile t;
+    if (!fwd_tile<SPLITS>(a, MR, t)) return;
     if (fast)
-        fwd_body<MR, kFwdORR, false>(a, ExactFastFwdCell{a.k2}, a.xrec, a.wsT, m0, o_lane);
+        fwd_body<MR, kFwdORR, false>(a, ExactFastFwdCell{a.k2}, a.xrec, a.wsT, t);
     else
-        fwd_body<MR, kFwdORR, false>(a, ExactGeneralFwdCell{a.c2}, a.xrec_alt, a.wsT_alt, m0, o_lane);
+        fwd_body<MR, kFwdORR, false>(a, ExactGeneralFwdCell{a.c2}, a.xrec_alt, a.wsT_alt, t);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1408,10 +1446,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void fwd_measured_kernel(FwdArgs a)
         __syncthreads();
         tab = s_tab;
     }
-    int m0, o_lane;
-    if (!fwd_tile(a, MR, m0, o_lane)) return;
-    fwd_body<MR, kFwdORR, false>(a, MeasuredFwdCell<PAIR>{reinterpret_cast<const char*>(tab)}, a.xrec, a.wsT, m0,
-                                 o_lane);
+    FwdTile t;
+    if (!fwd_tile<false>(a, MR, t)) return;
+    fwd_body<MR, kFwdORR, false>(a, MeasuredFwdCell<PAIR>{reinterpret_cast<const char*>(tab)}, a.xrec, a.wsT, t);
 }
 
 template <bool PAIR, bool LDS>
@@ -1793,10 +1830,18 @@ __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int 
 struct FwdPlan {
     int64_t Kp, Op;
     int mr, n_mt, n_ot, blocks;
-    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_stat, bytes;
+    int n_split, k_chunk;  // K split of small problems (n_split = 1: none)
+    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_stat, off_split, bytes;
 };
 
-FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
+constexpr int64_t kResidentWaves = 256 * 32;  // 32 waves on each of the 256 CUs
+#ifndef ISA_EKV_FWD_MIN_SPLIT_K
+#define ISA_EKV_FWD_MIN_SPLIT_K 32
+#endif
+constexpr int kFwdMaxSplit = 8;
+constexpr int kFwdMinSplitInputs = ISA_EKV_FWD_MIN_SPLIT_K;  // padded inputs per K split, at least
+
+FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_split = true) {
     FwdPlan p{};
     p.Kp = round_up(K > 0 ? K : 1, 8);
     p.Op = round_up(O > 0 ? O : 1, 64 * kFwdORR);
@@ -1807,7 +1852,16 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
     while (p.mr > 2 && ((M + p.mr - 1) / p.mr) * p.n_ot < waves_target) p.mr /= 2;
     const int64_t tokens_per_block = (int64_t)kFwdWaves * p.mr;
     p.n_mt = (int)((M + tokens_per_block - 1) / tokens_per_block);
-    p.blocks = p.n_mt * p.n_ot;
+    // problems too small to fill the chip even at two tokens per wave split K: each split
+    // sums k_chunk padded inputs into its own partial plane, finished by split_reduce_kernel
+    const int64_t waves = (int64_t)p.n_mt * kFwdWaves * p.n_ot;
+    int split = 1;
+    while (allow_split && split < kFwdMaxSplit && waves * split < kResidentWaves &&
+           p.Kp / (2 * split) >= kFwdMinSplitInputs)
+        split *= 2;
+    p.k_chunk = (int)round_up((p.Kp + split - 1) / split, 8);
+    p.n_split = (int)((p.Kp + p.k_chunk - 1) / p.k_chunk);
+    p.blocks = p.n_mt * p.n_ot * p.n_split;
     const size_t xrec_bytes = (size_t)round_up((int64_t)M * p.Kp * 8, 256);
     const size_t wsT_bytes = (size_t)round_up(p.Kp * p.Op * 8, 256);
     size_t off = 0;
@@ -1823,6 +1877,8 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact) {
     off += (size_t)round_up((kPrepBlocksX + kPrepBlocksW) * 8, 256);
     p.off_stat = off;
     off += 256;
+    p.off_split = off;
+    if (p.n_split > 1) off += (size_t)round_up((int64_t)p.n_split * M * O * 4, 256);
     p.bytes = round_up((int64_t)off, 256);
     return p;
 }
@@ -1940,23 +1996,31 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_
         p[e] = 0.0f;
 }
 
-void launch_forward(bool exact, int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+template <bool SPLITS>
+void launch_forward_split(bool exact, int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
     const dim3 block(kFwdWaves * 64);
     if (exact) {
         if (mr == 8)
-            hipLaunchKernelGGL(fwd_exact_kernel<8>, grid, block, 0, s, fa);
+            hipLaunchKernelGGL((fwd_exact_kernel<8, SPLITS>), grid, block, 0, s, fa);
         else if (mr == 4)
-            hipLaunchKernelGGL(fwd_exact_kernel<4>, grid, block, 0, s, fa);
+            hipLaunchKernelGGL((fwd_exact_kernel<4, SPLITS>), grid, block, 0, s, fa);
         else
-            hipLaunchKernelGGL(fwd_exact_kernel<2>, grid, block, 0, s, fa);
+            hipLaunchKernelGGL((fwd_exact_kernel<2, SPLITS>), grid, block, 0, s, fa);
         return;
     }
     if (mr == 8)
-        hipLaunchKernelGGL(fwd_kernel<8>, grid, block, lds, s, fa);
+        hipLaunchKernelGGL((fwd_kernel<8, SPLITS>), grid, block, lds, s, fa);
     else if (mr == 4)
-        hipLaunchKernelGGL(fwd_kernel<4>, grid, block, lds, s, fa);
+        hipLaunchKernelGGL((fwd_kernel<4, SPLITS>), grid, block, lds, s, fa);
     else
-        hipLaunchKernelGGL(fwd_kernel<2>, grid, block, lds, s, fa);
+        hipLaunchKernelGGL((fwd_kernel<2, SPLITS>), grid, block, lds, s, fa);
+}
+
+void launch_forward(bool exact, int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+    if (fa.n_split > 1)
+        launch_forward_split<true>(exact, mr, grid, lds, s, fa);
+    else
+        launch_forward_split<false>(exact, mr, grid, lds, s, fa);
 }
 
 template <bool SPLIT, bool LANE_RED>
@@ -2114,6 +2178,49 @@ __global__ void stat_merge_kernel(const unsigned* bits, float* abs_max, double* 
     if (total) *total += count;
 }
 
+// Finishes a K-split forward (fwd_body wrote each split's partial sums): the splits are summed
+// in split order, then clamped (LUT) or scaled (exact, measured) and given the layer glue
+// exactly as fwd_body's epilogue does. Grid-stride over the [M][O] outputs.
+__global__ __launch_bounds__(256) void split_reduce_kernel(FwdArgs a, int clamp_out) {
+    const int64_t n = (int64_t)a.M * a.O;
+    const bool has_r = a.glue && a.r_tia != nullptr;
+    const float r = has_r ? load_uniform1(a.r_tia) : 1.0f;
+    unsigned ymax = 0;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+        float v = a.split_part[e];
+        for (int sp = 1; sp < a.n_split; ++sp) v += a.split_part[(size_t)sp * n + e];
+        const float id = clamp_out ? fminf(fmaxf(v, a.out_min), a.out_max) : v * a.out_scale;
+        if (!a.glue) {
+            a.out[e] = id;
+            continue;
+        }
+        if (a.idiff) a.idiff[e] = id;
+        const float y = layer_tia(id, r, has_r, a.y_lo, a.y_hi);
+        ymax = max(ymax, layer_stat_bits(y));
+        a.out[e] = layer_adc(y, a.adc_scale, a.adc_shift, (int)(e % a.O));
+    }
+    if (a.stat_bits) {  // every lane of the wave is here: the loop has no early exit
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) ymax = max(ymax, (unsigned)__shfl_xor((int)ymax, d, 64));
+        if ((threadIdx.x & 63) == 0) atomicMax(a.stat_bits, ymax);
+    }
+}
+
+// Points a forward launch at the plan's K split (no-op without one).
+void set_split(const FwdPlan& p, char* ws, FwdArgs& fa) {
+    fa.n_split = p.n_split;
+    fa.k_chunk = p.k_chunk;
+    fa.split_part = p.n_split > 1 ? reinterpret_cast<float*>(ws + p.off_split) : nullptr;
+}
+
+hipError_t finish_split(const FwdPlan& p, const FwdArgs& fa, bool clamp_out, hipStream_t s) {
+    if (p.n_split <= 1) return hipSuccess;
+    const int64_t n = (int64_t)fa.M * fa.O;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, fa, clamp_out ? 1 : 0);
+    return hipGetLastError();
+}
+
 int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg, int64_t M,
                 int64_t K, int64_t O, float v_sat, float out_min, float out_max, float* out, void* workspace,
                 size_t workspace_bytes, hipStream_t s, const isa_ekv_glue* glue = nullptr,
@@ -2171,10 +2278,12 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.out_scale = 1.0f;
         lds = (size_t)fa.NP * 8;
     }
+    set_split(p, ws, fa);
     ProfiledLaunch* prof;
     prof_start(s, 0, &prof);
     launch_forward(cs.exact, p.mr, dim3(p.blocks), lds, s, fa);
     err = hipGetLastError();
+    if (err == hipSuccess) err = finish_split(p, fa, !cs.exact, s);
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "forward launch");
     if (stats) {
@@ -2417,7 +2526,7 @@ int run_measured_forward(const float* x, const short* ids_a, const short* ids_b,
                          hipStream_t s) {
     if (M == 0 || O == 0) return 0;
     if (!out) return fail(ISA_EKV_EINVAL, "out is null");
-    const FwdPlan p = plan_forward(M, K, O, false);
+    const FwdPlan p = plan_forward(M, K, O, false, false);
     const size_t tbytes = measured_table_bytes(cb->n_seg, cb->n_rows);
     const size_t need = p.bytes + tbytes;
     if (!workspace || workspace_bytes < need)
@@ -2753,7 +2862,7 @@ int isa_ekv_layer_backward(const float* x, const float* vth_pos, const float* vt
 
 size_t isa_ekv_measured_forward_workspace(int64_t M, int64_t K, int64_t O, int n_seg, int n_rows) {
     if (M < 0 || K < 0 || O < 0 || n_seg < 1 || n_rows < 1) return 0;
-    return plan_forward(M, K, O, false).bytes + measured_table_bytes(n_seg, n_rows);
+    return plan_forward(M, K, O, false, false).bytes + measured_table_bytes(n_seg, n_rows);
 }
 
 size_t isa_ekv_measured_backward_workspace(int64_t M, int64_t K, int64_t O, int n_seg, int n_rows) {
