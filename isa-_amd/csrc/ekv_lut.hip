@@ -1835,6 +1835,10 @@ struct FwdPlan {
 };
 
 constexpr int64_t kResidentWaves = 256 * 32;  // 32 waves on each of the 256 CUs
+#ifndef ISA_EKV_BWD_MIN_SPLIT_M
+#define ISA_EKV_BWD_MIN_SPLIT_M 16
+#endif
+constexpr int64_t kBwdMinSplitTokens = ISA_EKV_BWD_MIN_SPLIT_M;  // tokens per backward token split, at least
 #ifndef ISA_EKV_FWD_MIN_SPLIT_K
 #define ISA_EKV_FWD_MIN_SPLIT_K 32
 #endif
@@ -1929,7 +1933,7 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     const int64_t resident =
         exact ? 1 : std::max<int64_t>(1, std::min<int64_t>(ISA_EKV_BWD_MIN_BLOCKS, (int64_t)(kLdsBytes / p.lds_bytes)));
     const int64_t base_items = (int64_t)p.n_ob * p.n_kb;
-    const int64_t max_splits = (M + 63) / 64 > 0 ? (M + 63) / 64 : 1;  // >= 64 tokens per split
+    const int64_t max_splits = std::max<int64_t>(1, (M + kBwdMinSplitTokens - 1) / kBwdMinSplitTokens);
     const int64_t min_splits =
         std::min<int64_t>(max_splits, (2 * kCUs * resident * wpb + base_items - 1) / base_items);
     const int64_t top_splits = std::min<int64_t>(max_splits, 4 * min_splits + 8);

@@ -40,6 +40,7 @@ SHAPES = [
     (31, 67, 19),      # (test_exact_direct_conv.py:167-171)
     (5, 8, 256),
     (70, 129, 300),    # ragged in every dimension
+    (40, 260, 300),    # forward K split into 7 ranges of 40 padded inputs, the last one short
     (64, 192, 768),
     (520, 192, 768),   # config 1: ViT-S up-projection, full size
 ]
