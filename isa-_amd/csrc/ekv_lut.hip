@@ -755,7 +755,7 @@ struct FwdArgs {
     const float* adc_shift;
     unsigned* stat_bits;    // optional: atomic max of the |y| bit patterns (see layer_stat_bits)
     int glue;
-    // K split (small problems): n_split > 1 ranges of k_chunk padded inputs; each writes its
+    // K split (see plan_forward): n_split > 1 ranges of k_chunk padded inputs; each writes its
     // raw partial sums to split_part[s][M][O] and split_reduce_kernel finishes the outputs
     int n_split, k_chunk;
     float* split_part;
@@ -1834,7 +1834,6 @@ struct FwdPlan {
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_stat, off_split, bytes;
 };
 
-constexpr int64_t kResidentWaves = 256 * 32;  // 32 waves on each of the 256 CUs
 #ifndef ISA_EKV_BWD_MIN_SPLIT_M
 #define ISA_EKV_BWD_MIN_SPLIT_M 16
 #endif
@@ -1850,19 +1849,24 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
     p.Kp = round_up(K > 0 ? K : 1, 8);
     p.Op = round_up(O > 0 ? O : 1, 64 * kFwdORR);
     p.n_ot = (int)(p.Op / (64 * kFwdORR));
-    // choose tokens per wave so the grid covers the chip several times over
+    // Tokens per wave and K split. Each wave streams its 256 outputs' threshold records once
+    // per input for its MR tokens, so MR sets the threshold traffic per cell (8 / MR bytes
+    // from L2); take the largest MR whose waves, times a K split, cover the chip
+    // ISA_EKV_FWD_WT times over (MR = 2 and the largest split when none does). Each K split
+    // sums k_chunk padded inputs into its own partial plane, finished by split_reduce_kernel.
     const int64_t waves_target = (int64_t)ISA_EKV_FWD_WT * 256 * 16;
-    p.mr = 8;
-    while (p.mr > 2 && ((M + p.mr - 1) / p.mr) * p.n_ot < waves_target) p.mr /= 2;
+    int sp_max = 1;
+    while (allow_split && sp_max < kFwdMaxSplit && p.Kp / (2 * sp_max) >= kFwdMinSplitInputs) sp_max *= 2;
+    int split = 1;
+    for (p.mr = 8;; p.mr /= 2) {
+        const int64_t waves = round_up(M, (int64_t)kFwdWaves * p.mr) / p.mr * p.n_ot;
+        if (p.mr == 2 || waves * sp_max >= waves_target) {
+            while (split < sp_max && waves * split < waves_target) split *= 2;
+            break;
+        }
+    }
     const int64_t tokens_per_block = (int64_t)kFwdWaves * p.mr;
     p.n_mt = (int)((M + tokens_per_block - 1) / tokens_per_block);
-    // problems too small to fill the chip even at two tokens per wave split K: each split
-    // sums k_chunk padded inputs into its own partial plane, finished by split_reduce_kernel
-    const int64_t waves = (int64_t)p.n_mt * kFwdWaves * p.n_ot;
-    int split = 1;
-    while (allow_split && split < kFwdMaxSplit && waves * split < kResidentWaves &&
-           p.Kp / (2 * split) >= kFwdMinSplitInputs)
-        split *= 2;
     p.k_chunk = (int)round_up((p.Kp + split - 1) / split, 8);
     p.n_split = (int)((p.Kp + p.k_chunk - 1) / p.k_chunk);
     p.blocks = p.n_mt * p.n_ot * p.n_split;
