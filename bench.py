@@ -499,7 +499,9 @@ def main() -> int:
         "work": f"{bwd_instr} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
         "avg_launch_ms": round(bwd_avg, 4),
         "forward_kernel": {
-            "kernel": "fwd_exact_kernel" if exact else "fwd_kernel", "avg_launch_ms": round(fwd_avg, 4),
+            "kernel": ("fwd_exact_kernel" if exact else "fwd_kernel")
+                      + " (with split_reduce_kernel where the plan splits K)",
+            "avg_launch_ms": round(fwd_avg, 4),
             "achieved": round(fwd_cells_s * fwd_instr / 1e12, 3),
             "frac": round(fwd_cells_s * fwd_instr / VALU_PEAK, 4),
         },
