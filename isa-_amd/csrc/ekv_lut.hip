@@ -2188,24 +2188,60 @@ __global__ void stat_merge_kernel(const unsigned* bits, float* abs_max, double* 
 
 // Finishes a K-split forward (fwd_body wrote each split's partial sums): the splits are summed
 // in split order, then clamped (LUT) or scaled (exact, measured) and given the layer glue
-// exactly as fwd_body's epilogue does. Grid-stride over the [M][O] outputs.
+// exactly as fwd_body's epilogue does. Grid-stride over the [M][O] outputs, VEC of them per
+// thread (VEC = 4 when O and every pointer allow 16-byte accesses).
+template <int VEC>
 __global__ __launch_bounds__(256) void split_reduce_kernel(FwdArgs a, int clamp_out) {
     const int64_t n = (int64_t)a.M * a.O;
+    const int64_t nv = n / VEC;
     const bool has_r = a.glue && a.r_tia != nullptr;
     const float r = has_r ? load_uniform1(a.r_tia) : 1.0f;
     unsigned ymax = 0;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
-        float v = a.split_part[e];
-        for (int sp = 1; sp < a.n_split; ++sp) v += a.split_part[(size_t)sp * n + e];
-        const float id = clamp_out ? fminf(fmaxf(v, a.out_min), a.out_max) : v * a.out_scale;
+    for (int64_t ev = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; ev < nv; ev += (int64_t)gridDim.x * blockDim.x) {
+        float v[VEC], id[VEC];
+        if constexpr (VEC == 4) {
+            float4 t = reinterpret_cast<const float4*>(a.split_part)[ev];
+            for (int sp = 1; sp < a.n_split; ++sp) {
+                const float4 u = reinterpret_cast<const float4*>(a.split_part + (size_t)sp * n)[ev];
+                t.x += u.x;
+                t.y += u.y;
+                t.z += u.z;
+                t.w += u.w;
+            }
+            v[0] = t.x;
+            v[1] = t.y;
+            v[2] = t.z;
+            v[3] = t.w;
+        } else {
+            v[0] = a.split_part[ev];
+            for (int sp = 1; sp < a.n_split; ++sp) v[0] += a.split_part[(size_t)sp * n + ev];
+        }
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+            id[i] = clamp_out ? fminf(fmaxf(v[i], a.out_min), a.out_max) : v[i] * a.out_scale;
+        const int64_t e = ev * VEC;
         if (!a.glue) {
-            a.out[e] = id;
+            if constexpr (VEC == 4)
+                reinterpret_cast<float4*>(a.out)[ev] = make_float4(id[0], id[1], id[2], id[3]);
+            else
+                a.out[e] = id[0];
             continue;
         }
-        if (a.idiff) a.idiff[e] = id;
-        const float y = layer_tia(id, r, has_r, a.y_lo, a.y_hi);
-        ymax = max(ymax, layer_stat_bits(y));
-        a.out[e] = layer_adc(y, a.adc_scale, a.adc_shift, (int)(e % a.O));
+        const int o0 = (int)(e % a.O);  // VEC divides O: the VEC outputs share a row
+        float y[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            const float yt = layer_tia(id[i], r, has_r, a.y_lo, a.y_hi);
+            ymax = max(ymax, layer_stat_bits(yt));
+            y[i] = layer_adc(yt, a.adc_scale, a.adc_shift, o0 + i);
+        }
+        if constexpr (VEC == 4) {
+            if (a.idiff) reinterpret_cast<float4*>(a.idiff)[ev] = make_float4(id[0], id[1], id[2], id[3]);
+            reinterpret_cast<float4*>(a.out)[ev] = make_float4(y[0], y[1], y[2], y[3]);
+        } else {
+            if (a.idiff) a.idiff[e] = id[0];
+            a.out[e] = y[0];
+        }
     }
     if (a.stat_bits) {  // every lane of the wave is here: the loop has no early exit
 #pragma unroll
@@ -2221,11 +2257,19 @@ void set_split(const FwdPlan& p, char* ws, FwdArgs& fa) {
     fa.split_part = p.n_split > 1 ? reinterpret_cast<float*>(ws + p.off_split) : nullptr;
 }
 
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
 hipError_t finish_split(const FwdPlan& p, const FwdArgs& fa, bool clamp_out, hipStream_t s) {
     if (p.n_split <= 1) return hipSuccess;
     const int64_t n = (int64_t)fa.M * fa.O;
-    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, fa, clamp_out ? 1 : 0);
+    const bool vec4 = fa.O % 4 == 0 && aligned16(fa.out) && aligned16(fa.split_part) &&
+                      (!fa.glue || !fa.idiff || aligned16(fa.idiff));
+    const int64_t work = vec4 ? n / 4 : n;
+    const unsigned blocks = (unsigned)std::min<int64_t>((work + 255) / 256, 8192);
+    if (vec4)
+        hipLaunchKernelGGL(split_reduce_kernel<4>, dim3(blocks), dim3(256), 0, s, fa, clamp_out ? 1 : 0);
+    else
+        hipLaunchKernelGGL(split_reduce_kernel<1>, dim3(blocks), dim3(256), 0, s, fa, clamp_out ? 1 : 0);
     return hipGetLastError();
 }
 
