@@ -32,13 +32,16 @@
 //  * Lanes run along outputs o: the 64 gathers of one instruction share (m, k), so they
 //    fall inside the narrow window spanned by the thresholds. Token-side operands are
 //    wave-uniform and reach the VALU as SGPR operands (s_load), costing no VGPRs.
-//  * Forward: each wave owns MR tokens x 64*ORR outputs and reduces over K in registers.
+//  * Forward: each wave owns MR tokens x 64*ORR outputs and reduces over K (or, when the
+//    plan splits K to keep MR high on layers with few output blocks, over one K range, the
+//    ranges then summed in order by split_reduce_kernel) in registers.
 //  * Backward: each wave owns 64*ORR outputs x KR inputs and streams a range of tokens,
 //    keeping dVth accumulators in registers; the per-token dX partial sums over its
-//    outputs are transposed through an LDS buffer and reduced across the wave, then
-//    written as one partial per output block. Two small deterministic reduction kernels
-//    combine the output-block partials (dX) and token-range partials (dVth). No atomics:
-//    every result is bitwise reproducible.
+//    outputs are reduced across the wave with lane exchanges (the exact-formula kernels:
+//    through an LDS transpose buffer), then written as one partial per output block. Two
+//    small deterministic reduction kernels combine the output-block partials (dX) and
+//    token-range partials (dVth). No atomics in any sum (the only atomic, the optional
+//    output-statistics max, is order-free): every result is bitwise reproducible.
 
 #include <hip/hip_runtime.h>
 
@@ -973,8 +976,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void fwd_exact_kernel(FwdArgs a) {
 // ----------------------------------------------------------------------------------
 // Backward. Wave item = (output block ob of 64*ORR outputs, input block kb of KR inputs,
 // token split sp). Each lane keeps dVth accumulators for its ORR x KR (o, k) pairs over
-// the split's tokens; per token, the lane's partial dX over its outputs goes through the
-// transpose buffer and a wave reduction, giving one dX partial per (ob, m, k).
+// the split's tokens; per token, the lane's partial dX over its outputs is summed across the
+// wave (lane exchanges, or the LDS transpose buffer in the exact kernel), giving one dX
+// partial per (ob, m, k).
 // ----------------------------------------------------------------------------------
 
 struct BwdArgs {
