@@ -55,6 +55,23 @@ CASES = [
 ]
 
 
+def test_exact_random_shape_sweep(cuda_device):
+    """Ten seeded shapes up to 120 x 300 x 400 with mixed input ranges (forward plans with and
+    without K splits, many backward token splits), each against the float64 formula."""
+    rng = np.random.default_rng(20260809)
+    cfg = flash_cfg(4096, ekv_approx="exact")
+    modes = [("mapped", "init"), ("signed", "full"), ("wide", "wide")]
+    for case in range(10):
+        M, K, O = int(rng.integers(1, 121)), int(rng.integers(1, 301)), int(rng.integers(1, 401))
+        x_mode, vth_mode = modes[case % len(modes)]
+        print(f"[case] exact sweep {case}: M={M} K={K} O={O} {x_mode}/{vth_mode}", flush=True)
+        x, vp, vn, g = make_inputs(M, K, O, seed=2000 + case, x_mode=x_mode, vth_mode=vth_mode)
+        ref = _oracle(x, vp, vn, g, cfg)
+        got = _dev(x, vp, vn, g, cfg, cuda_device)
+        e = [errs(a, r)[0] for a, r in zip(got, ref)]
+        assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (M, K, O, x_mode, vth_mode, e)
+
+
 @pytest.mark.parametrize("M,K,O,x_mode,vth_mode", CASES)
 def test_exact_parity(cuda_device, M, K, O, x_mode, vth_mode):
     print(f"[case] exact parity M={M} K={K} O={O} x={x_mode} vth={vth_mode}", flush=True)

@@ -59,6 +59,24 @@ def test_forward_backward_parity(cuda_device, M, K, O):
     assert e["dX"][0] <= BWD_TOL and e["dVth+"][0] <= BWD_TOL and e["dVth-"][0] <= BWD_TOL
 
 
+def test_parity_random_shape_sweep(cuda_device):
+    """Twenty seeded shapes up to 300 x 600 x 700 with mixed input ranges, so the forward plan
+    visits every tokens-per-wave choice with and without K splits and the backward many
+    token-split counts, each checked against the oracle."""
+    rng = np.random.default_rng(20260808)
+    cfg = flash_cfg(4096)
+    modes = [("mapped", "init"), ("signed", "full"), ("mapped", "full"), ("wide", "wide")]
+    for case in range(20):
+        M, K, O = int(rng.integers(1, 301)), int(rng.integers(1, 601)), int(rng.integers(1, 701))
+        x_mode, vth_mode = modes[case % len(modes)]
+        print(f"[case] sweep {case}: M={M} K={K} O={O} {x_mode}/{vth_mode}", flush=True)
+        x, vp, vn, g = make_inputs(M, K, O, seed=1000 + case, x_mode=x_mode, vth_mode=vth_mode)
+        ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg)
+        out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device)
+        e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
+        assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (M, K, O, x_mode, vth_mode, e)
+
+
 @pytest.mark.parametrize("x_mode,vth_mode", [("signed", "full"), ("wide", "wide"), ("mapped", "full")])
 def test_parity_input_ranges(cuda_device, x_mode, vth_mode):
     """fc2-like signed inputs, trained-like thresholds, and out-of-table coordinates (clamping loop)."""
