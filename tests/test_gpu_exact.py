@@ -52,6 +52,7 @@ CASES = [
     (64, 192, 768, "mapped", "init"),
     (520, 192, 768, "mapped", "init"),  # ViT-S up-projection shape
     (96, 130, 260, "wide", "wide"),     # operands beyond the range-checked loop's bounds
+    (1, 1000, 3, "signed", "full"),     # one token: the forward splits K into eight ranges
 ]
 
 

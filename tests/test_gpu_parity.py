@@ -41,6 +41,8 @@ SHAPES = [
     (5, 8, 256),
     (70, 129, 300),    # ragged in every dimension
     (40, 260, 300),    # forward K split into 7 ranges of 40 padded inputs, the last one short
+    (1, 3000, 5),      # one token, one output block: eight K ranges of 376 inputs
+    (3, 1000, 1000),
     (64, 192, 768),
     (520, 192, 768),   # config 1: ViT-S up-projection, full size
 ]
