@@ -526,6 +526,26 @@ __device__ inline bool coords_in_padded_range(const float2* __restrict__ partial
     return __builtin_amdgcn_readfirstlane((int)ok) != 0;
 }
 
+// LUT forward with a second table copy: a gather's 64 lanes read the records of their own
+// thresholds, and once the thresholds spread over more than ~100 records, lanes of a
+// half-wave often hit one LDS bank pair with different records. A second copy of the table
+// 16 bank pairs away (the copy starts T1 records after the first, T1 % 32 == 16) lets each
+// (input, output) threshold pick the copy whose bank is less loaded (fwd_copy_assign_kernel;
+// the choice folds into the threshold coordinate, c' = c + T1, and copy 1 stores
+// A' = A - T1 dT so that fma(c', dT, A') = fma(c, dT, A)). With narrow thresholds (the
+// initial ones span ~69 records) the lanes share records often enough that splitting them
+// over two copies costs more than it saves, so the mode needs a wide spread and the
+// clamp-free loop (the fold assumes unclamped coordinates).
+constexpr float kFwdCopyMinWindow = 100.0f;  // threshold spread, in table records
+constexpr size_t kFwdCopyLdsBytes = 80 * 1024;  // both copies, with two forward blocks per CU
+
+__device__ inline bool fwd_copies_mode(const float2* __restrict__ partials, int n_pad_entries) {
+    const CoordRange c = read_coord_range(partials);
+    const bool ok = (c.xlo - c.whi >= 1.0f) && (c.xhi - c.wlo <= (float)(n_pad_entries - 2)) &&
+                    (c.whi - c.wlo >= kFwdCopyMinWindow);
+    return __builtin_amdgcn_readfirstlane((int)ok) != 0;
+}
+
 template <bool CLAMP>
 __device__ inline float coord(float xs, float ws, float cmin, float cmax) {
     float c = xs - ws;
@@ -762,6 +782,7 @@ struct FwdArgs {
     // raw partial sums to split_part[s][M][O] and split_reduce_kernel finishes the outputs
     int n_split, k_chunk;
     float* split_part;
+    int copy_offset;        // LUT: T1 > 0 when the launch may use the second table copy
 };
 
 // The work of one forward wave.
@@ -947,11 +968,82 @@ __device__ inline bool fwd_tile(const FwdArgs& a, int MR, FwdTile& t) {
     return t.m0 < a.M;
 }
 
+// Copy choice for the LUT forward's second table copy (see fwd_copies_mode). One thread per
+// 32-lane problem: the thresholds one gather instruction's half-wave reads, i.e. input k,
+// sign (+/-), output slot j of the lanes' kFwdORR outputs and half h of an output block:
+// lanes l = 0..31 read output block * 256 + (32 h + l) * kFwdORR + j. Lane by lane, a lane
+// whose threshold has the integer coordinate part of an earlier lane's takes that lane's
+// copy (they read the same record for most tokens: a broadcast), otherwise the copy whose
+// bank pair (floor coordinate, and its neighbour for the tokens whose fraction crosses the
+// threshold's) has the smaller expected load so far. Copy-1 thresholds are stored as
+// ws - T1 (so c' = xs - ws' = c + T1). Writes nothing unless the launch is in copy mode.
+constexpr int kAssignThreads = 128;
+
+__global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2* __restrict__ wsT,
+                                                              const float2* __restrict__ partials, int NP,
+                                                              int64_t Kp, int64_t Op, int copy_offset) {
+    if (!fwd_copies_mode(partials, NP)) return;
+    __shared__ float s_cnt[32][kAssignThreads];  // per-thread bank-pair loads; [bin][thread]: conflict-free
+    __shared__ float s_fl[32][kAssignThreads];   // per-thread integer coordinate parts of the lanes so far
+    const int tid = threadIdx.x;
+    const int64_t n_ot = Op / (64 * kFwdORR);
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + tid;
+    if (p >= Kp * n_ot * kFwdORR * 4) return;
+    const int sign = (int)(p & 1), half = (int)((p >> 1) & 1), j = (int)((p >> 2) % kFwdORR);
+    const int64_t rest = (p >> 2) / kFwdORR;
+    const int64_t tile = rest % n_ot, k = rest / n_ot;
+    float* w0 = reinterpret_cast<float*>(wsT + k * Op + tile * 64 * kFwdORR + j) + sign;
+    const int64_t lane_stride = 2 * kFwdORR;  // floats between consecutive lanes' records
+    const float t1 = (float)copy_offset;
+#pragma unroll
+    for (int b = 0; b < 32; ++b) s_cnt[b][tid] = 0.0f;
+    unsigned chosen = 0;  // bit l: lane l took copy 1
+    for (int l = 0; l < 32; ++l) {
+        float* wp = w0 + (int64_t)(32 * half + l) * lane_stride;
+        const float w = *wp;
+        const float fl = floorf(w);
+        const float fr = w - fl;
+        int c = -1;
+        for (int b = 0; b < l; ++b)
+            if (s_fl[b][tid] == fl) {
+                c = (chosen >> b) & 1;
+                break;
+            }
+        if (c < 0) {
+            // bank pair of the record at floor(u) - fl (weight 1 - fr) and one below (fr);
+            // floor(u) is common to the half-wave, so bin = -fl mod 32 (+16 for copy 1)
+            const int r0 = (-(int)fl) & 31, r1 = (r0 + 16) & 31;
+            const int m0 = (r0 + 31) & 31, m1 = (r1 + 31) & 31;
+            const float v0 = (1.0f - fr) * s_cnt[r0][tid] + fr * s_cnt[m0][tid];
+            const float v1 = (1.0f - fr) * s_cnt[r1][tid] + fr * s_cnt[m1][tid];
+            c = v1 < v0 ? 1 : 0;
+            s_cnt[c ? r1 : r0][tid] += 1.0f - fr;
+            s_cnt[c ? m1 : m0][tid] += fr;
+        }
+        s_fl[l][tid] = fl;
+        chosen |= (unsigned)c << l;
+        if (c) *wp = w - t1;
+    }
+}
+
 template <int MR, bool SPLITS>
 __global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
     for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
-    const bool fast = coords_in_padded_range(a.partials, a.NP);
+    // fast loop and copy mode from one read of the range partials (as coords_in_padded_range
+    // and fwd_copies_mode decide them; a second read here costs the main loop ~50 VGPRs)
+    const CoordRange cr = read_coord_range(a.partials);
+    const bool fast = __builtin_amdgcn_readfirstlane(
+                          (int)((cr.xlo - cr.whi >= 1.0f) && (cr.xhi - cr.wlo <= (float)(a.NP - 2)))) != 0;
+    const bool copies = fast && a.copy_offset > 0 &&
+                        __builtin_amdgcn_readfirstlane((int)(cr.whi - cr.wlo >= kFwdCopyMinWindow)) != 0;
+    if (copies) {  // record i of copy 1 holds {A - T1 dT, dT}: fma(c + T1, dT, A') = fma(c, dT, A)
+        const float t1 = (float)a.copy_offset;
+        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
+            const float2 r = a.lut[i];
+            s_lut_fwd[a.copy_offset + i] = make_float2(fmaf(-t1, r.y, r.x), r.y);
+        }
+    }
     __syncthreads();
     FwdTile t;
     if (!fwd_tile<SPLITS>(a, MR, t)) return;
@@ -2333,6 +2425,20 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.cmax = (float)(kPad + cs.n_entries - 1);
         fa.out_scale = 1.0f;
         lds = (size_t)fa.NP * 8;
+        // the second table copy (used when the thresholds spread wide, decided on the device)
+        // when both copies still leave room for two forward blocks per CU
+        const int t1 = (int)round_up(fa.NP - 16, 32) + 16;
+        const size_t lds2 = (size_t)(t1 + fa.NP) * 8;
+        if (lds2 <= kFwdCopyLdsBytes) {
+            fa.copy_offset = t1;
+            lds = lds2;
+            const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
+            hipLaunchKernelGGL(fwd_copy_assign_kernel, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
+                               dim3(kAssignThreads), 0, s,
+                               reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials, fa.NP, p.Kp, p.Op, t1);
+            err = hipGetLastError();
+            if (err != hipSuccess) return hip_fail(err, "forward copy assignment launch");
+        }
     }
     set_split(p, ws, fa);
     ProfiledLaunch* prof;
