@@ -979,10 +979,16 @@ __device__ inline bool fwd_tile(const FwdArgs& a, int MR, FwdTile& t) {
 // ws - T1 (so c' = xs - ws' = c + T1). Writes nothing unless the launch is in copy mode.
 constexpr int kAssignThreads = 128;
 
+// The launch's table-copy mode (fwd_copies_mode) as a word for the launches that follow.
+__global__ __launch_bounds__(64) void copy_mode_kernel(const float2* __restrict__ partials, int NP, int* mode_word) {
+    const bool on = fwd_copies_mode(partials, NP);
+    if (threadIdx.x == 0) *mode_word = on ? 1 : 0;
+}
+
 __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2* __restrict__ wsT,
-                                                              const float2* __restrict__ partials, int NP,
-                                                              int64_t Kp, int64_t Op, int copy_offset) {
-    if (!fwd_copies_mode(partials, NP)) return;
+                                                              const int* __restrict__ mode_word, int64_t Kp,
+                                                              int64_t Op, int copy_offset) {
+    if (__builtin_amdgcn_readfirstlane(*mode_word) == 0) return;
     __shared__ float s_cnt[32][kAssignThreads];  // per-thread bank-pair loads; [bin][thread]: conflict-free
     __shared__ float s_fl[32][kAssignThreads];   // per-thread integer coordinate parts of the lanes so far
     const int tid = threadIdx.x;
@@ -1081,6 +1087,7 @@ struct BwdArgs {
     const float* grad;      // [M][ldg]
     const float4* lut;      // LUT: [NP] {A_I, dI, A_D, dD}
     const float2* partials;
+    const int* copy_mode;   // kBwdOneCopy / kBwdTwoCopies launches: 1 when the copies are in use
     float* dx_part;         // [n_ob][M][K]            (need_x)
     float* dv_part;         // [S][2][Kp][Op]          (need_w)
     int M, K, O, Kp, Op, ldg, NP;
@@ -1327,40 +1334,70 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
     }
 }
 
-template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false>
+// Table-backward launch modes. kBwdAlone: the only launch. With the second table copy
+// (split layout, see fwd_copies_mode) the host enqueues two launches of which the device
+// picks one from the range partials: kBwdOneCopy (two 16-wave blocks per CU, exits in copy
+// mode) and kBwdTwoCopies (both copies, 132 KB of LDS: one block per CU; exits otherwise).
+// Copy 1 starts kBwdCopyOffset records after copy 0 (I half; its D half kSplitRecords
+// further, as copy 0's), 16 bank pairs away.
+constexpr int kBwdAlone = 0, kBwdOneCopy = 1, kBwdTwoCopies = 2;
+constexpr int kBwdCopyOffset = 2 * kSplitRecords + 16;
+constexpr size_t kBwdTwoCopiesLds = (size_t)(kBwdCopyOffset + 2 * kSplitRecords) * 8;
+
+template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false, int MODE = kBwdAlone>
 __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdArgs a) {
+    static_assert(MODE == kBwdAlone || SPLIT, "the second table copy uses the split layout");
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
+    // which launch of a pair works: the copy assignment pass wrote the mode word. (Where the
+    // checks sit matters: reading anything before the table loop costs the one-copy kernel
+    // ~10 VGPRs and with them its second block per CU, so it checks after the loop.)
+    if constexpr (MODE == kBwdTwoCopies)
+        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) == 0) return;
     for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
         const float4 rec = a.lut[i];
         if constexpr (SPLIT) {
             s_split[i] = make_float2(rec.x, rec.y);
             s_split[i + kSplitRecords] = make_float2(rec.z, rec.w);
+            if constexpr (MODE == kBwdTwoCopies) {  // {A - T1 dT, dT} for both halves
+                const float t1 = (float)kBwdCopyOffset;
+                s_split[kBwdCopyOffset + i] = make_float2(fmaf(-t1, rec.y, rec.x), rec.y);
+                s_split[kBwdCopyOffset + i + kSplitRecords] = make_float2(fmaf(-t1, rec.w, rec.z), rec.w);
+            }
         } else {
             s_lut_bwd[i] = rec;
         }
     }
     const bool fast = coords_in_padded_range(a.partials, a.NP);
+    if constexpr (MODE == kBwdOneCopy)
+        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
     __syncthreads();
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int table_records = SPLIT ? kSplitRecords : a.NP;
     float* red = LANE_RED ? nullptr
                           : reinterpret_cast<float*>(s_lut_bwd + table_records) + wave * (kRedSlots * kRedStride);
-    const int item = blockIdx.x * waves + wave;
-    if (item >= a.n_items) return;
     using Table = typename std::conditional<SPLIT, BwdTableSplit, BwdTableInterleaved>::type;
     Table t;
     if constexpr (SPLIT)
         t = BwdTableSplit{s_split};
     else
         t = BwdTableInterleaved{s_lut_bwd};
-    if (fast)
-        bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(
-            a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
-    else
-        bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(
-            a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+    // The two-copy launch runs one block per CU (its 132 KB of LDS) over as many blocks as CUs,
+    // each wave taking the plan's blocks in turn, so the launch costs little when it is not
+    // the working one and loads its tables once per CU when it is.
+    const int stride = MODE == kBwdTwoCopies ? (int)gridDim.x : 0;
+    for (int vb = blockIdx.x;; vb += stride) {
+        const int item = vb * waves + wave;
+        if (item >= a.n_items) return;
+        if (fast)
+            bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(
+                a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+        else
+            bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(
+                a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+        if (MODE != kBwdTwoCopies) return;
+    }
 }
 
 // Exact-formula backward (reference: ekv_triton.py:94-169): same work decomposition; LDS
@@ -1927,7 +1964,7 @@ struct FwdPlan {
     int64_t Kp, Op;
     int mr, n_mt, n_ot, blocks;
     int n_split, k_chunk;  // K split of small problems (n_split = 1: none)
-    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_stat, off_split, bytes;
+    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_stat, off_mode, off_split, bytes;
 };
 
 #ifndef ISA_EKV_BWD_MIN_SPLIT_M
@@ -1981,6 +2018,8 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
     off += (size_t)round_up((kPrepBlocksX + kPrepBlocksW) * 8, 256);
     p.off_stat = off;
     off += 256;
+    p.off_mode = off;  // the table-copy mode word
+    off += 256;
     p.off_split = off;
     if (p.n_split > 1) off += (size_t)round_up((int64_t)p.n_split * M * O * 4, 256);
     p.bytes = round_up((int64_t)off, 256);
@@ -1991,8 +2030,8 @@ struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
     bool grad_padded, split, lane_red;
-    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_gpad, off_dx, off_dv, off_glue, bytes,
-        lds_bytes;
+    size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
+        bytes, lds_bytes;
 };
 
 // n_entries = 0 plans the exact-formula backward (no LDS table, general-loop records).
@@ -2069,6 +2108,8 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     if (exact) off += wsT_bytes;
     p.off_part = off;
     off += (size_t)round_up((kPrepBlocksX + kPrepBlocksW) * 8, 256);
+    p.off_mode = off;  // the table-copy mode word
+    off += 256;
     p.off_gpad = off;
     if (p.grad_padded) off += (size_t)round_up((int64_t)M * p.Op * 4, 256);
     p.off_dx = off;
@@ -2136,6 +2177,20 @@ void launch_backward_layout(bool need_x, bool need_w, dim3 grid, dim3 block, siz
         hipLaunchKernelGGL((bwd_kernel<true, false, SPLIT, LANE_RED>), grid, block, lds, s, ba);
     else
         hipLaunchKernelGGL((bwd_kernel<false, true, SPLIT, false>), grid, block, lds, s, ba);
+}
+
+// The split-layout lane-exchange backward as a pair of launches (kBwdOneCopy, kBwdTwoCopies)
+// of which the device runs one; the same plan (grid, token splits, partial planes) serves both.
+void launch_backward_copies(bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s, const BwdArgs& ba) {
+    const dim3 grid2(std::min<unsigned>(grid.x, kCUs));  // persistent: one block per CU
+    if (need_w) {
+        hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s, ba);
+    } else {
+        hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s,
+                           ba);
+    }
 }
 
 void launch_backward(bool exact, bool need_x, bool need_w, bool split, bool lane_red, dim3 grid, dim3 block,
@@ -2432,10 +2487,12 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         if (lds2 <= kFwdCopyLdsBytes) {
             fa.copy_offset = t1;
             lds = lds2;
+            int* mode = reinterpret_cast<int*>(ws + p.off_mode);
+            hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, fa.partials, fa.NP, mode);
             const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
             hipLaunchKernelGGL(fwd_copy_assign_kernel, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
-                               dim3(kAssignThreads), 0, s,
-                               reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials, fa.NP, p.Kp, p.Op, t1);
+                               dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp,
+                               p.Op, t1);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward copy assignment launch");
         }
@@ -2568,9 +2625,27 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         ba.cmax = (float)(kPad + cs.n_entries - 1);
     }
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
+    // the second table copy for wide threshold spreads: split layout with lane-exchange dX
+    // (the plan's LDS then holds only the table, so both copies fit one block per CU)
+    const bool copies = kBwdORR == kFwdORR && !cs.exact && p.split && p.lane_red && need_x &&
+                        p.lds_bytes <= kBwdTwoCopiesLds / 2 && p.waves_per_block == 16;
+    if (copies) {
+        int* mode = reinterpret_cast<int*>(ws + p.off_mode);
+        hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, ba.partials, ba.NP, mode);
+        const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * 4;
+        hipLaunchKernelGGL(fwd_copy_assign_kernel, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
+                           dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp, p.Op,
+                           kBwdCopyOffset);
+        ba.copy_mode = mode;
+        err = hipGetLastError();
+        if (err != hipSuccess) return hip_fail(err, "backward copy assignment launch");
+    }
     ProfiledLaunch* prof;
     prof_start(s, 1, &prof);
-    launch_backward(cs.exact, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
+    if (copies)
+        launch_backward_copies(need_w, grid, block, p.lds_bytes, s, ba);
+    else
+        launch_backward(cs.exact, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
     err = hipGetLastError();
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "backward launch");
