@@ -1341,6 +1341,12 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
 // Copy 1 starts kBwdCopyOffset records after copy 0 (I half; its D half kSplitRecords
 // further, as copy 0's), 16 bank pairs away.
 constexpr int kBwdAlone = 0, kBwdOneCopy = 1, kBwdTwoCopies = 2;
+#ifndef ISA_EKV_BWD_KR_TWO_COPIES
+#define ISA_EKV_BWD_KR_TWO_COPIES 4
+#endif
+// one block per CU leaves the two-copy kernel the VGPRs for four inputs per wave (half the
+// G traffic and lane exchanges per cell); its launch gets its own item count for them
+constexpr int kBwdKRTwoCopies = ISA_EKV_BWD_KR_TWO_COPIES;
 constexpr int kBwdCopyOffset = 2 * kSplitRecords + 16;
 constexpr size_t kBwdTwoCopiesLds = (size_t)(kBwdCopyOffset + 2 * kSplitRecords) * 8;
 
@@ -1387,14 +1393,15 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
     // each wave taking the plan's blocks in turn, so the launch costs little when it is not
     // the working one and loads its tables once per CU when it is.
     const int stride = MODE == kBwdTwoCopies ? (int)gridDim.x : 0;
+    constexpr int KRM = MODE == kBwdTwoCopies ? kBwdKRTwoCopies : kBwdKR;  // inputs per wave
     for (int vb = blockIdx.x;; vb += stride) {
         const int item = vb * waves + wave;
         if (item >= a.n_items) return;
         if (fast)
-            bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(
+            bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(
                 a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
         else
-            bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(
+            bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(
                 a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
         if (MODE != kBwdTwoCopies) return;
     }
@@ -2181,15 +2188,19 @@ void launch_backward_layout(bool need_x, bool need_w, dim3 grid, dim3 block, siz
 
 // The split-layout lane-exchange backward as a pair of launches (kBwdOneCopy, kBwdTwoCopies)
 // of which the device runs one; the same plan (grid, token splits, partial planes) serves both.
-void launch_backward_copies(bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s, const BwdArgs& ba) {
+void launch_backward_copies(bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s, const BwdArgs& ba0) {
     const dim3 grid2(std::min<unsigned>(grid.x, kCUs));  // persistent: one block per CU
+    BwdArgs ba2 = ba0;  // the two-copy kernel's inputs per wave
+    ba2.n_kb = ba0.Kp / kBwdKRTwoCopies;
+    ba2.n_items = ba0.n_ob * ba2.n_kb * ba0.n_split;
+    const BwdArgs& ba = ba0;
     if (need_w) {
         hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
-        hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s, ba);
+        hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s, ba2);
     } else {
         hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
         hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s,
-                           ba);
+                           ba2);
     }
 }
 
