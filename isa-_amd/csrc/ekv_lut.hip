@@ -990,7 +990,6 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
                                                               int64_t Op, int copy_offset) {
     if (__builtin_amdgcn_readfirstlane(*mode_word) == 0) return;
     __shared__ float s_cnt[32][kAssignThreads];  // per-thread bank-pair loads; [bin][thread]: conflict-free
-    __shared__ float s_fl[32][kAssignThreads];   // per-thread integer coordinate parts of the lanes so far
     const int tid = threadIdx.x;
     const int64_t n_ot = Op / (64 * kFwdORR);
     const int64_t p = (int64_t)blockIdx.x * blockDim.x + tid;
@@ -1004,17 +1003,17 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
 #pragma unroll
     for (int b = 0; b < 32; ++b) s_cnt[b][tid] = 0.0f;
     unsigned chosen = 0;  // bit l: lane l took copy 1
+    float fls[32];        // integer coordinate parts of the lanes (registers: the loops unroll)
+#pragma unroll
     for (int l = 0; l < 32; ++l) {
         float* wp = w0 + (int64_t)(32 * half + l) * lane_stride;
         const float w = *wp;
         const float fl = floorf(w);
         const float fr = w - fl;
         int c = -1;
-        for (int b = 0; b < l; ++b)
-            if (s_fl[b][tid] == fl) {
-                c = (chosen >> b) & 1;
-                break;
-            }
+#pragma unroll
+        for (int b = l - 1; b >= 0; --b)  // the earliest match wins
+            if (fls[b] == fl) c = (chosen >> b) & 1;
         if (c < 0) {
             // bank pair of the record at floor(u) - fl (weight 1 - fr) and one below (fr);
             // floor(u) is common to the half-wave, so bin = -fl mod 32 (+16 for copy 1)
@@ -1026,7 +1025,7 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
             s_cnt[c ? r1 : r0][tid] += 1.0f - fr;
             s_cnt[c ? m1 : m0][tid] += fr;
         }
-        s_fl[l][tid] = fl;
+        fls[l] = fl;
         chosen |= (unsigned)c << l;
         if (c) *wp = w - t1;
     }
