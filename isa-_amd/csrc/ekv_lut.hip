@@ -538,6 +538,11 @@ __device__ inline bool coords_in_padded_range(const float2* __restrict__ partial
 // clamp-free loop (the fold assumes unclamped coordinates).
 constexpr float kFwdCopyMinWindow = 100.0f;  // threshold spread, in table records
 constexpr size_t kFwdCopyLdsBytes = 80 * 1024;  // both copies, with two forward blocks per CU
+constexpr int kFwdCopyMinInputs16 = 256;         // padded inputs per wave for the 16-wave copy blocks
+
+// second-copy offset (records, = 16 mod 32, past the first copy) and both copies' LDS bytes
+inline int fwd_copy_offset(int n_entries) { return (int)((n_entries + 2 * kPad - 16 + 31) / 32 * 32) + 16; }
+inline size_t fwd_copy_lds(int n_entries) { return (size_t)(fwd_copy_offset(n_entries) + n_entries + 2 * kPad) * 8; }
 
 __device__ inline bool fwd_copies_mode(const float2* __restrict__ partials, int n_pad_entries) {
     const CoordRange c = read_coord_range(partials);
@@ -954,7 +959,8 @@ __device__ inline bool fwd_tile(const FwdArgs& a, int MR, FwdTile& t) {
     const int tile_o = w / a.n_mt;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    t.m0 = (tile_m * kFwdWaves + wave) * MR;
+    const int wpb = blockDim.x >> 6;  // waves per block (8, or 16 for two 8192-entry tables)
+    t.m0 = (tile_m * wpb + wave) * MR;
     t.o_lane = tile_o * 64 * kFwdORR + lane * kFwdORR;
     if (SPLITS && a.n_split > 1) {
         t.k_lo = split * a.k_chunk;
@@ -1032,7 +1038,7 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
 }
 
 template <int MR, bool SPLITS>
-__global__ __launch_bounds__(kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
     for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
     // fast loop and copy mode from one read of the range partials (as coords_in_padded_range
@@ -1970,6 +1976,7 @@ struct FwdPlan {
     int64_t Kp, Op;
     int mr, n_mt, n_ot, blocks;
     int n_split, k_chunk;  // K split of small problems (n_split = 1: none)
+    int wpb;               // waves per block
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_stat, off_mode, off_split, bytes;
 };
 
@@ -1983,8 +1990,9 @@ constexpr int64_t kBwdMinSplitTokens = ISA_EKV_BWD_MIN_SPLIT_M;  // tokens per b
 constexpr int kFwdMaxSplit = 8;
 constexpr int kFwdMinSplitInputs = ISA_EKV_FWD_MIN_SPLIT_K;  // padded inputs per K split, at least
 
-FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_split = true) {
+FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_split = true, int wpb = kFwdWaves) {
     FwdPlan p{};
+    p.wpb = wpb;
     p.Kp = round_up(K > 0 ? K : 1, 8);
     p.Op = round_up(O > 0 ? O : 1, 64 * kFwdORR);
     p.n_ot = (int)(p.Op / (64 * kFwdORR));
@@ -1998,13 +2006,13 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
     while (allow_split && sp_max < kFwdMaxSplit && p.Kp / (2 * sp_max) >= kFwdMinSplitInputs) sp_max *= 2;
     int split = 1;
     for (p.mr = 8;; p.mr /= 2) {
-        const int64_t waves = round_up(M, (int64_t)kFwdWaves * p.mr) / p.mr * p.n_ot;
+        const int64_t waves = round_up(M, (int64_t)wpb * p.mr) / p.mr * p.n_ot;
         if (p.mr == 2 || waves * sp_max >= waves_target) {
             while (split < sp_max && waves * split < waves_target) split *= 2;
             break;
         }
     }
-    const int64_t tokens_per_block = (int64_t)kFwdWaves * p.mr;
+    const int64_t tokens_per_block = (int64_t)wpb * p.mr;
     p.n_mt = (int)((M + tokens_per_block - 1) / tokens_per_block);
     p.k_chunk = (int)round_up((p.Kp + split - 1) / split, 8);
     p.n_split = (int)((p.Kp + p.k_chunk - 1) / p.k_chunk);
@@ -2148,8 +2156,8 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_
 }
 
 template <bool SPLITS>
-void launch_forward_split(bool exact, int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
-    const dim3 block(kFwdWaves * 64);
+void launch_forward_split(bool exact, int mr, int wpb, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+    const dim3 block(wpb * 64);
     if (exact) {
         if (mr == 8)
             hipLaunchKernelGGL((fwd_exact_kernel<8, SPLITS>), grid, block, 0, s, fa);
@@ -2167,11 +2175,11 @@ void launch_forward_split(bool exact, int mr, dim3 grid, size_t lds, hipStream_t
         hipLaunchKernelGGL((fwd_kernel<2, SPLITS>), grid, block, lds, s, fa);
 }
 
-void launch_forward(bool exact, int mr, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+void launch_forward(bool exact, int mr, int wpb, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
     if (fa.n_split > 1)
-        launch_forward_split<true>(exact, mr, grid, lds, s, fa);
+        launch_forward_split<true>(exact, mr, wpb, grid, lds, s, fa);
     else
-        launch_forward_split<false>(exact, mr, grid, lds, s, fa);
+        launch_forward_split<false>(exact, mr, wpb, grid, lds, s, fa);
 }
 
 template <bool SPLIT, bool LANE_RED>
@@ -2440,7 +2448,15 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
                 float* idiff = nullptr) {
     if (M == 0 || O == 0) return 0;
     if (!out) return fail(ISA_EKV_EINVAL, "out is null");
-    const FwdPlan p = plan_forward(M, K, O, cs.exact);
+    // LUT tables past 4096 entries hold their two copies (132 KB) in one 16-wave block per CU,
+    // the same 16 waves per CU as two 8-wave blocks of one copy; that pays when each wave sums
+    // a long K range (measured: 768 inputs per wave -7%, 64 or 128 +9%: the block's table
+    // load, barrier and tail are spread over less work)
+    FwdPlan p = plan_forward(M, K, O, cs.exact, true, kFwdWaves);
+    if (!cs.exact && fwd_copy_lds(cs.n_entries) > kFwdCopyLdsBytes && fwd_copy_lds(cs.n_entries) <= (size_t)kLdsBytes) {
+        const FwdPlan p16 = plan_forward(M, K, O, false, true, 2 * kFwdWaves);
+        if (p16.k_chunk >= kFwdCopyMinInputs16) p = p16;
+    }
     if (!workspace || workspace_bytes < p.bytes)
         return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
     char* ws = static_cast<char*>(workspace);
@@ -2492,9 +2508,9 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         lds = (size_t)fa.NP * 8;
         // the second table copy (used when the thresholds spread wide, decided on the device)
         // when both copies still leave room for two forward blocks per CU
-        const int t1 = (int)round_up(fa.NP - 16, 32) + 16;
-        const size_t lds2 = (size_t)(t1 + fa.NP) * 8;
-        if (lds2 <= kFwdCopyLdsBytes) {
+        const int t1 = fwd_copy_offset(cs.n_entries);
+        const size_t lds2 = fwd_copy_lds(cs.n_entries);
+        if (lds2 <= (p.wpb == kFwdWaves ? kFwdCopyLdsBytes : (size_t)kLdsBytes)) {
             fa.copy_offset = t1;
             lds = lds2;
             int* mode = reinterpret_cast<int*>(ws + p.off_mode);
@@ -2510,7 +2526,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
     set_split(p, ws, fa);
     ProfiledLaunch* prof;
     prof_start(s, 0, &prof);
-    launch_forward(cs.exact, p.mr, dim3(p.blocks), lds, s, fa);
+    launch_forward(cs.exact, p.mr, p.wpb, dim3(p.blocks), lds, s, fa);
     err = hipGetLastError();
     if (err == hipSuccess) err = finish_split(p, fa, !cs.exact, s);
     prof_stop(s, prof);
@@ -2994,7 +3010,8 @@ int isa_ekv_profile_end(double* ms, int* launches) {
 
 size_t isa_ekv_forward_workspace(int64_t M, int64_t K, int64_t O) {
     if (M < 0 || K < 0 || O < 0) return 0;
-    return plan_forward(M, K, O, false).bytes;
+    // the table size is not an argument: cover both block shapes run_forward may plan
+    return std::max(plan_forward(M, K, O, false).bytes, plan_forward(M, K, O, false, true, 2 * kFwdWaves).bytes);
 }
 
 int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd, int64_t M,
