@@ -389,6 +389,9 @@ def main() -> int:
     ap.add_argument("--vth-spread", default="init", choices=["init", "full"],
                     help="thresholds: the reference's initialisation U(2.5 +- 0.5*2nU_T) (headline), or "
                          "U[V_TH_MIN, V_TH_MAX] as a stand-in for trained thresholds (wider table windows)")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the step as replays of one captured HIP graph (torch.cuda.CUDAGraph): "
+                         "no host launch cost; the per-kernel figures come from an eager pass after")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -456,19 +459,47 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    graph = None
+    if args.graph:
+        # the step captured once; each replay recomputes the outputs and gradients in the
+        # graph's own buffers (the library reads nothing back to the host and allocates nothing)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        model.zero_grad(set_to_none=True)
+        x.grad = None
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            model(x).backward(g)
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with _hip.KernelTimer() as kt:
+
+    def timed(run):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         e0.record()
         for _ in range(args.steps):
-            step()
+            run()
         e1.record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
+        return e0.elapsed_time(e1) / args.steps, time.perf_counter() - t0
+
+    if graph is None:
+        with _hip.KernelTimer() as kt:
+            ms, wall = timed(step)
+    else:
+        ms, wall = timed(graph.replay)
+        with _hip.KernelTimer() as kt:  # per-kernel launch times: the same kernels, eager
+            eager_ms, _ = timed(step)
+        log(f"[bench] {args.config}: eager step {eager_ms:.3f} ms (host launches included)")
     value = cells_step / (ms * 1e-3)
-    log(f"[bench] {args.config}: {ms:.3f} ms/step (wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
+    log(f"[bench] {args.config}: {ms:.3f} ms/step{' (graph replay)' if graph is not None else ''} "
+        f"(wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
 
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
@@ -545,7 +576,8 @@ def main() -> int:
                 "vits_up": "ViT-S up-projection: CIMLinear 192->768, X[8,65,192] fp32, fwd+bwd",
             }[args.config] + (" (exact-formula kernels, ekv_approx='exact')" if exact else "")
               + (f" (LUT_DTYPE={cfg['LUT_DTYPE']})" if args.lut_dtype else "")
-              + (" (thresholds U[V_TH_MIN, V_TH_MAX])" if args.vth_spread == "full" else ""),
+              + (" (thresholds U[V_TH_MIN, V_TH_MAX])" if args.vth_spread == "full" else "")
+              + (" (step replayed from one captured HIP graph)" if graph is not None else ""),
             "tokens": M,
             "lut_entries": args.lut_size,
             "cell_evals_per_step": cells_step,
