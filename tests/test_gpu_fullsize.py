@@ -75,3 +75,21 @@ def test_headline_equal_threshold_invariant(cuda_device):
     out, gx, gp, gn = _run(x, vp, vp, g, cfg, cuda_device)
     assert torch.count_nonzero(out) == 0 and torch.count_nonzero(gx) == 0
     assert torch.equal(gp, -gn)
+
+
+@pytest.mark.parametrize("size,vth_mode", [(8192, "init"), (4096, "full")])
+def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
+    """The regimes where the kernels hold a second, bank-rotated table copy, at the headline
+    fc1 shape: the 8192-entry table (its initial thresholds span ~135 records; the forward
+    runs both copies in one 16-wave block per CU, each wave summing all 768 inputs) and
+    thresholds spread over U[V_TH_MIN, V_TH_MAX] (forward copies, and the persistent
+    two-copy backward), checked on sampled exact sub-problems."""
+    print(f"[case] headline fc1 with table copies: {size} entries, thresholds {vth_mode}", flush=True)
+    cfg = flash_cfg(size)
+    rng = np.random.default_rng(size)
+    x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=7, vth_mode=vth_mode))
+    res = _run(x, vp, vn, g, cfg, cuda_device)
+    _check_samples(x, vp, vn, g, res, cfg, rng)
+    again = _run(x, vp, vn, g, cfg, cuda_device)
+    for a, b in zip(res, again):
+        assert torch.equal(a, b)
