@@ -84,7 +84,8 @@ size_t isa_ekv_forward_workspace(int64_t M, int64_t K, int64_t O);
 /* out[m,o] = clamp(sum_k (L(x-vth_pos) - L(x-vth_neg)) / (1 + x/v_sat), out_min, out_max)
  * with L the linear interpolation of table_i (lut_fwd = ISA_EKV_LUT_FWD layout).
  * Replaces the Triton _forward_kernel launch (ekv_lut_triton.py:37-62, :151-157) and
- * binding.cpp:57 `forward` (ekv_cuda.cu:351-387). n_entries <= 16384. */
+ * binding.cpp:57 `forward` (ekv_cuda.cu:351-387). n_entries <= 4194304: tables up to 16384
+ * entries are held in LDS, larger ones read from global memory (as the Triton forward). */
 int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd, int64_t M,
                     int64_t K, int64_t O, int n_entries, float delta_min, float delta_max, float v_sat,
                     float out_min, float out_max, float* out, void* workspace, size_t workspace_bytes,
@@ -100,7 +101,10 @@ size_t isa_ekv_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries
  * grad_x may be null (no dX); grad_vth_pos and grad_vth_neg are both null or both set.
  * Replaces binding.cpp:59 `grad_x_shared` (ekv_cuda.cu:193-252, :433-485) and
  * binding.cpp:61 `grad_w_shared` (ekv_cuda.cu:296-341, :530-574), i.e. the calls made by
- * cuda_backend.shared_backward (cuda_backend.py:50-99). n_entries <= 8192, as the reference. */
+ * cuda_backend.shared_backward (cuda_backend.py:50-99). n_entries <= 4194304: tables up to
+ * 8192 entries (the reference's shared-backward limit, which the Python layer keeps where
+ * CUDA_SHARED_BACKWARD is set) are held in LDS, larger ones read from global memory, the
+ * counterpart of the reference's Triton backward (ekv_lut_triton.py:193-218). */
 int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
                      const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries, float delta_min,
                      float delta_max, float v_sat, float* grad_x, float* grad_vth_pos, float* grad_vth_neg,

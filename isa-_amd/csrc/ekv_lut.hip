@@ -95,8 +95,11 @@ static_assert((kBwdORR == 2 || kBwdORR == 4) && (kBwdKR == 2 || kBwdKR == 4), "b
 constexpr int kRedStride = 68;    // floats per slot row in the transpose buffer (64 + pad)
 constexpr int kPrepBlocksX = 1024; // prep blocks for the token side
 constexpr int kPrepBlocksW = 256; // prep blocks for the threshold side
-constexpr int kMaxEntriesFwd = 16384;
-constexpr int kMaxEntriesBwd = 8192;
+constexpr int kMaxEntriesFwd = 16384;   // LDS-resident forward table
+constexpr int kMaxEntriesBwd = 8192;    // LDS-resident backward table
+// Larger tables are read from global memory (L2-resident) by the fwd/bwd_global kernels;
+// coordinates stay exact integers in fp32 up to this size.
+constexpr int kMaxEntriesGlobal = 1 << 22;
 #ifndef ISA_EKV_BWD_MIN_BLOCKS
 #define ISA_EKV_BWD_MIN_BLOCKS 2  // table-backward blocks per CU the VGPR budget is held to (64 VGPRs at 2)
 #endif
@@ -1064,6 +1067,20 @@ __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
         fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, t);
 }
 
+// LUT forward with the table in global memory (tables past kMaxEntriesFwd; the reference's
+// Triton forward reads its table from global memory at any size, ekv_lut_triton.py:33-64):
+// the same tiling and cells, the gathers served by the L1/L2 caches.
+template <int MR, bool SPLITS>
+__global__ __launch_bounds__(kFwdWaves * 64) void fwd_global_kernel(FwdArgs a) {
+    const bool fast = coords_in_padded_range(a.partials, a.NP);
+    FwdTile t;
+    if (!fwd_tile<SPLITS>(a, MR, t)) return;
+    if (fast)
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{a.lut, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+    else
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{a.lut, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+}
+
 // Exact-formula forward (reference: ekv_triton.py:69-91): same tiling, no table.
 template <int MR, bool SPLITS>
 __global__ __launch_bounds__(kFwdWaves * 64) void fwd_exact_kernel(FwdArgs a) {
@@ -1410,6 +1427,29 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
                 a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
         if (MODE != kBwdTwoCopies) return;
     }
+}
+
+// LUT backward with the table in global memory (tables past kMaxEntriesBwd: the reference's
+// Triton backward, ekv_lut_triton.py:193-218, for CUDA_SHARED_BACKWARD off): interleaved
+// records read through the caches, lane-exchange dX (LDS holds the transpose buffers only
+// for the dVth-only launch, which has no dX).
+template <bool NEED_X, bool NEED_W>
+__global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_global_kernel(BwdArgs a) {
+    extern __shared__ float4 s_red_global[];
+    constexpr bool LANE_RED = NEED_X;
+    const bool fast = coords_in_padded_range(a.partials, a.NP);
+    const int waves = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* red = LANE_RED ? nullptr : reinterpret_cast<float*>(s_red_global) + wave * (kRedSlots * kRedStride);
+    const int item = blockIdx.x * waves + wave;
+    if (item >= a.n_items) return;
+    const BwdTableInterleaved t{a.lut};
+    if (fast)
+        bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<false, BwdTableInterleaved>, LANE_RED>(
+            a, LutBwdCell<false, BwdTableInterleaved>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+    else
+        bwd_body<kBwdKR, NEED_X, NEED_W, LutBwdCell<true, BwdTableInterleaved>, LANE_RED>(
+            a, LutBwdCell<true, BwdTableInterleaved>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
 }
 
 // Exact-formula backward (reference: ekv_triton.py:94-169): same work decomposition; LDS
@@ -2043,7 +2083,7 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
 struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
-    bool grad_padded, split, lane_red;
+    bool grad_padded, split, lane_red, gtab;
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
         bytes, lds_bytes;
 };
@@ -2063,13 +2103,15 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     const int mb = kRedSlots / kr;  // tokens per dX batch
     p.n_kb = (int)(p.Kp / kr);
     const size_t red_bytes = (size_t)kRedSlots * kRedStride * 4;
-    p.split = !exact && ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
-    const size_t lut_bytes = exact ? 0 : (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
+    p.gtab = !exact && n_entries > kMaxEntriesBwd;  // table read from global memory
+    p.split = !exact && !p.gtab && ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
+    const size_t lut_bytes =
+        exact || p.gtab ? 0 : (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
     // dX reduction across the wave: lane exchanges (no LDS; measured 5% faster at N = 4096
     // and, with the 8192-entry table, the only way to keep 16 waves per block), or the LDS
     // transpose buffers
     p.lane_red = !exact && need_x &&
-                 (ISA_EKV_BWD_LANE_RED == 1 ||
+                 (p.gtab || ISA_EKV_BWD_LANE_RED == 1 ||
                   (ISA_EKV_BWD_LANE_RED == 2 && lut_bytes + 16 * red_bytes > (size_t)kLdsBytes));
     const size_t per_wave = p.lane_red ? 0 : red_bytes;
     int wpb = 16;
@@ -2084,7 +2126,9 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     // blocks resident per CU: the table kernels fit ISA_EKV_BWD_MIN_BLOCKS 16-wave blocks in
     // their VGPR budget when the LDS holds that many tables; the exact kernels fit one
     const int64_t resident =
-        exact ? 1 : std::max<int64_t>(1, std::min<int64_t>(ISA_EKV_BWD_MIN_BLOCKS, (int64_t)(kLdsBytes / p.lds_bytes)));
+        exact ? 1
+              : std::max<int64_t>(1, std::min<int64_t>(ISA_EKV_BWD_MIN_BLOCKS,
+                                                       (int64_t)(kLdsBytes / std::max<size_t>(p.lds_bytes, 1))));
     const int64_t base_items = (int64_t)p.n_ob * p.n_kb;
     const int64_t max_splits = std::max<int64_t>(1, (M + kBwdMinSplitTokens - 1) / kBwdMinSplitTokens);
     const int64_t min_splits =
@@ -2156,8 +2200,18 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_
 }
 
 template <bool SPLITS>
-void launch_forward_split(bool exact, int mr, int wpb, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+void launch_forward_split(bool exact, bool gtab, int mr, int wpb, dim3 grid, size_t lds, hipStream_t s,
+                          const FwdArgs& fa) {
     const dim3 block(wpb * 64);
+    if (gtab) {
+        if (mr == 8)
+            hipLaunchKernelGGL((fwd_global_kernel<8, SPLITS>), grid, block, 0, s, fa);
+        else if (mr == 4)
+            hipLaunchKernelGGL((fwd_global_kernel<4, SPLITS>), grid, block, 0, s, fa);
+        else
+            hipLaunchKernelGGL((fwd_global_kernel<2, SPLITS>), grid, block, 0, s, fa);
+        return;
+    }
     if (exact) {
         if (mr == 8)
             hipLaunchKernelGGL((fwd_exact_kernel<8, SPLITS>), grid, block, 0, s, fa);
@@ -2175,11 +2229,12 @@ void launch_forward_split(bool exact, int mr, int wpb, dim3 grid, size_t lds, hi
         hipLaunchKernelGGL((fwd_kernel<2, SPLITS>), grid, block, lds, s, fa);
 }
 
-void launch_forward(bool exact, int mr, int wpb, dim3 grid, size_t lds, hipStream_t s, const FwdArgs& fa) {
+void launch_forward(bool exact, bool gtab, int mr, int wpb, dim3 grid, size_t lds, hipStream_t s,
+                    const FwdArgs& fa) {
     if (fa.n_split > 1)
-        launch_forward_split<true>(exact, mr, wpb, grid, lds, s, fa);
+        launch_forward_split<true>(exact, gtab, mr, wpb, grid, lds, s, fa);
     else
-        launch_forward_split<false>(exact, mr, wpb, grid, lds, s, fa);
+        launch_forward_split<false>(exact, gtab, mr, wpb, grid, lds, s, fa);
 }
 
 template <bool SPLIT, bool LANE_RED>
@@ -2211,9 +2266,16 @@ void launch_backward_copies(bool need_w, dim3 grid, dim3 block, size_t lds, hipS
     }
 }
 
-void launch_backward(bool exact, bool need_x, bool need_w, bool split, bool lane_red, dim3 grid, dim3 block,
-                     size_t lds, hipStream_t s, const BwdArgs& ba) {
-    if (exact) {
+void launch_backward(bool exact, bool gtab, bool need_x, bool need_w, bool split, bool lane_red, dim3 grid,
+                     dim3 block, size_t lds, hipStream_t s, const BwdArgs& ba) {
+    if (gtab) {
+        if (need_x && need_w)
+            hipLaunchKernelGGL((bwd_global_kernel<true, true>), grid, block, lds, s, ba);
+        else if (need_x)
+            hipLaunchKernelGGL((bwd_global_kernel<true, false>), grid, block, lds, s, ba);
+        else
+            hipLaunchKernelGGL((bwd_global_kernel<false, true>), grid, block, lds, s, ba);
+    } else if (exact) {
         if (need_x && need_w)
             hipLaunchKernelGGL((bwd_exact_kernel<true, true>), grid, block, lds, s, ba);
         else if (need_x)
@@ -2495,6 +2557,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.stat_bits = stat_bits;
     }
     size_t lds = 0;
+    const bool gtab = !cs.exact && cs.n_entries > kMaxEntriesFwd;  // table read from global memory
     if (cs.exact) {
         fa.out_scale = (float)cs.cur_scale;
         fa.k2 = cs.k2;
@@ -2505,12 +2568,12 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.cmin = (float)kPad;
         fa.cmax = (float)(kPad + cs.n_entries - 1);
         fa.out_scale = 1.0f;
-        lds = (size_t)fa.NP * 8;
+        lds = gtab ? 0 : (size_t)fa.NP * 8;
         // the second table copy (used when the thresholds spread wide, decided on the device)
         // when both copies still leave room for two forward blocks per CU
         const int t1 = fwd_copy_offset(cs.n_entries);
         const size_t lds2 = fwd_copy_lds(cs.n_entries);
-        if (lds2 <= (p.wpb == kFwdWaves ? kFwdCopyLdsBytes : (size_t)kLdsBytes)) {
+        if (!gtab && lds2 <= (p.wpb == kFwdWaves ? kFwdCopyLdsBytes : (size_t)kLdsBytes)) {
             fa.copy_offset = t1;
             lds = lds2;
             int* mode = reinterpret_cast<int*>(ws + p.off_mode);
@@ -2526,7 +2589,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
     set_split(p, ws, fa);
     ProfiledLaunch* prof;
     prof_start(s, 0, &prof);
-    launch_forward(cs.exact, p.mr, p.wpb, dim3(p.blocks), lds, s, fa);
+    launch_forward(cs.exact, gtab, p.mr, p.wpb, dim3(p.blocks), lds, s, fa);
     err = hipGetLastError();
     if (err == hipSuccess) err = finish_split(p, fa, !cs.exact, s);
     prof_stop(s, prof);
@@ -2671,7 +2734,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     if (copies)
         launch_backward_copies(need_w, grid, block, p.lds_bytes, s, ba);
     else
-        launch_backward(cs.exact, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
+        launch_backward(cs.exact, p.gtab, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
     err = hipGetLastError();
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "backward launch");
@@ -3020,9 +3083,9 @@ int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, 
                     void* stream) {
     const int rc = check_common(x, vth_pos, vth_neg, lut_fwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
     if (rc) return rc;
-    if (n_entries > kMaxEntriesFwd)
-        return fail(ISA_EKV_EINVAL, "LDS-resident forward supports LUT_DELTA_SIZE <= %d (got %d)",
-                    kMaxEntriesFwd, n_entries);
+    if (n_entries > kMaxEntriesGlobal)
+        return fail(ISA_EKV_EINVAL, "LUT forward supports LUT_DELTA_SIZE <= %d (got %d)", kMaxEntriesGlobal,
+                    n_entries);
     return run_forward(lut_setup(lut_fwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, M, K, O, v_sat,
                        out_min, out_max, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
@@ -3039,8 +3102,9 @@ int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg,
                      void* workspace, size_t workspace_bytes, void* stream) {
     const int rc = check_common(x, vth_pos, vth_neg, lut_bwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
     if (rc) return rc;
-    if (n_entries > kMaxEntriesBwd)
-        return fail(ISA_EKV_EINVAL, "shared backward supports LUT_DELTA_SIZE <= %d", kMaxEntriesBwd);
+    if (n_entries > kMaxEntriesGlobal)
+        return fail(ISA_EKV_EINVAL, "LUT backward supports LUT_DELTA_SIZE <= %d (got %d)", kMaxEntriesGlobal,
+                    n_entries);
     return run_backward(lut_setup(lut_bwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, grad_out, M, K,
                         O, v_sat, grad_x, grad_vth_pos, grad_vth_neg, workspace, workspace_bytes,
                         static_cast<hipStream_t>(stream));
@@ -3099,9 +3163,9 @@ int isa_ekv_layer_forward(const float* x, const float* vth_pos, const float* vth
     if (rc) return rc;
     rc = check_glue(glue, nullptr, false);
     if (rc) return rc;
-    if (n_entries > kMaxEntriesFwd)
-        return fail(ISA_EKV_EINVAL, "LDS-resident forward supports LUT_DELTA_SIZE <= %d (got %d)",
-                    kMaxEntriesFwd, n_entries);
+    if (n_entries > kMaxEntriesGlobal)
+        return fail(ISA_EKV_EINVAL, "LUT forward supports LUT_DELTA_SIZE <= %d (got %d)", kMaxEntriesGlobal,
+                    n_entries);
     return run_forward(lut_setup(lut_fwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, M, K, O, v_sat,
                        idiff_min, idiff_max, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream), glue,
                        idiff);
@@ -3116,8 +3180,9 @@ int isa_ekv_layer_backward(const float* x, const float* vth_pos, const float* vt
     if (rc) return rc;
     rc = check_glue(glue, glue_grads, grad_x != nullptr || M * K == 0);
     if (rc) return rc;
-    if (n_entries > kMaxEntriesBwd)
-        return fail(ISA_EKV_EINVAL, "shared backward supports LUT_DELTA_SIZE <= %d", kMaxEntriesBwd);
+    if (n_entries > kMaxEntriesGlobal)
+        return fail(ISA_EKV_EINVAL, "LUT backward supports LUT_DELTA_SIZE <= %d (got %d)", kMaxEntriesGlobal,
+                    n_entries);
     if (M * O > 0 && !idiff) return fail(ISA_EKV_EINVAL, "idiff is null");
     return run_backward(lut_setup(lut_bwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, grad_out, M, K,
                         O, v_sat, grad_x, grad_vth_pos, grad_vth_neg, workspace, workspace_bytes,

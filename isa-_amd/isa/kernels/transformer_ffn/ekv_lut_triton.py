@@ -8,9 +8,10 @@ HIP kernels of libisa_ekv_hip.so. Behaviour follows the reference:
 * forward: builds or fetches the tables for `cfg`, computes Idiff[M, O] in fp32 clamped to
   [V_signed_min, V_signed_max] (`ekv_lut_triton.py:136-161`);
 * backward: gradients for the inputs that need them, cast back to their dtypes, with the
-  reference's LUT_DELTA_SIZE <= 8192 limit and message (`:171-191`). The reference's
-  Triton fallback backward (`CUDA_SHARED_BACKWARD=0`, split-M atomics, `:193-218`) has no
-  separate counterpart: the one deterministic HIP backward serves both settings.
+  reference's LUT_DELTA_SIZE <= 8192 limit and message when `CUDA_SHARED_BACKWARD` is set
+  (`:171-191`). With it off the reference runs its Triton backward (split-M atomics,
+  `:193-218`) at any table size; here the same deterministic HIP backward serves both
+  settings, reading tables past 8192 entries from global memory.
 """
 
 from __future__ import annotations
@@ -49,7 +50,7 @@ class LUTTritonEKVMatmulFn(torch.autograd.Function):
     def backward(ctx, grad_out: torch.Tensor):
         x, wpos, wneg, _table_i, _table_ddelta = ctx.saved_tensors
         delta_min, delta_max, delta_size, v_sat = ctx.meta
-        if delta_size > ops.MAX_ENTRIES_BACKWARD:
+        if bool(ctx.cfg.get("CUDA_SHARED_BACKWARD", False)) and delta_size > ops.MAX_ENTRIES_BACKWARD:
             raise RuntimeError("CUDA shared EKV backward requires LUT_DELTA_SIZE <= 8192")
         need_x = bool(ctx.needs_input_grad[0])
         need_w = bool(ctx.needs_input_grad[1] or ctx.needs_input_grad[2])

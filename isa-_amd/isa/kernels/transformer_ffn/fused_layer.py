@@ -42,13 +42,14 @@ class FusedCIMLayerFn(torch.autograd.Function):
         ctx.save_for_backward(x, wpos, wneg, idiff, in_affine, r_tia, adc_scale, adc_shift)
         ctx.bwd_records = bwd_records
         ctx.meta = (delta_min, delta_max, size, float(cfg["V_sat"]), lo, hi, tuple(in_range))
+        ctx.shared_backward = bool(cfg.get("CUDA_SHARED_BACKWARD", False))
         return out
 
     @staticmethod
     def backward(ctx, grad_out: torch.Tensor):
         x, wpos, wneg, idiff, in_affine, r_tia, adc_scale, adc_shift = ctx.saved_tensors
         delta_min, delta_max, size, v_sat, lo, hi, in_range = ctx.meta
-        if size > ops.MAX_ENTRIES_BACKWARD:
+        if ctx.shared_backward and size > ops.MAX_ENTRIES_BACKWARD:  # the reference's limit and message
             raise RuntimeError("CUDA shared EKV backward requires LUT_DELTA_SIZE <= 8192")
         need = ctx.needs_input_grad
         res = ops.lut_layer_backward(

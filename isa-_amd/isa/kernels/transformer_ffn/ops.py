@@ -15,8 +15,9 @@ import torch
 
 from isa.kernels.transformer_ffn import _hip
 
-MAX_ENTRIES_FORWARD = 16384
-MAX_ENTRIES_BACKWARD = 8192
+MAX_ENTRIES_FORWARD = 16384   # forward table resident in LDS up to this size
+MAX_ENTRIES_BACKWARD = 8192   # backward table resident in LDS; the reference's shared-backward limit
+MAX_ENTRIES = 1 << 22         # larger tables up to this size are read from global memory
 
 
 def _require_cuda(t: torch.Tensor, name: str) -> None:
@@ -98,8 +99,8 @@ def lut_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_rec
     """Idiff[M, O] fp32 (clamped to [out_min, out_max])."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
-    if n_entries > MAX_ENTRIES_FORWARD:
-        raise RuntimeError(f"LDS-resident LUT forward supports LUT_DELTA_SIZE <= {MAX_ENTRIES_FORWARD}")
+    if n_entries > MAX_ENTRIES:
+        raise RuntimeError(f"LUT forward supports LUT_DELTA_SIZE <= {MAX_ENTRIES}")
     dev = x.device
     out = torch.empty((M, O), dtype=torch.float32, device=dev)
     if M == 0 or O == 0:
@@ -125,8 +126,8 @@ def lut_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_o
     _require_cuda(grad_out, "grad_out")
     if tuple(grad_out.shape) != (M, O):
         raise RuntimeError(f"grad_out must be [{M}, {O}], got {tuple(grad_out.shape)}")
-    if n_entries > MAX_ENTRIES_BACKWARD:
-        raise RuntimeError(f"shared backward supports LUT_DELTA_SIZE <= {MAX_ENTRIES_BACKWARD}")
+    if n_entries > MAX_ENTRIES:
+        raise RuntimeError(f"LUT backward supports LUT_DELTA_SIZE <= {MAX_ENTRIES}")
     dev = x.device
     gx = torch.empty((M, K), dtype=torch.float32, device=dev) if need_grad_x else None
     gp = torch.empty((O, K), dtype=torch.float32, device=dev) if need_grad_w else None
@@ -241,8 +242,8 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
     output statistics (cim.py:194-198), updated in place: maximum with max|y|, plus M * O."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
-    if n_entries > MAX_ENTRIES_FORWARD:
-        raise RuntimeError(f"LDS-resident LUT forward supports LUT_DELTA_SIZE <= {MAX_ENTRIES_FORWARD}")
+    if n_entries > MAX_ENTRIES:
+        raise RuntimeError(f"LUT forward supports LUT_DELTA_SIZE <= {MAX_ENTRIES}")
     dev = x.device
     aff = _glue_operand(in_affine, 2, "in_affine", dev)
     r = _glue_operand(r_tia, 1, "r_tia", dev)
@@ -282,8 +283,8 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
     _require_cuda(grad_out, "grad_out")
     if tuple(grad_out.shape) != (M, O) or tuple(idiff.shape) != (M, O):
         raise RuntimeError(f"grad_out and idiff must be [{M}, {O}]")
-    if n_entries > MAX_ENTRIES_BACKWARD:
-        raise RuntimeError(f"shared backward supports LUT_DELTA_SIZE <= {MAX_ENTRIES_BACKWARD}")
+    if n_entries > MAX_ENTRIES:
+        raise RuntimeError(f"LUT backward supports LUT_DELTA_SIZE <= {MAX_ENTRIES}")
     dev = x.device
     aff = _glue_operand(in_affine, 2, "in_affine", dev)
     r = _glue_operand(r_tia, 1, "r_tia", dev)

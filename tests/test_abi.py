@@ -81,7 +81,7 @@ def test_forward_rejects_bad_arguments_before_launch():
 
     assert call(M=-1) == -1 and "negative shape" in _err(lib)
     assert call(n=0) == -1 and "LUT_DELTA_SIZE" in _err(lib)
-    assert call(n=16385) == -1 and "16384" in _err(lib)
+    assert call(n=(1 << 22) + 1) == -1 and "4194304" in _err(lib)
     assert call(dmax=-10.0) == -1 and "delta_max > delta_min" in _err(lib)
     assert call(vsat=0.0) == -1 and "V_sat" in _err(lib)
     assert call() == -1 and "workspace too small" in _err(lib)
@@ -97,7 +97,7 @@ def test_backward_rejects_bad_arguments_before_launch():
         return lib.isa_ekv_backward(fake, fake, fake, fake, fake, 8, 8, 8, n, -9.0, 4.0, 8.26, gx, gp, gn,
                                     fake, ws_bytes, None)
 
-    assert call(n=8193) == -1 and "8192" in _err(lib)
+    assert call(n=(1 << 22) + 1) == -1 and "4194304" in _err(lib)
     assert call(gp=None) == -1 and "both" in _err(lib)
     assert call() == -1 and "workspace too small" in _err(lib)
     assert call(gx=None, gp=None, gn=None) == 0  # nothing requested

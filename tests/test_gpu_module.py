@@ -177,6 +177,32 @@ def test_backward_size_limit_message(cuda_device):
         out.sum().backward()
 
 
+def test_backward_large_table_without_shared_backward(cuda_device):
+    """With CUDA_SHARED_BACKWARD off the reference runs its Triton backward at any table size
+    (ekv_lut_triton.py:193-218); here the global-memory table kernels serve it, through the
+    autograd function and the fused CIMLinear layer alike."""
+    from isa.kernels.transformer_ffn.ekv_lut_triton import triton_lut_ekv_matmul
+    from isa.operators.cim import CIMLinear
+
+    cfg = flash_cfg(12000, CUDA_SHARED_BACKWARD=False)
+    x, vp, vn, g = make_inputs(8, 16, 32, seed=0)
+    dmin, dmax, n = oracle.lut_range(cfg)
+    ti, td = oracle.lut_tables(cfg)
+    xd = x.to(cuda_device).requires_grad_(True)
+    pd, nd = vp.to(cuda_device).requires_grad_(True), vn.to(cuda_device).requires_grad_(True)
+    out = triton_lut_ekv_matmul(xd, pd, nd, cfg)
+    out.backward(g.to(cuda_device))
+    X, P, N, G = (t.numpy() for t in (x, vp, vn, g))
+    assert errs(out.detach(), oracle.forward(X, P, N, ti, dmin, dmax, cfg["V_sat"]))[0] <= 1e-4
+    assert errs(xd.grad, oracle.grad_x(X, P, N, G, ti, td, dmin, dmax, cfg["V_sat"]))[0] <= 1e-3
+    rgp, rgn = oracle.grad_w(X, P, N, G, td, dmin, dmax, cfg["V_sat"])
+    assert errs(pd.grad, rgp)[0] <= 1e-3 and errs(nd.grad, rgn)[0] <= 1e-3
+    layer = CIMLinear(16, 32, cfg).to(cuda_device)
+    xl = (torch.rand(3, 5, 16, device=cuda_device) * 4.0).requires_grad_(True)
+    layer(xl).sum().backward()
+    assert torch.isfinite(xl.grad).all() and layer.vth_pos.grad is not None
+
+
 def test_prebuild(cuda_device, capsys):
     from isa.kernels.transformer_ffn import cuda_backend
 

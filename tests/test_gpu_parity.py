@@ -103,6 +103,32 @@ def test_parity_table_sizes(cuda_device, size):
     assert max(errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]) <= BWD_TOL
 
 
+@pytest.mark.parametrize("size", [12000, 16384, 32768])
+def test_parity_global_memory_tables(cuda_device, size):
+    """Tables past the LDS-resident limits (backward > 8192, forward > 16384 entries) are read
+    from global memory by their own kernels: parity in the clamp-free loop and, with
+    out-of-table coordinates, the clamping loop, plus a ragged K-split shape."""
+    cfg = flash_cfg(size, CUDA_SHARED_BACKWARD=False)
+    for (M, K, O), (x_mode, vth_mode) in (((48, 96, 300), ("mapped", "init")), ((33, 70, 130), ("wide", "wide")),
+                                          ((5, 900, 257), ("signed", "full"))):
+        print(f"[case] global-memory table {size}: M={M} K={K} O={O} {x_mode}/{vth_mode}", flush=True)
+        x, vp, vn, g = make_inputs(M, K, O, seed=size + M, x_mode=x_mode, vth_mode=vth_mode)
+        ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
+        out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf)
+        e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
+        assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (size, M, K, O, e)
+        again = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf)
+        for u, v in zip((out, gx, gp, gn), again):
+            assert torch.equal(u, v)
+    # gradient subsets through the same kernels
+    x, vp, vn, g = make_inputs(24, 40, 256, seed=3)
+    _, gx_all, gp_all, gn_all = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    _, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, need_x=True, need_w=False)
+    assert gp is None and torch.equal(gx, gx_all)
+    _, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, need_x=False, need_w=True)
+    assert gx is None and torch.equal(gp, gp_all) and torch.equal(gn, gn_all)
+
+
 def test_forward_16384_entries(cuda_device):
     """The forward keeps the reference's fallback LUT size (delta_lut.py:48) resident in LDS."""
     cfg = flash_cfg(16384)
