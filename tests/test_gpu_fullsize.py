@@ -77,13 +77,14 @@ def test_headline_equal_threshold_invariant(cuda_device):
     assert torch.equal(gp, -gn)
 
 
-@pytest.mark.parametrize("size,vth_mode", [(8192, "init"), (4096, "full")])
+@pytest.mark.parametrize("size,vth_mode", [(8192, "init"), (4096, "full"), (16384, "init")])
 def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     """The regimes where the kernels hold a second, bank-rotated table copy, at the headline
     fc1 shape: the 8192-entry table (its initial thresholds span ~135 records; the forward
     runs both copies in one 16-wave block per CU, each wave summing all 768 inputs) and
     thresholds spread over U[V_TH_MIN, V_TH_MAX] (forward copies, and the persistent
-    two-copy backward), checked on sampled exact sub-problems."""
+    two-copy backward); and the 16384-entry table (one 131 KB copy per CU in the forward, the
+    backward from global memory), checked on sampled exact sub-problems."""
     print(f"[case] headline fc1 with table copies: {size} entries, thresholds {vth_mode}", flush=True)
     cfg = flash_cfg(size)
     rng = np.random.default_rng(size)
