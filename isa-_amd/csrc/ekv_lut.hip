@@ -988,34 +988,57 @@ __device__ inline bool fwd_tile(const FwdArgs& a, int MR, FwdTile& t) {
 // ws - T1 (so c' = xs - ws' = c + T1). Writes nothing unless the launch is in copy mode.
 constexpr int kAssignThreads = 128;
 
-// The launch's table-copy mode (fwd_copies_mode) as a word for the launches that follow.
-__global__ __launch_bounds__(64) void copy_mode_kernel(const float2* __restrict__ partials, int NP, int* mode_word) {
-    const bool on = fwd_copies_mode(partials, NP);
+// Records [lo, lo + n) of the padded table hold every record the clamp-free loop reads, with
+// two records of margin each side (the second copy's coordinates c + T1 round separately).
+__device__ inline void coord_window(const CoordRange& c, int NP, int& lo, int& n) {
+    const int l = max(0, (int)floorf(c.xlo - c.whi) - 2);
+    const int h = min(NP - 1, (int)floorf(c.xhi - c.wlo) + 3);
+    lo = __builtin_amdgcn_readfirstlane(l);
+    n = __builtin_amdgcn_readfirstlane(h - l + 1);
+}
+
+// The launch's table-copy mode (fwd_copies_mode) as a word for the launches that follow;
+// tables longer than max_window records also need their coordinate window to fit it.
+__global__ __launch_bounds__(64) void copy_mode_kernel(const float2* __restrict__ partials, int NP, int max_window,
+                                                       int* mode_word) {
+    bool on = fwd_copies_mode(partials, NP);
+    if (on && NP > max_window) {
+        int lo, n;
+        coord_window(read_coord_range(partials), NP, lo, n);
+        on = n <= max_window;
+    }
     if (threadIdx.x == 0) *mode_word = on ? 1 : 0;
 }
 
+// LANES = 32: 8-byte records, gathered by half-waves over 32 bank pairs; LANES = 16: 16-byte
+// records, gathered by quarter-waves over 16 bank quads. Copy 1 sits LANES / 2 bins away.
+template <int LANES>
 __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2* __restrict__ wsT,
                                                               const int* __restrict__ mode_word, int64_t Kp,
                                                               int64_t Op, int copy_offset) {
+    static_assert(LANES == 32 || LANES == 16, "half-wave or quarter-wave gathers");
+    constexpr int kGroups = 64 / LANES, kMask = LANES - 1;
     if (__builtin_amdgcn_readfirstlane(*mode_word) == 0) return;
-    __shared__ float s_cnt[32][kAssignThreads];  // per-thread bank-pair loads; [bin][thread]: conflict-free
+    __shared__ float s_cnt[LANES][kAssignThreads];  // per-thread bank loads; [bin][thread]: conflict-free
     const int tid = threadIdx.x;
     const int64_t n_ot = Op / (64 * kFwdORR);
     const int64_t p = (int64_t)blockIdx.x * blockDim.x + tid;
-    if (p >= Kp * n_ot * kFwdORR * 4) return;
-    const int sign = (int)(p & 1), half = (int)((p >> 1) & 1), j = (int)((p >> 2) % kFwdORR);
-    const int64_t rest = (p >> 2) / kFwdORR;
+    if (p >= Kp * n_ot * kFwdORR * 2 * kGroups) return;
+    const int sign = (int)(p & 1), group = (int)((p >> 1) % kGroups);
+    const int64_t rest0 = (p >> 1) / kGroups;
+    const int j = (int)(rest0 % kFwdORR);
+    const int64_t rest = rest0 / kFwdORR;
     const int64_t tile = rest % n_ot, k = rest / n_ot;
     float* w0 = reinterpret_cast<float*>(wsT + k * Op + tile * 64 * kFwdORR + j) + sign;
     const int64_t lane_stride = 2 * kFwdORR;  // floats between consecutive lanes' records
     const float t1 = (float)copy_offset;
 #pragma unroll
-    for (int b = 0; b < 32; ++b) s_cnt[b][tid] = 0.0f;
+    for (int b = 0; b < LANES; ++b) s_cnt[b][tid] = 0.0f;
     unsigned chosen = 0;  // bit l: lane l took copy 1
-    float fls[32];        // integer coordinate parts of the lanes (registers: the loops unroll)
+    float fls[LANES];     // integer coordinate parts of the lanes (registers: the loops unroll)
 #pragma unroll
-    for (int l = 0; l < 32; ++l) {
-        float* wp = w0 + (int64_t)(32 * half + l) * lane_stride;
+    for (int l = 0; l < LANES; ++l) {
+        float* wp = w0 + (int64_t)(LANES * group + l) * lane_stride;
         const float w = *wp;
         const float fl = floorf(w);
         const float fr = w - fl;
@@ -1024,10 +1047,10 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
         for (int b = l - 1; b >= 0; --b)  // the earliest match wins
             if (fls[b] == fl) c = (chosen >> b) & 1;
         if (c < 0) {
-            // bank pair of the record at floor(u) - fl (weight 1 - fr) and one below (fr);
-            // floor(u) is common to the half-wave, so bin = -fl mod 32 (+16 for copy 1)
-            const int r0 = (-(int)fl) & 31, r1 = (r0 + 16) & 31;
-            const int m0 = (r0 + 31) & 31, m1 = (r1 + 31) & 31;
+            // bank bin of the record at floor(u) - fl (weight 1 - fr) and one below (fr);
+            // floor(u) is common to the lane group, so bin = -fl mod LANES (+LANES/2 for copy 1)
+            const int r0 = (-(int)fl) & kMask, r1 = (r0 + LANES / 2) & kMask;
+            const int m0 = (r0 + kMask) & kMask, m1 = (r1 + kMask) & kMask;
             const float v0 = (1.0f - fr) * s_cnt[r0][tid] + fr * s_cnt[m0][tid];
             const float v1 = (1.0f - fr) * s_cnt[r1][tid] + fr * s_cnt[m1][tid];
             c = v1 < v0 ? 1 : 0;
@@ -1370,20 +1393,35 @@ constexpr int kBwdAlone = 0, kBwdOneCopy = 1, kBwdTwoCopies = 2;
 // G traffic and lane exchanges per cell); its launch gets its own item count for them
 constexpr int kBwdKRTwoCopies = ISA_EKV_BWD_KR_TWO_COPIES;
 constexpr int kBwdCopyOffset = 2 * kSplitRecords + 16;
+// interleaved 16-byte records (tables past kSplitRecords, their coordinate window held): copy 1
+// 8 bank quads past copy 0's kSplitRecords records
+constexpr int kBwdCopyOffsetI = kSplitRecords + 8;
 constexpr size_t kBwdTwoCopiesLds = (size_t)(kBwdCopyOffset + 2 * kSplitRecords) * 8;
+constexpr size_t kBwdTwoCopiesLdsI = (size_t)(kBwdCopyOffsetI + kSplitRecords) * 16;
 
 template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false, int MODE = kBwdAlone>
 __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdArgs a) {
-    static_assert(MODE == kBwdAlone || SPLIT, "the second table copy uses the split layout");
+    static_assert(kSplitRecords % 16 == 0 && kBwdCopyOffsetI % 16 == 8, "copy 1 eight bank quads away");
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
     // which launch of a pair works: the copy assignment pass wrote the mode word. (Where the
-    // checks sit matters: reading anything before the table loop costs the one-copy kernel
-    // ~10 VGPRs and with them its second block per CU, so it checks after the loop.)
-    if constexpr (MODE == kBwdTwoCopies)
+    // checks sit matters: reading anything before the table loop costs the one-copy split
+    // kernel ~10 VGPRs and with them its second block per CU, so it checks after the loop;
+    // the interleaved one runs one block per CU in any case and checks first.)
+    int lo = 0, n_rec = a.NP;  // table records held: [lo, lo + n_rec)
+    if constexpr (MODE == kBwdTwoCopies) {
         if (__builtin_amdgcn_readfirstlane(*a.copy_mode) == 0) return;
-    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
-        const float4 rec = a.lut[i];
+        // tables past kSplitRecords hold the window the launch's coordinates reach (the mode
+        // word is set only when it fits)
+        if (a.NP > kSplitRecords) {
+            coord_window(read_coord_range(a.partials), a.NP, lo, n_rec);
+            n_rec = min(n_rec, kSplitRecords);  // as the mode word's test: the window fits
+        }
+    }
+    if constexpr (MODE == kBwdOneCopy && !SPLIT)
+        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
+    for (int i = threadIdx.x; i < n_rec; i += blockDim.x) {
+        const float4 rec = a.lut[lo + i];
         if constexpr (SPLIT) {
             s_split[i] = make_float2(rec.x, rec.y);
             s_split[i + kSplitRecords] = make_float2(rec.z, rec.w);
@@ -1394,10 +1432,15 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
             }
         } else {
             s_lut_bwd[i] = rec;
+            if constexpr (MODE == kBwdTwoCopies) {
+                const float t1 = (float)kBwdCopyOffsetI;
+                s_lut_bwd[kBwdCopyOffsetI + i] =
+                    make_float4(fmaf(-t1, rec.y, rec.x), rec.y, fmaf(-t1, rec.w, rec.z), rec.w);
+            }
         }
     }
     const bool fast = coords_in_padded_range(a.partials, a.NP);
-    if constexpr (MODE == kBwdOneCopy)
+    if constexpr (MODE == kBwdOneCopy && SPLIT)
         if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
     __syncthreads();
     const int waves = blockDim.x >> 6;
@@ -1408,9 +1451,9 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
     using Table = typename std::conditional<SPLIT, BwdTableSplit, BwdTableInterleaved>::type;
     Table t;
     if constexpr (SPLIT)
-        t = BwdTableSplit{s_split};
+        t = BwdTableSplit{s_split - lo};  // record i of the table at LDS record i - lo
     else
-        t = BwdTableInterleaved{s_lut_bwd};
+        t = BwdTableInterleaved{s_lut_bwd - lo};
     // The two-copy launch runs one block per CU (its 132 KB of LDS) over as many blocks as CUs,
     // each wave taking the plan's blocks in turn, so the launch costs little when it is not
     // the working one and loads its tables once per CU when it is.
@@ -2142,10 +2185,24 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
         const int64_t rounds = (blocks + slots - 1) / slots;
         return (double)blocks / (double)(rounds * slots);
     };
+    // interleaved tables (past kSplitRecords entries) may run the persistent two-copy launch
+    // instead (one 16-wave block per CU, kBwdKRTwoCopies inputs per wave, decided on the
+    // device): fill the rounds of both
+    const bool pair = !exact && !p.gtab && !p.split && p.lane_red && wpb == 16 && kBwdORR == kFwdORR;
+    auto fill_pair = [&](int64_t sp) {
+        const double f1 = fill_of(sp);
+        if (!pair) return f1;
+        const int64_t chunk = round_up((M + sp - 1) / sp, mb);
+        const int64_t n_sp = (M + chunk - 1) / chunk;
+        const int64_t items = (int64_t)p.n_ob * (p.Kp / kBwdKRTwoCopies) * n_sp;
+        const int64_t slots = (int64_t)kCUs * 16;
+        const int64_t rounds = (items + slots - 1) / slots;
+        return std::min(f1, (double)items / (double)(rounds * slots));
+    };
     double best_fill = 0.0;
-    for (int64_t sp = min_splits; sp <= top_splits; ++sp) best_fill = std::max(best_fill, fill_of(sp));
+    for (int64_t sp = min_splits; sp <= top_splits; ++sp) best_fill = std::max(best_fill, fill_pair(sp));
     int64_t best_splits = min_splits;
-    while (best_splits < top_splits && fill_of(best_splits) < best_fill - 0.005) ++best_splits;
+    while (best_splits < top_splits && fill_pair(best_splits) < best_fill - 0.005) ++best_splits;
     p.m_chunk = (int)round_up((M + best_splits - 1) / best_splits, mb);
     if (p.m_chunk < mb) p.m_chunk = mb;
     p.n_split = (int)((M + p.m_chunk - 1) / p.m_chunk);
@@ -2250,19 +2307,35 @@ void launch_backward_layout(bool need_x, bool need_w, dim3 grid, dim3 block, siz
 
 // The split-layout lane-exchange backward as a pair of launches (kBwdOneCopy, kBwdTwoCopies)
 // of which the device runs one; the same plan (grid, token splits, partial planes) serves both.
-void launch_backward_copies(bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s, const BwdArgs& ba0) {
+void launch_backward_copies(bool split, bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                            const BwdArgs& ba0) {
     const dim3 grid2(std::min<unsigned>(grid.x, kCUs));  // persistent: one block per CU
     BwdArgs ba2 = ba0;  // the two-copy kernel's inputs per wave
     ba2.n_kb = ba0.Kp / kBwdKRTwoCopies;
     ba2.n_items = ba0.n_ob * ba2.n_kb * ba0.n_split;
     const BwdArgs& ba = ba0;
     if (need_w) {
-        hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
-        hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s, ba2);
+        if (split)
+            hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
+        else
+            hipLaunchKernelGGL((bwd_kernel<true, true, false, true, kBwdOneCopy>), grid, block, lds, s, ba);
+        if (split)
+            hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s,
+                               ba2);
+        else
+            hipLaunchKernelGGL((bwd_kernel<true, true, false, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLdsI,
+                               s, ba2);
     } else {
-        hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
-        hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s,
-                           ba2);
+        if (split)
+            hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdOneCopy>), grid, block, lds, s, ba);
+        else
+            hipLaunchKernelGGL((bwd_kernel<true, false, false, true, kBwdOneCopy>), grid, block, lds, s, ba);
+        if (split)
+            hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s,
+                               ba2);
+        else
+            hipLaunchKernelGGL((bwd_kernel<true, false, false, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLdsI,
+                               s, ba2);
     }
 }
 
@@ -2577,9 +2650,9 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
             fa.copy_offset = t1;
             lds = lds2;
             int* mode = reinterpret_cast<int*>(ws + p.off_mode);
-            hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, fa.partials, fa.NP, mode);
+            hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, fa.partials, fa.NP, fa.NP, mode);
             const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
-            hipLaunchKernelGGL(fwd_copy_assign_kernel, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
+            hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
                                dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp,
                                p.Op, t1);
             err = hipGetLastError();
@@ -2716,15 +2789,22 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
     // the second table copy for wide threshold spreads: split layout with lane-exchange dX
     // (the plan's LDS then holds only the table, so both copies fit one block per CU)
-    const bool copies = kBwdORR == kFwdORR && !cs.exact && p.split && p.lane_red && need_x &&
-                        p.lds_bytes <= kBwdTwoCopiesLds / 2 && p.waves_per_block == 16;
+    // (tables past the split layout's length, the 8192-entry ones, take the copies when the
+    // coordinate window the launch reaches fits that length, decided on the device)
+    const bool copies = kBwdORR == kFwdORR && !cs.exact && !p.gtab && p.lane_red && need_x &&
+                        (p.split ? p.lds_bytes <= kBwdTwoCopiesLds / 2 : true) && p.waves_per_block == 16;
     if (copies) {
         int* mode = reinterpret_cast<int*>(ws + p.off_mode);
-        hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, ba.partials, ba.NP, mode);
-        const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * 4;
-        hipLaunchKernelGGL(fwd_copy_assign_kernel, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
-                           dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp, p.Op,
-                           kBwdCopyOffset);
+        hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, ba.partials, ba.NP, kSplitRecords, mode);
+        // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
+        const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * (p.split ? 4 : 8);
+        const dim3 agrid((unsigned)((problems + kAssignThreads - 1) / kAssignThreads));
+        if (p.split)
+            hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, agrid, dim3(kAssignThreads), 0, s,
+                               reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp, p.Op, kBwdCopyOffset);
+        else
+            hipLaunchKernelGGL(fwd_copy_assign_kernel<16>, agrid, dim3(kAssignThreads), 0, s,
+                               reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp, p.Op, kBwdCopyOffsetI);
         ba.copy_mode = mode;
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "backward copy assignment launch");
@@ -2732,7 +2812,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     ProfiledLaunch* prof;
     prof_start(s, 1, &prof);
     if (copies)
-        launch_backward_copies(need_w, grid, block, p.lds_bytes, s, ba);
+        launch_backward_copies(p.split, need_w, grid, block, p.lds_bytes, s, ba);
     else
         launch_backward(cs.exact, p.gtab, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
     err = hipGetLastError();

@@ -129,6 +129,26 @@ def test_parity_global_memory_tables(cuda_device, size):
     assert gx is None and torch.equal(gp, gp_all) and torch.equal(gn, gn_all)
 
 
+@pytest.mark.parametrize("x_mode,vth_mode", [("mapped", "init"), ("signed", "init"), ("wide", "wide"),
+                                             ("mapped", "full")])
+def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
+    """8192-entry tables: with mapped inputs the coordinates reach ~2700 of the 8224 records
+    and the backward holds two bank-rotated copies of that window (the thresholds span ~135
+    records); signed inputs reach too wide a window and wide thresholds need the clamping
+    loop, so those run one interleaved copy; thresholds over [0, 5] V with mapped inputs reach
+    too wide a window as well."""
+    print(f"[case] 8192 entries {x_mode}/{vth_mode}", flush=True)
+    cfg = flash_cfg(8192)
+    for M, K, O in ((64, 200, 300), (40, 768, 256)):
+        x, vp, vn, g = make_inputs(M, K, O, seed=M + K, x_mode=x_mode, vth_mode=vth_mode)
+        ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
+        out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf)
+        e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
+        assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (M, K, O, e)
+        _, gx2, gp2, gn2 = _dev_run(x, vp, vn, g, cfg, cuda_device, need_x=True, need_w=False)
+        assert torch.equal(gx2, gx)
+
+
 def test_forward_16384_entries(cuda_device):
     """The forward keeps the reference's fallback LUT size (delta_lut.py:48) resident in LDS."""
     cfg = flash_cfg(16384)
