@@ -542,6 +542,7 @@ __device__ inline bool coords_in_padded_range(const float2* __restrict__ partial
 constexpr float kFwdCopyMinWindow = 100.0f;  // threshold spread, in table records
 constexpr size_t kFwdCopyLdsBytes = 80 * 1024;  // both copies, with two forward blocks per CU
 constexpr int kFwdCopyMinInputs16 = 256;         // padded inputs per wave for the 16-wave copy blocks
+constexpr int kFwdWinOffset = kSplitRecords + 16;  // second copy of a coordinate window (16 mod 32)
 
 // second-copy offset (records, = 16 mod 32, past the first copy) and both copies' LDS bytes
 inline int fwd_copy_offset(int n_entries) { return (int)((n_entries + 2 * kPad - 16 + 31) / 32 * 32) + 16; }
@@ -791,6 +792,7 @@ struct FwdArgs {
     int n_split, k_chunk;
     float* split_part;
     int copy_offset;        // LUT: T1 > 0 when the launch may use the second table copy
+    int copy_window;        // LUT: > 0: the copies hold only the coordinate window, of at most this many records
 };
 
 // The work of one forward wave.
@@ -1063,31 +1065,48 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
     }
 }
 
-template <int MR, bool SPLITS>
+// WIN: the launch may hold two copies of only the coordinate window (tables whose two full
+// copies do not fit); the range is then read before the table load. Without WIN the load
+// comes first (reading the range first costs the 4096-entry kernels ~1%).
+template <int MR, bool SPLITS, bool WIN = false>
 __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
-    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
-    // fast loop and copy mode from one read of the range partials (as coords_in_padded_range
-    // and fwd_copies_mode decide them; a second read here costs the main loop ~50 VGPRs)
+    if constexpr (!WIN)
+        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
+    // fast loop and copy mode from one read of the range partials (as coords_in_padded_range,
+    // fwd_copies_mode and copy_mode_kernel decide them; a second read costs the main loop
+    // ~50 VGPRs)
     const CoordRange cr = read_coord_range(a.partials);
     const bool fast = __builtin_amdgcn_readfirstlane(
                           (int)((cr.xlo - cr.whi >= 1.0f) && (cr.xhi - cr.wlo <= (float)(a.NP - 2)))) != 0;
-    const bool copies = fast && a.copy_offset > 0 &&
-                        __builtin_amdgcn_readfirstlane((int)(cr.whi - cr.wlo >= kFwdCopyMinWindow)) != 0;
+    bool copies = fast && a.copy_offset > 0 &&
+                  __builtin_amdgcn_readfirstlane((int)(cr.whi - cr.wlo >= kFwdCopyMinWindow)) != 0;
+    int lo = 0, n_rec = a.NP;  // records held per copy: [lo, lo + n_rec)
+    if constexpr (WIN) {
+        if (copies) {
+            coord_window(cr, a.NP, lo, n_rec);
+            copies = n_rec <= a.copy_window;
+            if (!copies) lo = 0, n_rec = a.NP;
+        }
+        if (!copies)
+            for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
+    }
     if (copies) {  // record i of copy 1 holds {A - T1 dT, dT}: fma(c + T1, dT, A') = fma(c, dT, A)
         const float t1 = (float)a.copy_offset;
-        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
-            const float2 r = a.lut[i];
+        for (int i = threadIdx.x; i < n_rec; i += blockDim.x) {
+            const float2 r = a.lut[lo + i];
+            if constexpr (WIN) s_lut_fwd[i] = r;
             s_lut_fwd[a.copy_offset + i] = make_float2(fmaf(-t1, r.y, r.x), r.y);
         }
     }
     __syncthreads();
     FwdTile t;
     if (!fwd_tile<SPLITS>(a, MR, t)) return;
+    const float2* tab = WIN ? s_lut_fwd - lo : s_lut_fwd;  // record i of the table at LDS record i - lo
     if (fast)
-        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
     else
-        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{s_lut_fwd, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
 }
 
 // LUT forward with the table in global memory (tables past kMaxEntriesFwd; the reference's
@@ -2278,6 +2297,15 @@ void launch_forward_split(bool exact, bool gtab, int mr, int wpb, dim3 grid, siz
             hipLaunchKernelGGL((fwd_exact_kernel<2, SPLITS>), grid, block, 0, s, fa);
         return;
     }
+    if (fa.copy_window > 0) {
+        if (mr == 8)
+            hipLaunchKernelGGL((fwd_kernel<8, SPLITS, true>), grid, block, lds, s, fa);
+        else if (mr == 4)
+            hipLaunchKernelGGL((fwd_kernel<4, SPLITS, true>), grid, block, lds, s, fa);
+        else
+            hipLaunchKernelGGL((fwd_kernel<2, SPLITS, true>), grid, block, lds, s, fa);
+        return;
+    }
     if (mr == 8)
         hipLaunchKernelGGL((fwd_kernel<8, SPLITS>), grid, block, lds, s, fa);
     else if (mr == 4)
@@ -2644,13 +2672,24 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         lds = gtab ? 0 : (size_t)fa.NP * 8;
         // the second table copy (used when the thresholds spread wide, decided on the device)
         // when both copies still leave room for two forward blocks per CU
-        const int t1 = fwd_copy_offset(cs.n_entries);
-        const size_t lds2 = fwd_copy_lds(cs.n_entries);
-        if (!gtab && lds2 <= (p.wpb == kFwdWaves ? kFwdCopyLdsBytes : (size_t)kLdsBytes)) {
+        int t1 = fwd_copy_offset(cs.n_entries);
+        size_t lds2 = fwd_copy_lds(cs.n_entries);
+        const size_t lds_cap = p.wpb == kFwdWaves ? kFwdCopyLdsBytes : (size_t)kLdsBytes;
+        // tables whose two full copies do not fit copy only the coordinate window the launch
+        // reaches (decided on the device; the allocation also holds the whole table for the
+        // one-copy case)
+        const size_t lds_win = std::max(lds, (size_t)(kFwdWinOffset + kSplitRecords) * 8);
+        if (!gtab && lds2 > lds_cap && lds_win <= lds_cap) {
+            t1 = kFwdWinOffset;
+            lds2 = lds_win;
+            fa.copy_window = kSplitRecords;
+        }
+        if (!gtab && lds2 <= lds_cap) {
             fa.copy_offset = t1;
             lds = lds2;
             int* mode = reinterpret_cast<int*>(ws + p.off_mode);
-            hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, fa.partials, fa.NP, fa.NP, mode);
+            hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, fa.partials, fa.NP,
+                               fa.copy_window > 0 ? fa.copy_window : fa.NP, mode);
             const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
                                dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp,
