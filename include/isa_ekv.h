@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 7
+#define ISA_EKV_ABI_VERSION 8
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -250,6 +250,24 @@ int isa_ekv_measured_backward(const float* x, const int16_t* ids_a, const int16_
  * pointer may be null. Not thread-safe; for benchmarks. */
 int isa_ekv_profile_begin(void);
 int isa_ekv_profile_end(double* ms, int* launches);
+
+/* Plan of a LUT call at this shape (test and measurement aid, no reference counterpart).
+ * which: ISA_EKV_PLAN_FORWARD (isa_ekv_forward, isa_ekv_layer_forward), ISA_EKV_PLAN_BACKWARD
+ * (isa_ekv_backward), ISA_EKV_PLAN_LAYER_BACKWARD (isa_ekv_layer_backward). Writes
+ * min(n_info, ISA_EKV_PLAN_INFO_LEN) values (later slots get 0):
+ *   [0] workspace bytes
+ *   [1] byte offset in the workspace of the table-copy mode word (int32: after the call, 1 when
+ *       the main kernel ran with the second, bank-rotated table copy, 0 when with one copy),
+ *       or -1 when the call cannot use a second copy (the word is then not written)
+ *   [2] forward: K ranges summed separately (1: no split); backward: token splits
+ *   [3] forward: tokens per wave; backward: inputs per wave of the one-copy kernel
+ *   [4] main-kernel blocks   [5] waves per block   [6] LDS bytes per block */
+#define ISA_EKV_PLAN_FORWARD 0
+#define ISA_EKV_PLAN_BACKWARD 1
+#define ISA_EKV_PLAN_LAYER_BACKWARD 2
+#define ISA_EKV_PLAN_INFO_LEN 7
+int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x, int need_grad_w,
+                      int64_t* info, int n_info);
 
 /* Measurement aid, no reference counterpart: launches two 1024-thread blocks per CU, each
  * issuing 16 waves x 8 x `iterations` random LDS gathers of `record_bytes` (8: ds_read_b64,

@@ -389,7 +389,8 @@ __device__ inline void prep_tokens(const PrepArgs& a, float& lo, float& hi) {
         for (int j = 0; j < 4; ++j) {
             mj[j] = m;
             kj[j] = k;
-            xv[j] = (q < total && k < a.K) ? a.x[m * a.K + k] : 0.0f;
+            // padded inputs k >= K read input K - 1 (their records repeat its coordinate)
+            xv[j] = (q < total && a.K > 0) ? a.x[m * a.K + (k < a.K ? k : a.K - 1)] : 0.0f;
             q += blockDim.x;
             k += blockDim.x;
             while (k >= a.Kp) {
@@ -402,17 +403,23 @@ __device__ inline void prep_tokens(const PrepArgs& a, float& lo, float& hi) {
             const int64_t e = mj[j] * a.Kp + kj[j];
             if (e >= total) break;
             float c, r, f = 1.0f;
-            if (kj[j] < a.K) {
+            const bool real = kj[j] < a.K;
+            if (a.K > 0) {
+                // a padded input k >= K is input K - 1 again (coordinate, and thresholds on the
+                // threshold side) with r = 0: its cells read records the real cells read, so
+                // they stay inside any table window the range partials select, and add 0
                 float x = xv[j];
                 if (a.in_affine) x = input_map(x, aff_s, aff_b, a.in_lo, a.in_hi);
                 c = fmaf(x - a.xoff, a.scale, a.xadd);
-                r = 1.0f / (1.0f + x / a.v_sat);
+                r = real ? 1.0f / (1.0f + x / a.v_sat) : 0.0f;
                 if (EXACT) f = (float)exp2((double)x * a.scale_d);
-                const bool bad = c != c;
-                lo = fminf(lo, bad ? -INFINITY : c);
-                hi = fmaxf(hi, bad ? INFINITY : c);
+                if (real) {
+                    const bool bad = c != c;
+                    lo = fminf(lo, bad ? -INFINITY : c);
+                    hi = fmaxf(hi, bad ? INFINITY : c);
+                }
             } else {
-                c = a.pad_coord;  // padded inputs pair with zero thresholds: in range, r = 0
+                c = a.pad_coord;  // K == 0: every input is padding, paired with zero thresholds
                 r = 0.0f;
             }
             const float z = -r / a.z_div;
@@ -455,10 +462,11 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
             int64_t o = ot * 64 + rr;
             const int64_t k = kt * 32 + tx;
             float2 v = make_float2(0.0f, 0.0f);
-            if (k < a.K && a.O > 0) {
-                const bool real = o < a.O;
-                if (!real) o = a.O - 1;  // padded outputs copy a real row; results are dropped
-                v = make_float2(a.wp[o * a.K + k], a.wn[o * a.K + k]);
+            if (a.K > 0 && a.O > 0) {
+                const bool real = o < a.O && k < a.K;
+                if (o >= a.O) o = a.O - 1;  // padded outputs copy a real row; results are dropped
+                const int64_t kc = k < a.K ? k : a.K - 1;  // padded inputs copy input K - 1 (r = 0)
+                v = make_float2(a.wp[o * a.K + kc], a.wn[o * a.K + kc]);
                 if (real) {
                     const float p = v.x * a.scale, q = v.y * a.scale;
                     const bool bad = (p != p) || (q != q);
@@ -2605,21 +2613,61 @@ hipError_t finish_split(const FwdPlan& p, const FwdArgs& fa, bool clamp_out, hip
     return hipGetLastError();
 }
 
+// The forward plan of a call. LUT tables past 4096 entries hold their two copies (132 KB) in
+// one 16-wave block per CU, the same 16 waves per CU as two 8-wave blocks of one copy; that
+// pays when each wave sums a long K range (measured: 768 inputs per wave -7%, 64 or 128 +9%:
+// the block's table load, barrier and tail are spread over less work).
+FwdPlan plan_forward_call(bool exact, int n_entries, int64_t M, int64_t K, int64_t O) {
+    FwdPlan p = plan_forward(M, K, O, exact, true, kFwdWaves);
+    if (!exact && fwd_copy_lds(n_entries) > kFwdCopyLdsBytes && fwd_copy_lds(n_entries) <= (size_t)kLdsBytes) {
+        const FwdPlan p16 = plan_forward(M, K, O, false, true, 2 * kFwdWaves);
+        if (p16.k_chunk >= kFwdCopyMinInputs16) p = p16;
+    }
+    return p;
+}
+
+// Table placement of a LUT forward launch with wpb waves per block: LDS bytes, and the second
+// table copy (copy_offset > 0: the launch may use it, decided on the device from the range
+// partials and recorded in the mode word; copy_window > 0: the copies hold only the
+// coordinate window, of at most that many records).
+struct FwdTableCfg {
+    bool gtab;  // table read from global memory
+    size_t lds;
+    int copy_offset, copy_window;
+};
+
+FwdTableCfg fwd_table_cfg(int n_entries, int wpb) {
+    FwdTableCfg t{};
+    t.gtab = n_entries > kMaxEntriesFwd;
+    t.lds = t.gtab ? 0 : (size_t)lut_records(n_entries) * 8;
+    if (t.gtab) return t;
+    // the second table copy (used when the thresholds spread wide) when both copies still
+    // leave room for two forward blocks per CU
+    int t1 = fwd_copy_offset(n_entries);
+    size_t lds2 = fwd_copy_lds(n_entries);
+    const size_t lds_cap = wpb == kFwdWaves ? kFwdCopyLdsBytes : (size_t)kLdsBytes;
+    // tables whose two full copies do not fit copy only the coordinate window the launch
+    // reaches (the allocation also holds the whole table for the one-copy case)
+    const size_t lds_win = std::max(t.lds, (size_t)(kFwdWinOffset + kSplitRecords) * 8);
+    if (lds2 > lds_cap && lds_win <= lds_cap) {
+        t1 = kFwdWinOffset;
+        lds2 = lds_win;
+        t.copy_window = kSplitRecords;
+    }
+    if (lds2 <= lds_cap) {
+        t.copy_offset = t1;
+        t.lds = lds2;
+    }
+    return t;
+}
+
 int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg, int64_t M,
                 int64_t K, int64_t O, float v_sat, float out_min, float out_max, float* out, void* workspace,
                 size_t workspace_bytes, hipStream_t s, const isa_ekv_glue* glue = nullptr,
                 float* idiff = nullptr) {
     if (M == 0 || O == 0) return 0;
     if (!out) return fail(ISA_EKV_EINVAL, "out is null");
-    // LUT tables past 4096 entries hold their two copies (132 KB) in one 16-wave block per CU,
-    // the same 16 waves per CU as two 8-wave blocks of one copy; that pays when each wave sums
-    // a long K range (measured: 768 inputs per wave -7%, 64 or 128 +9%: the block's table
-    // load, barrier and tail are spread over less work)
-    FwdPlan p = plan_forward(M, K, O, cs.exact, true, kFwdWaves);
-    if (!cs.exact && fwd_copy_lds(cs.n_entries) > kFwdCopyLdsBytes && fwd_copy_lds(cs.n_entries) <= (size_t)kLdsBytes) {
-        const FwdPlan p16 = plan_forward(M, K, O, false, true, 2 * kFwdWaves);
-        if (p16.k_chunk >= kFwdCopyMinInputs16) p = p16;
-    }
+    const FwdPlan p = plan_forward_call(cs.exact, cs.n_entries, M, K, O);
     if (!workspace || workspace_bytes < p.bytes)
         return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
     char* ws = static_cast<char*>(workspace);
@@ -2658,7 +2706,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.stat_bits = stat_bits;
     }
     size_t lds = 0;
-    const bool gtab = !cs.exact && cs.n_entries > kMaxEntriesFwd;  // table read from global memory
+    bool gtab = false;
     if (cs.exact) {
         fa.out_scale = (float)cs.cur_scale;
         fa.k2 = cs.k2;
@@ -2669,31 +2717,19 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.cmin = (float)kPad;
         fa.cmax = (float)(kPad + cs.n_entries - 1);
         fa.out_scale = 1.0f;
-        lds = gtab ? 0 : (size_t)fa.NP * 8;
-        // the second table copy (used when the thresholds spread wide, decided on the device)
-        // when both copies still leave room for two forward blocks per CU
-        int t1 = fwd_copy_offset(cs.n_entries);
-        size_t lds2 = fwd_copy_lds(cs.n_entries);
-        const size_t lds_cap = p.wpb == kFwdWaves ? kFwdCopyLdsBytes : (size_t)kLdsBytes;
-        // tables whose two full copies do not fit copy only the coordinate window the launch
-        // reaches (decided on the device; the allocation also holds the whole table for the
-        // one-copy case)
-        const size_t lds_win = std::max(lds, (size_t)(kFwdWinOffset + kSplitRecords) * 8);
-        if (!gtab && lds2 > lds_cap && lds_win <= lds_cap) {
-            t1 = kFwdWinOffset;
-            lds2 = lds_win;
-            fa.copy_window = kSplitRecords;
-        }
-        if (!gtab && lds2 <= lds_cap) {
-            fa.copy_offset = t1;
-            lds = lds2;
+        const FwdTableCfg tc = fwd_table_cfg(cs.n_entries, p.wpb);
+        gtab = tc.gtab;
+        lds = tc.lds;
+        fa.copy_offset = tc.copy_offset;
+        fa.copy_window = tc.copy_window;
+        if (tc.copy_offset > 0) {
             int* mode = reinterpret_cast<int*>(ws + p.off_mode);
             hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, fa.partials, fa.NP,
                                fa.copy_window > 0 ? fa.copy_window : fa.NP, mode);
             const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
                                dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp,
-                               p.Op, t1);
+                               p.Op, tc.copy_offset);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward copy assignment launch");
         }
@@ -2713,6 +2749,16 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         if (err != hipSuccess) return hip_fail(err, "output statistics launch");
     }
     return 0;
+}
+
+// Whether a table backward enqueues the second-copy pair of launches (the device then picks
+// one and records it in the mode word): split layout with lane-exchange dX, whose LDS holds
+// only the table, so both copies fit one block per CU; tables past the split layout's length
+// (the 8192-entry ones) take the copies when the coordinate window the launch reaches fits
+// that length, which the device decides.
+bool bwd_may_use_copies(const BwdPlan& p, bool exact, bool need_x) {
+    return kBwdORR == kFwdORR && !exact && !p.gtab && p.lane_red && need_x &&
+           (p.split ? p.lds_bytes <= kBwdTwoCopiesLds / 2 : true) && p.waves_per_block == 16;
 }
 
 void zero_fill(float* p, int64_t n, hipStream_t s) {
@@ -2826,12 +2872,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         ba.cmax = (float)(kPad + cs.n_entries - 1);
     }
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
-    // the second table copy for wide threshold spreads: split layout with lane-exchange dX
-    // (the plan's LDS then holds only the table, so both copies fit one block per CU)
-    // (tables past the split layout's length, the 8192-entry ones, take the copies when the
-    // coordinate window the launch reaches fits that length, decided on the device)
-    const bool copies = kBwdORR == kFwdORR && !cs.exact && !p.gtab && p.lane_red && need_x &&
-                        (p.split ? p.lds_bytes <= kBwdTwoCopiesLds / 2 : true) && p.waves_per_block == 16;
+    const bool copies = bwd_may_use_copies(p, cs.exact, need_x);
     if (copies) {
         int* mode = reinterpret_cast<int*>(ws + p.off_mode);
         hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, ba.partials, ba.NP, kSplitRecords, mode);
@@ -3348,6 +3389,40 @@ int isa_ekv_measured_backward(const float* x, const int16_t* ids_a, const int16_
     return run_measured_backward(x, reinterpret_cast<const short*>(ids_a), reinterpret_cast<const short*>(ids_b), M,
                                  K, O, codebook, current_scale, grad_out, out_pre, r_tia, out_min, out_max, grad_x,
                                  workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x, int need_grad_w,
+                      int64_t* info, int n_info) {
+    if (!info || n_info < 1) return fail(ISA_EKV_EINVAL, "info is null");
+    if (M < 0 || K < 0 || O < 0) return fail(ISA_EKV_EINVAL, "negative shape");
+    if (n_entries < 1 || n_entries > kMaxEntriesGlobal)
+        return fail(ISA_EKV_EINVAL, "LUT_DELTA_SIZE must be in [1, %d] (got %d)", kMaxEntriesGlobal, n_entries);
+    int64_t v[ISA_EKV_PLAN_INFO_LEN];
+    if (which == ISA_EKV_PLAN_FORWARD) {
+        const FwdPlan p = plan_forward_call(false, n_entries, M, K, O);
+        const FwdTableCfg tc = fwd_table_cfg(n_entries, p.wpb);
+        v[0] = (int64_t)p.bytes;
+        v[1] = tc.copy_offset > 0 ? (int64_t)p.off_mode : -1;
+        v[2] = p.n_split;
+        v[3] = p.mr;
+        v[4] = p.blocks;
+        v[5] = p.wpb;
+        v[6] = (int64_t)tc.lds;
+    } else if (which == ISA_EKV_PLAN_BACKWARD || which == ISA_EKV_PLAN_LAYER_BACKWARD) {
+        const bool nx = need_grad_x != 0, nw = need_grad_w != 0;
+        const BwdPlan p = plan_backward(M, K, O, n_entries, nx, nw, which == ISA_EKV_PLAN_LAYER_BACKWARD);
+        v[0] = (int64_t)p.bytes;
+        v[1] = bwd_may_use_copies(p, false, nx) ? (int64_t)p.off_mode : -1;
+        v[2] = p.n_split;
+        v[3] = p.Kp / p.n_kb;
+        v[4] = p.blocks;
+        v[5] = p.waves_per_block;
+        v[6] = (int64_t)p.lds_bytes;
+    } else {
+        return fail(ISA_EKV_EINVAL, "unknown plan kind %d", which);
+    }
+    for (int i = 0; i < n_info; ++i) info[i] = i < ISA_EKV_PLAN_INFO_LEN ? v[i] : 0;
+    return 0;
 }
 
 int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iterations, float* out, int64_t out_floats,

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -21,6 +21,11 @@ LUT_PLAIN_F32 = 0
 LUT_FWD = 1
 LUT_BWD = 2
 LUT_PLAIN_BF16 = 3
+
+PLAN_FORWARD = 0
+PLAN_BACKWARD = 1
+PLAN_LAYER_BACKWARD = 2
+PLAN_INFO_LEN = 7
 
 EXPORTS = (
     "isa_ekv_abi_version",
@@ -48,6 +53,7 @@ EXPORTS = (
     "isa_ekv_profile_begin",
     "isa_ekv_profile_end",
     "isa_ekv_probe_lds_gather",
+    "isa_ekv_plan_info",
 )
 
 _lock = threading.Lock()
@@ -170,6 +176,8 @@ def _declare(lib) -> None:
     lib.isa_ekv_profile_end.restype = ci
     lib.isa_ekv_probe_lds_gather.argtypes = [ci, ci, ci, vp, i64, ctypes.POINTER(ci), vp]
     lib.isa_ekv_probe_lds_gather.restype = ci
+    lib.isa_ekv_plan_info.argtypes = [ci, i64, i64, i64, ci, ci, ci, ctypes.POINTER(i64), ci]
+    lib.isa_ekv_plan_info.restype = ci
 
 
 def load(path: Path | None = None):

@@ -37,8 +37,44 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+def _workspace(nbytes: int, device: torch.device, given: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The call's workspace: `given` (a caller's uint8 device buffer, checked) or a new one."""
+    if given is None:
+        return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+    _require_cuda(given, "workspace")
+    if given.dtype != torch.uint8 or not given.is_contiguous() or given.device != device:
+        raise RuntimeError(f"workspace must be a contiguous uint8 tensor on {device}")
+    if given.numel() < nbytes or given.data_ptr() % 256:
+        raise RuntimeError(f"workspace needs {int(nbytes)} bytes at a 256-byte aligned address")
+    return given
+
+
+_PLAN_KINDS = {"forward": _hip.PLAN_FORWARD, "backward": _hip.PLAN_BACKWARD,
+               "layer_backward": _hip.PLAN_LAYER_BACKWARD}
+
+
+def plan_info(kind: str, M: int, K: int, O: int, n_entries: int, need_grad_x: bool = True,
+              need_grad_w: bool = True) -> dict:
+    """The library's plan for a LUT call at this shape (isa_ekv_plan_info): workspace bytes,
+    the byte offset of the table-copy mode word in the workspace (-1 when the call has none),
+    K splits (forward) or token splits (backward), tokens (forward) or inputs (backward) per
+    wave, main-kernel blocks, waves per block and LDS bytes per block."""
+    lib = _hip.load()
+    info = (ctypes.c_int64 * _hip.PLAN_INFO_LEN)()
+    rc = lib.isa_ekv_plan_info(_PLAN_KINDS[kind], int(M), int(K), int(O), int(n_entries), int(need_grad_x),
+                               int(need_grad_w), info, _hip.PLAN_INFO_LEN)
+    _hip.check(rc, "isa_ekv_plan_info")
+    keys = ("workspace_bytes", "mode_offset", "splits", "per_wave", "blocks", "waves_per_block", "lds_bytes")
+    return dict(zip(keys, (int(v) for v in info)))
+
+
+def copy_mode(workspace: torch.Tensor, plan: dict) -> Optional[int]:
+    """After a call that used `workspace` (and synchronised), whether its main kernel ran with
+    the second table copy (1) or one copy (0); None when the plan has no second copy."""
+    off = plan["mode_offset"]
+    if off < 0:
+        return None
+    return int(workspace[off:off + 4].view(torch.int32).item())
 
 
 def build_plain_tables(params: Tuple[float, float, float, float], delta_min: float, delta_max: float,
@@ -95,8 +131,9 @@ def _check_operands(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor) -> 
 
 def lut_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_records: torch.Tensor,
                 n_entries: int, delta_min: float, delta_max: float, v_sat: float,
-                out_min: float, out_max: float) -> torch.Tensor:
-    """Idiff[M, O] fp32 (clamped to [out_min, out_max])."""
+                out_min: float, out_max: float, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Idiff[M, O] fp32 (clamped to [out_min, out_max]). workspace: optional caller buffer
+    (uint8, at least isa_ekv_forward_workspace bytes)."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
     if n_entries > MAX_ENTRIES:
@@ -107,7 +144,7 @@ def lut_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_rec
         return out
     x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
     ws_bytes = lib.isa_ekv_forward_workspace(M, K, O)
-    ws = _workspace(ws_bytes, dev)
+    ws = _workspace(ws_bytes, dev, workspace)
     with torch.cuda.device(dev):
         rc = lib.isa_ekv_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), fwd_records.data_ptr(), M, K, O,
                                  int(n_entries), float(delta_min), float(delta_max), float(v_sat),
@@ -119,8 +156,8 @@ def lut_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_rec
 
 def lut_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_out: torch.Tensor,
                  bwd_records: torch.Tensor, n_entries: int, delta_min: float, delta_max: float, v_sat: float,
-                 need_grad_x: bool, need_grad_w: bool):
-    """(dX | None, dVth+ | None, dVth- | None), all fp32."""
+                 need_grad_x: bool, need_grad_w: bool, workspace: Optional[torch.Tensor] = None):
+    """(dX | None, dVth+ | None, dVth- | None), all fp32. workspace: optional caller buffer."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
     _require_cuda(grad_out, "grad_out")
@@ -136,7 +173,7 @@ def lut_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_o
         return gx, gp, gn
     x32, wp32, wn32, g32 = (as_kernel_f32(t) for t in (x, wpos, wneg, grad_out))
     ws_bytes = lib.isa_ekv_backward_workspace(M, K, O, int(n_entries), int(need_grad_x), int(need_grad_w))
-    ws = _workspace(ws_bytes, dev)
+    ws = _workspace(ws_bytes, dev, workspace)
     with torch.cuda.device(dev):
         rc = lib.isa_ekv_backward(_ptr(x32), _ptr(wp32), _ptr(wn32), _ptr(g32), bwd_records.data_ptr(), M, K, O,
                                   int(n_entries), float(delta_min), float(delta_max), float(v_sat),
@@ -235,11 +272,13 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
                       idiff_max: float, *, in_affine: Optional[torch.Tensor] = None, in_range=(0.0, 4.0),
                       r_tia: Optional[torch.Tensor] = None, y_range=(-4.0, 4.0),
                       adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None,
-                      stat_abs_max: Optional[torch.Tensor] = None, stat_total: Optional[torch.Tensor] = None):
+                      stat_abs_max: Optional[torch.Tensor] = None, stat_total: Optional[torch.Tensor] = None,
+                      workspace: Optional[torch.Tensor] = None):
     """(out, idiff) of the LUT projection with its glue fused: x -> clamp(x*s + b) ->
     Idiff (clamped to [idiff_min, idiff_max]) -> y = clamp(Idiff * r_tia) -> y * adc_scale +
     adc_shift. stat_abs_max (fp32) and stat_total (fp64), one element each, are CIMLinear's
-    output statistics (cim.py:194-198), updated in place: maximum with max|y|, plus M * O."""
+    output statistics (cim.py:194-198), updated in place: maximum with max|y|, plus M * O.
+    workspace: optional caller buffer."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
     if n_entries > MAX_ENTRIES:
@@ -259,7 +298,7 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
         return out, idiff
     x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
     glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c, s_max, s_tot)
-    ws = _workspace(lib.isa_ekv_layer_forward_workspace(M, K, O), dev)
+    ws = _workspace(lib.isa_ekv_layer_forward_workspace(M, K, O), dev, workspace)
     with torch.cuda.device(dev):
         rc = lib.isa_ekv_layer_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), fwd_records.data_ptr(), M, K, O,
                                        int(n_entries), float(delta_min), float(delta_max), float(v_sat),
@@ -275,9 +314,11 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
                        in_affine: Optional[torch.Tensor] = None, in_range=(0.0, 4.0),
                        r_tia: Optional[torch.Tensor] = None, y_range=(-4.0, 4.0),
                        adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None,
-                       need_in_affine: bool = False, need_r_tia: bool = False, need_adc: bool = False):
+                       need_in_affine: bool = False, need_r_tia: bool = False, need_adc: bool = False,
+                       workspace: Optional[torch.Tensor] = None):
     """Gradients of lut_layer_forward's out: dict with dx, dvth_pos, dvth_neg, d_in_affine,
-    d_r_tia, d_adc_scale, d_adc_shift (None where not requested), all fp32."""
+    d_r_tia, d_adc_scale, d_adc_shift (None where not requested), all fp32. workspace:
+    optional caller buffer."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
     _require_cuda(grad_out, "grad_out")
@@ -311,7 +352,8 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
         return res
     x32, wp32, wn32, g32, id32 = (as_kernel_f32(t) for t in (x, wpos, wneg, grad_out, idiff))
     glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c)
-    ws = _workspace(lib.isa_ekv_layer_backward_workspace(M, K, O, int(n_entries), int(need_x), int(need_grad_w)), dev)
+    ws = _workspace(lib.isa_ekv_layer_backward_workspace(M, K, O, int(n_entries), int(need_x), int(need_grad_w)), dev,
+                    workspace)
     with torch.cuda.device(dev):
         rc = lib.isa_ekv_layer_backward(_ptr(x32), _ptr(wp32), _ptr(wn32), _ptr(g32), _ptr(id32),
                                         bwd_records.data_ptr(), M, K, O, int(n_entries), float(delta_min),

@@ -221,3 +221,33 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_hip, "_lib", None)
     with pytest.raises(_hip.HipExtensionError, match="not found"):
         _hip.load(tmp_path / "absent.so")
+
+
+def test_plan_info_reports_the_call_plans():
+    """isa_ekv_plan_info (host-side planning only): workspace sizes agree with the workspace
+    queries, and the table-copy mode word exists exactly where a second copy can be used."""
+    from isa.kernels.transformer_ffn import ops
+
+    lib = _hip.load()
+    f = ops.plan_info("forward", 8192, 768, 3072, 4096)
+    assert 0 < f["workspace_bytes"] <= lib.isa_ekv_forward_workspace(8192, 768, 3072)
+    assert f["mode_offset"] >= 0 and f["mode_offset"] % 4 == 0
+    assert f["splits"] == 1 and f["waves_per_block"] == 8
+    b = ops.plan_info("backward", 8192, 768, 3072, 4096)
+    assert b["workspace_bytes"] == lib.isa_ekv_backward_workspace(8192, 768, 3072, 4096, 1, 1)
+    assert b["mode_offset"] >= 0 and b["splits"] >= 1 and b["waves_per_block"] == 16
+    lb = ops.plan_info("layer_backward", 8192, 3072, 768, 4096)
+    assert lb["workspace_bytes"] == lib.isa_ekv_layer_backward_workspace(8192, 3072, 768, 4096, 1, 1)
+    # fc2 of the headline (O = 768, three output blocks) splits K to fill the chip
+    assert ops.plan_info("forward", 8192, 3072, 768, 4096)["splits"] > 1
+    # 8192 entries, 768 inputs per wave: both copies in one 16-wave block per CU
+    f8 = ops.plan_info("forward", 8192, 768, 3072, 8192)
+    assert f8["waves_per_block"] == 16 and f8["mode_offset"] >= 0
+    # 16384 entries: one LDS copy in the forward, global-memory backward, no mode word
+    assert ops.plan_info("forward", 8192, 768, 3072, 16384)["mode_offset"] == -1
+    assert ops.plan_info("backward", 8192, 768, 3072, 16384)["mode_offset"] == -1
+    # a dVth-only backward runs no copy pair
+    assert ops.plan_info("backward", 512, 64, 256, 4096, need_grad_x=False)["mode_offset"] == -1
+    info = (ctypes.c_int64 * 7)()
+    assert lib.isa_ekv_plan_info(9, 1, 1, 1, 4096, 1, 1, info, 7) == -1 and "plan kind" in _err(lib)
+    assert lib.isa_ekv_plan_info(0, 1, 1, 1, 0, 1, 1, info, 7) == -1 and "LUT_DELTA_SIZE" in _err(lib)

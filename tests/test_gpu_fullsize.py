@@ -18,15 +18,24 @@ from tests.helpers import errs, flash_cfg, make_inputs
 pytestmark = pytest.mark.gpu
 
 
-def _run(x, vp, vn, g, cfg, dev):
+def _run(x, vp, vn, g, cfg, dev, modes=None):
+    """Forward and backward through the C ABI; modes (a dict) receives the table-copy mode each
+    main kernel ran in (1 two copies, 0 one copy, None no second copy in the plan)."""
     from isa.approximations.delta_lut import get_packed_tables, lut_range
     from isa.kernels.transformer_ffn import ops
 
     dmin, dmax, n = lut_range(cfg)
     fwd, bwd = get_packed_tables(cfg, dev)
-    out = ops.lut_forward(x, vp, vn, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0)
-    gx, gp, gn = ops.lut_backward(x, vp, vn, g, bwd, n, dmin, dmax, cfg["V_sat"], True, True)
+    M, K = x.shape
+    O = vp.shape[0]
+    pf, pb = ops.plan_info("forward", M, K, O, n), ops.plan_info("backward", M, K, O, n)
+    wsf = torch.empty(pf["workspace_bytes"], dtype=torch.uint8, device=dev)
+    wsb = torch.empty(pb["workspace_bytes"], dtype=torch.uint8, device=dev)
+    out = ops.lut_forward(x, vp, vn, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0, workspace=wsf)
+    gx, gp, gn = ops.lut_backward(x, vp, vn, g, bwd, n, dmin, dmax, cfg["V_sat"], True, True, workspace=wsb)
     torch.cuda.synchronize()
+    if modes is not None:
+        modes["fwd"], modes["bwd"] = ops.copy_mode(wsf, pf), ops.copy_mode(wsb, pb)
     return out, gx, gp, gn
 
 
@@ -52,7 +61,9 @@ def test_headline_ffn_layers(cuda_device):
     cfg = flash_cfg(4096)
     rng = np.random.default_rng(0)
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=0))
-    res1 = _run(x, vp, vn, g, cfg, cuda_device)
+    modes = {}
+    res1 = _run(x, vp, vn, g, cfg, cuda_device, modes)
+    assert modes == {"fwd": 0, "bwd": 0}, modes  # the initial thresholds span ~69 records: one copy
     _check_samples(x, vp, vn, g, res1, cfg, rng)
     # fc2 is driven by the TIA output of fc1: clamp(R_TIA * Idiff, -4, 4) (cim.py:192-193)
     x2 = (res1[0] * 1e5).clamp(-4.0, 4.0).contiguous()
@@ -89,7 +100,10 @@ def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     cfg = flash_cfg(size)
     rng = np.random.default_rng(size)
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=7, vth_mode=vth_mode))
-    res = _run(x, vp, vn, g, cfg, cuda_device)
+    modes = {}
+    res = _run(x, vp, vn, g, cfg, cuda_device, modes)
+    expect = None if size > 8192 else 1  # 16384 entries: no LDS room for a second copy
+    assert modes == {"fwd": expect, "bwd": expect}, modes
     _check_samples(x, vp, vn, g, res, cfg, rng)
     again = _run(x, vp, vn, g, cfg, cuda_device)
     for a, b in zip(res, again):
