@@ -91,6 +91,20 @@ int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, 
                     float out_min, float out_max, float* out, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* isa_ekv_forward without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid it). No
+ * counterpart in the reference. Same arguments, results and errors as isa_ekv_forward, bitwise
+ * equal outputs; the call allocates nothing (no hipMalloc/hipFree, no allocating library
+ * routine, no profiling events). Its scratch is a file-scope device array of
+ * ISA_EKV_NOALLOC_MAX_BYTES that each device the library runs on holds until the process
+ * ends; shapes whose forward needs more (isa_ekv_plan_info slot [0]) are rejected with
+ * ISA_EKV_EINVAL before anything is enqueued. All calls on one device share that array:
+ * calls that overlap on a device (different streams, or threads without ordering) race. */
+#define ISA_EKV_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int isa_ekv_forward_noalloc(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd,
+                            int64_t M, int64_t K, int64_t O, int n_entries, float delta_min, float delta_max,
+                            float v_sat, float out_min, float out_max, float* out, void* stream);
+
 /* Workspace bytes for isa_ekv_backward at this shape and gradient selection. */
 size_t isa_ekv_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x,
                                   int need_grad_w);

@@ -45,6 +45,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include <algorithm>
@@ -153,8 +154,10 @@ void prof_stop(hipStream_t s, ProfiledLaunch* slot) {
 // Times a whole library call (every kernel it enqueues), closing on every return path.
 struct CallTimer {
     hipStream_t stream;
-    ProfiledLaunch* slot;
-    CallTimer(hipStream_t s, int kind) : stream(s) { prof_start(s, kind, &slot); }
+    ProfiledLaunch* slot = nullptr;
+    CallTimer(hipStream_t s, int kind, bool on = true) : stream(s) {
+        if (on) prof_start(s, kind, &slot);
+    }
     ~CallTimer() { prof_stop(stream, slot); }
 };
 
@@ -2664,14 +2667,14 @@ FwdTableCfg fwd_table_cfg(int n_entries, int wpb) {
 int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const float* vth_neg, int64_t M,
                 int64_t K, int64_t O, float v_sat, float out_min, float out_max, float* out, void* workspace,
                 size_t workspace_bytes, hipStream_t s, const isa_ekv_glue* glue = nullptr,
-                float* idiff = nullptr) {
+                float* idiff = nullptr, bool timed = true) {
     if (M == 0 || O == 0) return 0;
     if (!out) return fail(ISA_EKV_EINVAL, "out is null");
     const FwdPlan p = plan_forward_call(cs.exact, cs.n_entries, M, K, O);
     if (!workspace || workspace_bytes < p.bytes)
         return fail(ISA_EKV_EINVAL, "forward workspace too small (%zu < %zu bytes)", workspace_bytes, p.bytes);
     char* ws = static_cast<char*>(workspace);
-    CallTimer call_timer(s, 2);
+    CallTimer call_timer(s, 2, timed);
     PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 2, ws, p.off_xrec, p.off_wsT,
                             p.off_xrec_alt, p.off_wsT_alt, p.off_part, glue);
     const bool stats = glue && (glue->stat_abs_max || glue->stat_total);
@@ -2735,8 +2738,8 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         }
     }
     set_split(p, ws, fa);
-    ProfiledLaunch* prof;
-    prof_start(s, 0, &prof);
+    ProfiledLaunch* prof = nullptr;
+    if (timed) prof_start(s, 0, &prof);
     launch_forward(cs.exact, gtab, p.mr, p.wpb, dim3(p.blocks), lds, s, fa);
     err = hipGetLastError();
     if (err == hipSuccess) err = finish_split(p, fa, !cs.exact, s);
@@ -3138,6 +3141,49 @@ int run_measured_backward(const float* x, const short* ids_a, const short* ids_b
 }  // namespace
 
 // ----------------------------------------------------------------------------------
+// No-allocation forward (isa_ekv_forward_noalloc). Its workspace is `scratch`, a file-scope
+// device array of kScratchBytes that every device the library runs on holds from module load
+// to process end, so a caller that cannot allocate (HIP graph capture, serving loops) still
+// gets the forward. In host code `scratch` names a host-side stand-in, not device memory: the
+// array's address on the current device comes from hipGetSymbolAddress, resolved once per
+// device on the first call there and kept in g_scratch_ptr, and only that pointer is handed to
+// kernels. Every workspace byte the forward reads is written earlier in the same call (token
+// and threshold records, range partials, the table-copy mode word, K-split planes), so nothing
+// needs clearing between calls; calls that overlap on one device share the array and race.
+// ----------------------------------------------------------------------------------
+
+constexpr size_t kScratchBytes = ISA_EKV_NOALLOC_MAX_BYTES;  // 64 MiB per device
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kScratchMaxDevices] = {};
+
+// The current device's address of `scratch` (resolved on the first call on that device).
+int scratch_for_current_device(void** ptr) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+    if (dev < 0 || dev >= kScratchMaxDevices)
+        return fail(ISA_EKV_EINVAL, "device %d is past the %d devices the scratch table covers", dev,
+                    kScratchMaxDevices);
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(ISA_EKV_EINVAL, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------------------------
 // C ABI
 // ----------------------------------------------------------------------------------
 
@@ -3248,6 +3294,29 @@ int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, 
                     n_entries);
     return run_forward(lut_setup(lut_fwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, M, K, O, v_sat,
                        out_min, out_max, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int isa_ekv_forward_noalloc(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd,
+                            int64_t M, int64_t K, int64_t O, int n_entries, float delta_min, float delta_max,
+                            float v_sat, float out_min, float out_max, float* out, void* stream) {
+    const int rc = check_common(x, vth_pos, vth_neg, lut_fwd, M, K, O, n_entries, delta_min, delta_max, v_sat);
+    if (rc) return rc;
+    if (n_entries > kMaxEntriesGlobal)
+        return fail(ISA_EKV_EINVAL, "LUT forward supports LUT_DELTA_SIZE <= %d (got %d)", kMaxEntriesGlobal,
+                    n_entries);
+    if (M == 0 || O == 0) return 0;
+    const size_t need = plan_forward_call(false, n_entries, M, K, O).bytes;
+    if (need > kScratchBytes)
+        return fail(ISA_EKV_EINVAL,
+                    "isa_ekv_forward_noalloc: shape (M=%lld, K=%lld, O=%lld) needs %zu bytes of scratch, more "
+                    "than its %zu-byte maximum; use isa_ekv_forward with a workspace",
+                    (long long)M, (long long)K, (long long)O, need, kScratchBytes);
+    void* ws = nullptr;
+    const int src = scratch_for_current_device(&ws);
+    if (src) return src;
+    return run_forward(lut_setup(lut_fwd, n_entries, delta_min, delta_max), x, vth_pos, vth_neg, M, K, O, v_sat,
+                       out_min, out_max, out, ws, kScratchBytes, static_cast<hipStream_t>(stream), nullptr, nullptr,
+                       false);
 }
 
 size_t isa_ekv_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x,

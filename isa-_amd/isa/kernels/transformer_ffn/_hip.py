@@ -26,6 +26,7 @@ PLAN_FORWARD = 0
 PLAN_BACKWARD = 1
 PLAN_LAYER_BACKWARD = 2
 PLAN_INFO_LEN = 7
+NOALLOC_MAX_BYTES = 64 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
 
 EXPORTS = (
     "isa_ekv_abi_version",
@@ -36,6 +37,7 @@ EXPORTS = (
     "isa_ekv_lut_pack",
     "isa_ekv_forward_workspace",
     "isa_ekv_forward",
+    "isa_ekv_forward_noalloc",
     "isa_ekv_backward_workspace",
     "isa_ekv_backward",
     "isa_ekv_exact_forward_workspace",
@@ -137,6 +139,8 @@ def _declare(lib) -> None:
     lib.isa_ekv_forward_workspace.restype = sz
     lib.isa_ekv_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, f32, f32, vp, vp, sz, vp]
     lib.isa_ekv_forward.restype = ci
+    lib.isa_ekv_forward_noalloc.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, f32, f32, vp, vp]
+    lib.isa_ekv_forward_noalloc.restype = ci
     lib.isa_ekv_backward_workspace.argtypes = [i64, i64, i64, ci, ci, ci]
     lib.isa_ekv_backward_workspace.restype = sz
     lib.isa_ekv_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, ci, f32, f32, f32, vp, vp, vp, vp, sz, vp]

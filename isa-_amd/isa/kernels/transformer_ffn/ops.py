@@ -154,6 +154,32 @@ def lut_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_rec
     return out
 
 
+def lut_forward_noalloc(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_records: torch.Tensor,
+                        n_entries: int, delta_min: float, delta_max: float, v_sat: float, out_min: float,
+                        out_max: float, out: torch.Tensor) -> torch.Tensor:
+    """lut_forward through isa_ekv_forward_noalloc: the library's own fixed scratch instead of
+    a workspace, for callers that cannot allocate (e.g. inside HIP graph capture). The caller
+    passes `out` [M, O] fp32 and fp32 contiguous operands, so this function allocates nothing
+    either; shapes needing more than NOALLOC_MAX_BYTES of scratch raise."""
+    lib = _hip.load()
+    M, K, O = _check_operands(x, wpos, wneg)
+    for t, name in ((x, "x"), (wpos, "wpos"), (wneg, "wneg"), (out, "out")):
+        if t.dtype != torch.float32 or not t.is_contiguous() or (t.numel() and t.data_ptr() % 16):
+            raise RuntimeError(f"{name} must be fp32, contiguous and 16-byte aligned")
+    _require_cuda(out, "out")
+    if tuple(out.shape) != (M, O) or out.device != x.device:
+        raise RuntimeError(f"out must be [{M}, {O}] on {x.device}")
+    if n_entries > MAX_ENTRIES:
+        raise RuntimeError(f"LUT forward supports LUT_DELTA_SIZE <= {MAX_ENTRIES}")
+    dev = x.device
+    with torch.cuda.device(dev):
+        rc = lib.isa_ekv_forward_noalloc(_ptr(x), _ptr(wpos), _ptr(wneg), fwd_records.data_ptr(), M, K, O,
+                                         int(n_entries), float(delta_min), float(delta_max), float(v_sat),
+                                         float(out_min), float(out_max), out.data_ptr(), _hip.stream_handle(dev))
+    _hip.check(rc, "isa_ekv_forward_noalloc")
+    return out
+
+
 def lut_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_out: torch.Tensor,
                  bwd_records: torch.Tensor, n_entries: int, delta_min: float, delta_max: float, v_sat: float,
                  need_grad_x: bool, need_grad_w: bool, workspace: Optional[torch.Tensor] = None):

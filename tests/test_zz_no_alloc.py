@@ -1,0 +1,67 @@
+"""isa_ekv_forward_noalloc (the forward without a workspace argument, for callers that
+cannot allocate) against isa_ekv_forward, through the C ABI: the same kernels on the same
+inputs, so outputs must be bitwise equal. Two calls in a row, the second smaller than the
+first (the scratch array keeps the first call's contents), then a call in the windowed
+two-copy regime of the 8192-entry table, and the size limit."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.helpers import flash_cfg, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _both(x, vp, vn, cfg, dev):
+    from isa.approximations.delta_lut import get_packed_tables, lut_range
+    from isa.kernels.transformer_ffn import ops
+
+    dmin, dmax, n = lut_range(cfg)
+    fwd, _ = get_packed_tables(cfg, dev)
+    xd, pd, nd = (t.to(dev).contiguous() for t in (x, vp, vn))
+    ref = ops.lut_forward(xd, pd, nd, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0)
+    out = torch.full_like(ref, float("nan"))
+    ops.lut_forward_noalloc(xd, pd, nd, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0, out)
+    torch.cuda.synchronize()
+    return ref, out
+
+
+def test_noalloc_forward_matches_workspace_forward(cuda_device):
+    cfg = flash_cfg(4096)
+    for M, K, O in ((300, 203, 500), (37, 64, 130)):  # second call smaller; K % 8 != 0 first
+        print(f"[case] noalloc forward M={M} K={K} O={O}", flush=True)
+        x, vp, vn, _ = make_inputs(M, K, O, seed=M + K + O)
+        ref, out = _both(x, vp, vn, cfg, cuda_device)
+        assert torch.equal(out, ref)
+        assert torch.count_nonzero(ref) > 0
+
+
+def test_noalloc_forward_table_copies(cuda_device):
+    """8192-entry table, mapped inputs, initial thresholds: the windowed two-copy forward, whose
+    mode word and reassigned threshold records live in the scratch array."""
+    cfg = flash_cfg(8192)
+    for M, K, O in ((256, 400, 600), (64, 203, 300)):
+        print(f"[case] noalloc forward 8192 entries M={M} K={K} O={O}", flush=True)
+        x, vp, vn, _ = make_inputs(M, K, O, seed=7 * M + K)
+        ref, out = _both(x, vp, vn, cfg, cuda_device)
+        assert torch.equal(out, ref)
+
+
+def test_noalloc_forward_rejects_oversized_shapes(cuda_device):
+    from isa.approximations.delta_lut import get_packed_tables, lut_range
+    from isa.kernels.transformer_ffn import _hip, ops
+
+    cfg = flash_cfg(4096)
+    M, K, O = 8192, 768, 3072  # headline fc1: ~69 MB of workspace
+    assert ops.plan_info("forward", M, K, O, 4096)["workspace_bytes"] > _hip.NOALLOC_MAX_BYTES
+    dmin, dmax, n = lut_range(cfg)
+    fwd, _ = get_packed_tables(cfg, cuda_device)
+    x = torch.zeros(M, K, device=cuda_device)
+    w = torch.zeros(O, K, device=cuda_device)
+    out = torch.full((M, O), 7.0, device=cuda_device)
+    with pytest.raises(RuntimeError, match="maximum"):
+        ops.lut_forward_noalloc(x, w, w, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0, out)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())  # nothing was enqueued (a forward would have written zeros)
