@@ -235,23 +235,26 @@ def measured_fc1_step(args) -> int:
     return 0
 
 
-def gpt_train_step(args) -> int:
-    """one GPT training step (12 layers, d=768, 12 heads, Physical FFN 3072 on the
-    HIP kernels, causal SDPA attention, vocab 50304 tied embeddings, 8 x 1024 tokens, AdamW,
-    then the thresholds are clamped to [V_TH_MIN, V_TH_MAX] as the reference's language
-    trainer does). Reports tokens/s and the share of step time spent in the CIM library calls."""
+GPT_SHAPE = dict(n_layer=12, n_head=12, d=768, d_ffn=3072, vocab=50304, B=8, T=1024)
+
+
+def make_gpt_train(lut_size: int, dev, seed: int = 0):
+    """configs[4]'s model and step: a GPT (12 layers, d=768, 12 heads, Physical FFN 3072 on the
+    HIP kernels, causal SDPA attention, vocab 50304 tied embeddings) on 8 x 1024 uniform random
+    token ids, AdamW, then the thresholds clamped to [V_TH_MIN, V_TH_MAX] as the reference's
+    language trainer does. Returns (model, optimizer, step); step() runs one training step and
+    returns the loss tensor."""
     import torch
     import torch.nn as nn
     import torch.nn.functional as F
 
     from isa.device_models.config import make_flash_transistor_ekv_config
-    from isa.kernels.transformer_ffn import _hip
     from isa.operators.cim import PhysicalFFN
 
-    dev = torch.device("cuda", 0)
-    n_layer, n_head, d, d_ffn, vocab, B, T = 12, 12, 768, 3072, 50304, 8, 1024
-    cfg = make_flash_transistor_ekv_config(default_lut_size=args.lut_size)
-    cfg["LUT_DELTA_SIZE"] = args.lut_size
+    n_layer, n_head, d, d_ffn, vocab, B, T = (GPT_SHAPE[k] for k in ("n_layer", "n_head", "d", "d_ffn", "vocab",
+                                                                     "B", "T"))
+    cfg = make_flash_transistor_ekv_config(default_lut_size=lut_size)
+    cfg["LUT_DELTA_SIZE"] = lut_size
 
     class Block(nn.Module):
         def __init__(self):
@@ -286,7 +289,7 @@ def gpt_train_step(args) -> int:
                 x = blk(x)
             return self.head(self.ln_f(x))
 
-    torch.manual_seed(0)
+    torch.manual_seed(seed)
     model = GPT().to(dev)
     opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.0)
     ids = torch.randint(0, vocab, (B, T + 1), device=dev)
@@ -302,6 +305,20 @@ def gpt_train_step(args) -> int:
         for f in ffns:
             f.clamp_vth()
         return loss
+
+    return model, opt, step
+
+
+def gpt_train_step(args) -> int:
+    """GPT training steps on make_gpt_train's model. Reports tokens/s and the share
+    of step time spent in the CIM library calls."""
+    import torch
+
+    from isa.kernels.transformer_ffn import _hip
+
+    dev = torch.device("cuda", 0)
+    n_layer, d, d_ffn, vocab, B, T = (GPT_SHAPE[k] for k in ("n_layer", "d", "d_ffn", "vocab", "B", "T"))
+    model, opt, step = make_gpt_train(args.lut_size, dev)
 
     for _ in range(args.warmup):
         step()
