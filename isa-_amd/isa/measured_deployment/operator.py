@@ -52,6 +52,42 @@ class _MeasuredFn(torch.autograd.Function):
         return gx, None, None, None, None, None, None, None
 
 
+# Shared codebooks (install_fused_backend): key -> the tensors of _codebook_tables, which also
+# hold the source tensors so that their ids cannot be reused while an entry is alive.
+_SHARED_CODEBOOKS: dict[tuple, dict[str, object]] = {}
+
+
+def _codebook_tables(vg: torch.Tensor, currents_a: torch.Tensor, device: torch.device, bins: int,
+                     v_min: float, v_max: float) -> dict[str, object]:
+    """The validated codebook on `device` and its compact coefficient tables: per-segment line
+    slopes and intercepts of every measured curve ([states, segments]: I = S v + C on segment
+    s), and the tables the kernel reads: those lines, or in vin_lut_bins mode every state's
+    current at each bin centre as a zero-slope table ([states, bins])."""
+    mvg = vg.detach().to(device=device, dtype=torch.float32).contiguous()
+    cur = currents_a.detach().to(device=device, dtype=torch.float32).contiguous()
+    if mvg.ndim != 1 or cur.ndim != 2 or cur.shape[1] != mvg.numel():
+        raise ValueError("Measured codebook tensors have inconsistent shapes")
+    if mvg.numel() < 2 or not bool(torch.all(mvg[1:] > mvg[:-1])):
+        raise ValueError("Measured Vg grid must be strictly increasing")
+    lookup = (max(float(mvg[0].item()), v_min), min(float(mvg[-1].item()), v_max))
+    step = mvg[1:] - mvg[:-1]
+    seg_s = ((cur[:, 1:] - cur[:, :-1]) / step.unsqueeze(0)).contiguous()
+    seg_c = (cur[:, :-1] - seg_s * mvg[:-1].unsqueeze(0)).contiguous()
+    book = {"source": (vg, currents_a), "vg": mvg, "currents": cur, "lookup": lookup,
+            "segment_slopes": seg_s, "segment_intercepts": seg_c}
+    if bins > 0:
+        centers = torch.linspace(lookup[0], lookup[1], bins, device=device, dtype=torch.float32)
+        seg = (torch.searchsorted(mvg, centers, right=True) - 1).clamp(0, mvg.numel() - 2)
+        at_centers = (seg_s[:, seg] * centers.unsqueeze(0) + seg_c[:, seg]).contiguous()
+        book.update(table_slopes=torch.zeros_like(at_centers), table_intercepts=at_centers,
+                    active_segments=torch.empty(0, dtype=torch.long, device=device), bin_centers=centers)
+    else:
+        active = torch.nonzero((mvg[:-1] <= lookup[1]) & (mvg[1:] >= lookup[0]), as_tuple=False).flatten()
+        book.update(table_slopes=seg_s, table_intercepts=seg_c, active_segments=active,
+                    bin_centers=torch.empty(0, device=device))
+    return book
+
+
 class DeploymentAwareCIMLinear(CIMLinear):
     """CIMLinear whose forward can be continuous, measured, or measured+STE (operator.py:21-233)."""
 
@@ -75,6 +111,9 @@ class DeploymentAwareCIMLinear(CIMLinear):
         # compact codebook tables of the kernel: [curves, segments] slope/intercept
         self.register_buffer("curve_slopes", torch.empty(0), persistent=False)
         self.register_buffer("curve_intercepts", torch.empty(0), persistent=False)
+        # segment lines of the measured curves ([curves, segments]), for currents_at
+        self.register_buffer("_segment_slopes", torch.empty(0), persistent=False)
+        self.register_buffer("_segment_intercepts", torch.empty(0), persistent=False)
 
     @classmethod
     def from_cimlinear(cls, original: CIMLinear) -> "DeploymentAwareCIMLinear":
@@ -90,76 +129,65 @@ class DeploymentAwareCIMLinear(CIMLinear):
 
     @torch.no_grad()
     def configure_codebook(self, vg: torch.Tensor, currents_a: torch.Tensor, vin_lut_bins: int = 0) -> None:
-        """operator.py:56-75."""
-        device = self.vth_pos.device
-        vg = vg.detach().to(device=device, dtype=torch.float32).contiguous()
-        currents = currents_a.detach().to(device=device, dtype=torch.float32).contiguous()
-        if vg.ndim != 1 or currents.ndim != 2 or currents.shape[1] != vg.numel():
-            raise ValueError("Measured codebook tensors have inconsistent shapes")
-        if vg.numel() < 2 or not bool(torch.all(vg[1:] > vg[:-1])):
-            raise ValueError("Measured Vg grid must be strictly increasing")
-        self.measured_vg = vg
-        self.measured_currents = currents
-        self.lookup_min = max(float(vg[0].item()), float(self.cfg.get("V_min", 0.0)))
-        self.lookup_max = min(float(vg[-1].item()), float(self.cfg.get("V_max", 4.0)))
-        self.vin_lut_bins = int(vin_lut_bins)
-        if self.vin_lut_bins < 0:
+        """operator.py:56-75: validate and hold the codebook, plus the compact coefficient tables
+        the kernel reads (they depend on the codebook only, not on the assignment). With
+        install_fused_backend() in effect, layers configured from the same source tensors on
+        one device share one copy of all of them (fused_backend.py:37-131)."""
+        if int(vin_lut_bins) < 0:
             raise ValueError("vin_lut_bins must be non-negative")
+        device = self.vth_pos.device
+        shared = bool(getattr(type(self), "_fg50_fused_backend_installed", False))
+        key = (device.type, device.index, id(vg), id(currents_a), tuple(vg.shape), tuple(currents_a.shape),
+               int(vin_lut_bins), float(self.cfg.get("V_min", 0.0)), float(self.cfg.get("V_max", 4.0)))
+        book = _SHARED_CODEBOOKS.get(key) if shared else None
+        if book is None:
+            book = _codebook_tables(vg, currents_a, device, int(vin_lut_bins), float(self.cfg.get("V_min", 0.0)),
+                                    float(self.cfg.get("V_max", 4.0)))
+            if shared:
+                _SHARED_CODEBOOKS[key] = book
+        self.measured_vg = book["vg"]
+        self.measured_currents = book["currents"]
+        self.lookup_min, self.lookup_max = book["lookup"]
+        self.vin_lut_bins = int(vin_lut_bins)
+        self._segment_slopes = book["segment_slopes"]
+        self._segment_intercepts = book["segment_intercepts"]
+        self.curve_slopes = book["table_slopes"]
+        self.curve_intercepts = book["table_intercepts"]
+        self.active_segments = book["active_segments"]
+        self.bin_centers = book["bin_centers"]
 
     @torch.no_grad()
     def set_assignment(self, pos_idx: torch.Tensor, neg_idx: torch.Tensor) -> None:
-        """operator.py:77-146: validation and the per-mode coefficient tables. The kernel
-        reads the compact [curves, segments] tables instead of the expanded per-cell ones."""
+        """operator.py:77-146: the assignment's validation, with the reference's messages. The
+        kernel reads the compact per-state tables configure_codebook holds instead of the
+        expanded per-cell ones."""
         if self.measured_vg.numel() == 0:
             raise RuntimeError("configure_codebook must be called before set_assignment")
         expected = (self.out_features, self.in_features)
         if tuple(pos_idx.shape) != expected or tuple(neg_idx.shape) != expected:
             raise ValueError(f"Assignment shape must be {expected}")
         device = self.vth_pos.device
-        self.pos_idx = pos_idx.to(device=device, dtype=torch.int16).contiguous()
-        self.neg_idx = neg_idx.to(device=device, dtype=torch.int16).contiguous()
-        pos = self.pos_idx.long()
-        neg = self.neg_idx.long()
-        if int(pos.min()) < 0 or int(neg.min()) < 0:
+        pos = pos_idx.to(device=device, dtype=torch.int16).contiguous()
+        neg = neg_idx.to(device=device, dtype=torch.int16).contiguous()
+        if int(torch.minimum(pos.min(), neg.min())) < 0:
             raise ValueError("Assignment contains negative state indices")
         state_count = int(self.measured_currents.shape[0])
-        if int(pos.max()) >= state_count or int(neg.max()) >= state_count:
+        if int(torch.maximum(pos.max(), neg.max())) >= state_count:
             raise ValueError("Assignment references a state outside the codebook")
-
-        if self.vin_lut_bins > 0:
-            centers = torch.linspace(self.lookup_min, self.lookup_max, self.vin_lut_bins, device=device,
-                                     dtype=torch.float32)
-            # currents of every state at every bin centre: [states, bins], zero slopes
-            at_centers = torch.stack([self.currents_at(center) for center in centers], dim=1)
-            self.bin_centers = centers
-            self.curve_slopes = torch.zeros_like(at_centers)
-            self.curve_intercepts = at_centers.contiguous()
-            self.active_segments = torch.empty(0, dtype=torch.long, device=device)
-            return
-
-        vg = self.measured_vg
-        currents = self.measured_currents
-        dv = vg[1:] - vg[:-1]
-        slopes = (currents[:, 1:] - currents[:, :-1]) / dv.unsqueeze(0)
-        intercepts = currents[:, :-1] - slopes * vg[:-1].unsqueeze(0)
-        self.active_segments = torch.nonzero(
-            (vg[:-1] <= self.lookup_max) & (vg[1:] >= self.lookup_min), as_tuple=False
-        ).flatten()
-        self.curve_slopes = slopes.contiguous()
-        self.curve_intercepts = intercepts.contiguous()
-        self.bin_centers = torch.empty(0, device=device)
+        self.pos_idx, self.neg_idx = pos, neg
 
     def currents_at(self, voltage: torch.Tensor | float) -> torch.Tensor:
-        """operator.py:148-162: every state's current at `voltage` (linear interpolation)."""
+        """Every state's current at `voltage` (operator.py:148-162): [states] for a scalar,
+        [states, *voltage.shape] for a tensor. Evaluated as the kernel's cells evaluate the
+        curves, S[state, seg] * v + C[state, seg] on the segment seg holding v (clamped to
+        the measured grid)."""
         if self.measured_vg.numel() == 0:
             raise RuntimeError("Measured codebook has not been configured")
-        value = torch.as_tensor(voltage, device=self.measured_vg.device, dtype=torch.float32).clamp(
-            self.measured_vg[0], self.measured_vg[-1])
-        upper = torch.searchsorted(self.measured_vg, value, right=True).clamp(1, self.measured_vg.numel() - 1)
-        lower = upper - 1
-        alpha = (value - self.measured_vg[lower]) / (self.measured_vg[upper] - self.measured_vg[lower])
-        return self.measured_currents[:, lower] + alpha * (
-            self.measured_currents[:, upper] - self.measured_currents[:, lower])
+        vg = self.measured_vg
+        v = torch.as_tensor(voltage, device=vg.device, dtype=torch.float32).clamp(vg[0], vg[-1])
+        seg = (torch.searchsorted(vg, v.reshape(-1), right=True) - 1).clamp(0, vg.numel() - 2)
+        out = self._segment_slopes[:, seg] * v.reshape(1, -1) + self._segment_intercepts[:, seg]
+        return out.reshape(self._segment_slopes.shape[0], *v.shape)
 
     def measured_forward(self, x: torch.Tensor) -> torch.Tensor:
         """operator.py:164-224 on the HIP kernel: fp32 even under autocast, output
