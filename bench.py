@@ -20,6 +20,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import subprocess
 import sys
 import time
@@ -69,8 +70,11 @@ def cpu_info() -> str:
         return platform.processor() or "unknown"
 
 
-def cpu_baseline(d_model: int, d_ffn: int, target_s: float) -> dict:
-    """Reference CPU path (exact formula, cim.py:201-214 + flash_transistor.py:95-131) on fc1."""
+def cpu_baseline(layers, target_s: float) -> dict:
+    """The reference's PyTorch CPU path (exact formula, cim.py:201-214 + flash_transistor.py:95-131),
+    restated in oracle/exact.py, fwd+bwd on a token sample of every CIM layer of the workload
+    (K -> O pairs; about target_s / len(layers) seconds each). fc1 takes mapped inputs
+    clamp(N(0,1), 0, 4), a later layer signed TIA outputs clamp(N(0,1), -4, 4)."""
     import torch
 
     from oracle import exact, oracle
@@ -80,32 +84,39 @@ def cpu_baseline(d_model: int, d_ffn: int, target_s: float) -> dict:
     cfg = dict(oracle.FLASH_PARAMS)
     g = torch.Generator().manual_seed(0)
     lo, hi = 2.5 - 0.5 * 2 * cfg["n"] * cfg["U_T"], 2.5 + 0.5 * 2 * cfg["n"] * cfg["U_T"]
-    vp = torch.empty(d_ffn, d_model).uniform_(lo, hi, generator=g).requires_grad_(True)
-    vn = torch.empty(d_ffn, d_model).uniform_(lo, hi, generator=g).requires_grad_(True)
+    total_cells, total_s, parts = 0.0, 0.0, []
+    for idx, (k_in, o_out) in enumerate(layers):
+        vp = torch.empty(o_out, k_in).uniform_(lo, hi, generator=g).requires_grad_(True)
+        vn = torch.empty(o_out, k_in).uniform_(lo, hi, generator=g).requires_grad_(True)
+        x_lo = 0.0 if idx == 0 else -4.0
 
-    def run(tokens: int) -> float:
-        x = torch.randn(1, tokens, d_model, generator=g).clamp(0.0, 4.0).requires_grad_(True)
-        gr = torch.randn(1, tokens, d_ffn, generator=g)
-        t0 = time.perf_counter()
-        out = exact.cim_idiff_cpu(x, vp, vn, cfg)
-        out.backward(gr)
-        return time.perf_counter() - t0
+        def run(tokens: int) -> float:
+            x = torch.randn(1, tokens, k_in, generator=g).clamp(x_lo, 4.0).requires_grad_(True)
+            gr = torch.randn(1, tokens, o_out, generator=g)
+            t0 = time.perf_counter()
+            out = exact.cim_idiff_cpu(x, vp, vn, cfg)
+            out.backward(gr)
+            return time.perf_counter() - t0
 
-    run(2)  # warm-up
-    tokens = 4
-    dt = run(tokens)
-    # scale the sample to roughly target_s of CPU work
-    want = max(4, min(4096, int(tokens * target_s / max(dt, 1e-3))))
-    dt = run(want)
-    cells = 2.0 * want * d_model * d_ffn
+        run(2)  # warm-up
+        dt = run(4)
+        # scale the sample to this layer's share of the CPU time budget
+        want = max(4, min(4096, int(4 * target_s / len(layers) / max(dt, 1e-3))))
+        dt = run(want)
+        cells = 2.0 * want * k_in * o_out
+        total_cells += cells
+        total_s += dt
+        parts.append(f"{k_in}->{o_out} on {want} tokens ({cells:.3e} cell-evals, {dt:.1f} s, "
+                     f"{cells / dt:.3e}/s)")
     return {
-        "value": cells / dt,
+        "value": total_cells / total_s,
         "unit": "cell-evals/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"reference CPU path (exact EKV formula, chunked over 64 outputs, analytic backward) "
-                  f"restated in oracle/exact.py: fc1 {d_model}->{d_ffn} fwd+bwd on {want} tokens "
-                  f"({cells:.3e} cell-evals, {dt:.1f} s); host {cpu_info()}, os.cpu_count()={os.cpu_count()}",
+        "sample": "reference CPU path (exact EKV formula, chunked over 64 outputs, analytic backward) restated "
+                  "in oracle/exact.py, fwd+bwd, every CIM layer on a token sample: " + "; ".join(parts)
+                  + f"; total {total_cells:.3e} cell-evals in {total_s:.1f} s; host {cpu_info()}, "
+                  f"os.cpu_count()={os.cpu_count()}",
     }
 
 
@@ -145,16 +156,17 @@ def cpu_lut_oracle(d_model: int, d_ffn: int, target_s: float) -> dict:
 
 
 def measured_traffic(config: str):
-    """HBM bytes per backward main-kernel launch from the committed rocprofv3 counter summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel), or None if absent."""
+    """(HBM bytes per backward main-kernel launch, source) from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel), or (None, None): the
+    counters need a rocprofv3 --pmc run of their own, so this run does not measure them."""
     path = ROOT / "profiles" / f"bwd_kernel_{config}_hbm_traffic.txt"
     try:
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch:"):
-                return float(line.split(":", 1)[1])
+                return float(line.split(":", 1)[1]), f"profiles/{path.name} (rocprofv3 --pmc, not this run)"
     except OSError:
         pass
-    return None
+    return None, None
 
 
 def measured_fc1_step(args) -> int:
@@ -372,11 +384,15 @@ def lds_roofline(model, cfg: dict, cells_launch: float, fwd_ms: float, bwd_ms: f
         if name.endswith("vth_pos") or name.endswith("vth_neg"):
             spans.append(float(p.detach().max() - p.detach().min()))
     window = max(1, min(8192, int(math.ceil(max(spans) / step)) + 1))
-    ns = ops.probe_lds_gather(window, 8, device=dev)
+    clock = {}
+    ns = ops.probe_lds_gather(window, 8, device=dev, clock=clock)
+    ns_free = ops.probe_lds_gather(32, 8, device=dev)  # one record per bank pair: no conflicts
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     waves_per_launch = cells_launch / 64.0
     fwd_roof = 2 * waves_per_launch * ns / cus * 1e-6  # ms
     bwd_roof = 4 * waves_per_launch * ns / cus * 1e-6
+    fwd_free = 2 * waves_per_launch * ns_free / cus * 1e-6
+    bwd_free = 4 * waves_per_launch * ns_free / cus * 1e-6
     return {
         "bound": "lds",
         "window_records": window,
@@ -385,7 +401,12 @@ def lds_roofline(model, cfg: dict, cells_launch: float, fwd_ms: float, bwd_ms: f
         "forward_frac": round(fwd_roof / fwd_ms, 4) if fwd_ms else None,
         "backward_roof_ms": round(bwd_roof, 4),
         "backward_frac": round(bwd_roof / bwd_ms, 4) if bwd_ms else None,
-        "work": "forward 2, backward 4 random ds_read_b64 gathers per cell-eval (wave-level: per 64 cells)",
+        "conflict_free_ns_per_gather_per_cu": round(ns_free, 4),
+        "conflict_free_frac": {"forward": round(fwd_free / fwd_ms, 4) if fwd_ms else None,
+                               "backward": round(bwd_free / bwd_ms, 4) if bwd_ms else None},
+        "work": "forward 2, backward 4 random ds_read_b64 gathers per cell-eval (wave-level: per 64 cells); "
+                "conflict_free_frac prices them at the probe's W = 32 rate (one record per bank pair)",
+        "_clock": clock,
     }
 
 
@@ -396,7 +417,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="gptl_ffn", choices=sorted(CONFIGS) + ["gptl_train", "measured_fc1"])
     ap.add_argument("--lut-size", type=int, default=4096)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ekv-approx", default="lut", choices=["lut", "exact"],
                     help="CIMLinear projection: the LUT kernels (headline) or the exact-formula kernels")
@@ -496,14 +517,22 @@ def main() -> int:
         torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
+    step_ms = []
+
     def timed(run):
+        """Mean ms per step over the timed region (the whole-job rate), wall seconds; the
+        per-step durations from HIP events between steps go to step_ms (for the median)."""
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         e0.record()
-        for _ in range(args.steps):
+        for i in range(args.steps):
+            marks[i].record()
             run()
+        marks[-1].record()
         e1.record()
         torch.cuda.synchronize()
+        step_ms[:] = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
         return e0.elapsed_time(e1) / args.steps, time.perf_counter() - t0
 
     if graph is None:
@@ -515,7 +544,9 @@ def main() -> int:
             eager_ms, _ = timed(step)
         log(f"[bench] {args.config}: eager step {eager_ms:.3f} ms (host launches included)")
     value = cells_step / (ms * 1e-3)
-    log(f"[bench] {args.config}: {ms:.3f} ms/step{' (graph replay)' if graph is not None else ''} "
+    median_ms = statistics.median(step_ms) if step_ms else ms
+    log(f"[bench] {args.config}: {ms:.3f} ms/step mean, {median_ms:.3f} median"
+        f"{' (graph replay)' if graph is not None else ''} "
         f"(wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
 
     if args.copy_calibration_mib > 0:
@@ -541,7 +572,8 @@ def main() -> int:
         "peak": round(peak, 3),
         "unit": "TOP/s",
         "frac": round(achieved / peak, 4),
-        "traffic": None if exact else measured_traffic(args.config),
+        "traffic": None if exact else measured_traffic(args.config)[0],
+        "traffic_source": None if exact else measured_traffic(args.config)[1],
         "kernel": ("bwd_exact_kernel<true,true>" if exact else "bwd_kernel<true,true,true,true>")
                   + " (backward main kernel, dominant)",
         "work": f"{bwd_instr} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
@@ -559,15 +591,28 @@ def main() -> int:
         f"bwd kernel {bwd_avg:.3f} ms/launch ({roofline['frac']:.3f})")
     if not exact:
         roofline["lds"] = lds_roofline(model, cfg, cells_launch, fwd_avg, bwd_avg, dev)
+        clock = roofline["lds"].pop("_clock")
         log(f"[bench] LDS gather roofline (window {roofline['lds']['window_records']} records, "
             f"{roofline['lds']['ns_per_gather_per_cu']:.3f} ns per gather per CU): fwd "
-            f"{roofline['lds']['forward_frac']:.3f}, bwd {roofline['lds']['backward_frac']:.3f}")
+            f"{roofline['lds']['forward_frac']:.3f}, bwd {roofline['lds']['backward_frac']:.3f}; "
+            f"conflict-free {roofline['lds']['conflict_free_frac']}")
+        if clock.get("ghz"):
+            # the same kernels priced at the shader clock the CUs sustained under a gather load
+            ghz = clock["ghz"]
+            roofline["sustained_clock"] = {
+                "ghz": round(ghz, 4),
+                "frac": round(roofline["frac"] * 2.4 / ghz, 4),
+                "forward_frac": round(roofline["forward_kernel"]["frac"] * 2.4 / ghz, 4),
+                "source": "clock64 cycles / wall_clock64 time of each CU's first wave in the LDS gather probe "
+                          "launched right after the timed steps (median over blocks)",
+            }
+            log(f"[bench] sustained shader clock {ghz:.3f} GHz: bwd frac {roofline['sustained_clock']['frac']:.3f}")
 
     cpu = None
     lut_cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline ...")
-        cpu = cpu_baseline(D, F, args.cpu_seconds)
+        cpu = cpu_baseline([(k, o) for _, k, o in layers], args.cpu_seconds)
         log(f"[bench] cpu {cpu['value']:.4e} cell-evals/s on {cpu['cores']} threads")
         lut_cpu = cpu_lut_oracle(D, F, 4.0)
         log(f"[bench] cpu LUT oracle {lut_cpu['value']:.4e} cell-evals/s on {lut_cpu['cores']} threads")
@@ -580,6 +625,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "ms_per_step_median": median_ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

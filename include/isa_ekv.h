@@ -289,9 +289,13 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  * of the table kernels' gathers when a wave's thresholds span window_records table entries.
  * The caller times the launch on `stream` (asynchronous) to get the LDS gather rate that
  * bounds those kernels. out: device buffer of >= (2 x CU count x 1024) floats (scratch results).
- * *gathers_per_cu (nullable) receives the wave-level gathers each CU issues. */
+ * *gathers_per_cu (nullable) receives the wave-level gathers each CU issues. clocks (nullable,
+ * device, 2 x blocks int64) receives, per block, the shader-clock cycles (clock64) and the
+ * constant-rate wall-clock ticks (wall_clock64) of its first wave's gather loop, and
+ * *wall_clock_khz (nullable, host) the wall clock's rate: cycles / ticks x rate is the shader
+ * clock the CUs sustained while gathering. */
 int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iterations, float* out, int64_t out_floats,
-                             int* gathers_per_cu, void* stream);
+                             int* gathers_per_cu, int64_t* clocks, int* wall_clock_khz, void* stream);
 
 #ifdef __cplusplus
 }

@@ -2022,11 +2022,15 @@ constexpr int kProbeLdsBytes = 65536;
 constexpr int kProbeBlocksPerCU = 2;  // 32 waves per CU, as the table kernels run
 
 template <int REC>
-__global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int iters, unsigned seed, float* out) {
+__global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int iters, unsigned seed, float* out,
+                                                                 long long* clocks) {
     extern __shared__ float4 probe_table[];
     for (int i = threadIdx.x; i < kProbeLdsBytes / 16; i += blockDim.x)
         probe_table[i] = make_float4(i, 0.5f * i, 0.25f * i, 1.0f);
     __syncthreads();
+    // shader-clock cycles (clock64) and constant-rate wall-clock ticks (wall_clock64) over this
+    // wave's gather loop: their ratio is the sustained shader clock while the CU gathers
+    const long long c0 = clocks ? clock64() : 0, w0 = clocks ? wall_clock64() : 0;
     unsigned h = (threadIdx.x + 1) * 2654435761u ^ seed ^ blockIdx.x * 40503u;
     unsigned addr[8];
 #pragma unroll
@@ -2079,6 +2083,11 @@ __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int 
         }
     }
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+    if (clocks && threadIdx.x == 0) {
+        const long long c1 = clock64(), w1 = wall_clock64();
+        clocks[2 * blockIdx.x] = c1 - c0;
+        clocks[2 * blockIdx.x + 1] = w1 - w0;
+    }
 }
 
 // ----------------------------------------------------------------------------------
@@ -3495,7 +3504,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
 }
 
 int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iterations, float* out, int64_t out_floats,
-                             int* gathers_per_cu, void* stream) {
+                             int* gathers_per_cu, int64_t* clocks, int* wall_clock_khz, void* stream) {
     if (record_bytes != 8 && record_bytes != 16)
         return fail(ISA_EKV_EINVAL, "record_bytes must be 8 or 16 (got %d)", record_bytes);
     if (window_records < 1 || window_records > kProbeLdsBytes / record_bytes)
@@ -3512,12 +3521,17 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
         return fail(ISA_EKV_EINVAL, "out needs %lld floats (one per thread of %d blocks)", (long long)blocks * 1024,
                     blocks);
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (wall_clock_khz) {
+        err = hipDeviceGetAttribute(wall_clock_khz, hipDeviceAttributeWallClockRate, dev);
+        if (err != hipSuccess) return hip_fail(err, "wall clock rate query");
+    }
+    long long* clk = reinterpret_cast<long long*>(clocks);
     if (record_bytes == 8)
         hipLaunchKernelGGL(lds_gather_probe_kernel<8>, dim3(blocks), dim3(1024), kProbeLdsBytes, s, window_records,
-                           iterations, 12345u, out);
+                           iterations, 12345u, out, clk);
     else
         hipLaunchKernelGGL(lds_gather_probe_kernel<16>, dim3(blocks), dim3(1024), kProbeLdsBytes, s, window_records,
-                           iterations, 12345u, out);
+                           iterations, 12345u, out, clk);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "lds probe launch");
     if (gathers_per_cu) *gathers_per_cu = kProbeBlocksPerCU * 16 * 8 * iterations;

@@ -178,7 +178,7 @@ def _declare(lib) -> None:
     lib.isa_ekv_profile_begin.restype = ci
     lib.isa_ekv_profile_end.argtypes = [ctypes.POINTER(f64), ctypes.POINTER(ci)]
     lib.isa_ekv_profile_end.restype = ci
-    lib.isa_ekv_probe_lds_gather.argtypes = [ci, ci, ci, vp, i64, ctypes.POINTER(ci), vp]
+    lib.isa_ekv_probe_lds_gather.argtypes = [ci, ci, ci, vp, i64, ctypes.POINTER(ci), vp, ctypes.POINTER(ci), vp]
     lib.isa_ekv_probe_lds_gather.restype = ci
     lib.isa_ekv_plan_info.argtypes = [ci, i64, i64, i64, ci, ci, ci, ctypes.POINTER(i64), ci]
     lib.isa_ekv_plan_info.restype = ci

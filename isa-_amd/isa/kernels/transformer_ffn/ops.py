@@ -491,30 +491,41 @@ def measured_backward(x: torch.Tensor, ids_a: torch.Tensor, ids_b: Optional[torc
 
 
 def probe_lds_gather(window_records: int, record_bytes: int = 8, iterations: int = 2048,
-                     device: Optional[torch.device] = None, repeats: int = 5) -> float:
+                     device: Optional[torch.device] = None, repeats: int = 5, clock: Optional[dict] = None) -> float:
     """Average nanoseconds per wave-level LDS gather per CU for random `record_bytes`
     gathers whose 64 lanes draw indices uniformly from `window_records` entries (one
     `isa_ekv_probe_lds_gather` launch per repeat, after one untimed launch, timed with HIP
-    events on the current stream). A measurement aid for the table kernels' LDS bound."""
+    events on the current stream). A measurement aid for the table kernels' LDS bound.
+    clock: a dict that receives the shader clock the CUs sustained during the timed launches
+    ("ghz": median over blocks and launches of clock64 cycles / wall_clock64 time)."""
     lib = _hip.load()
     dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     out = torch.empty(2 * cus * 1024, dtype=torch.float32, device=dev)
+    clocks = torch.zeros((repeats, 2 * cus, 2), dtype=torch.int64, device=dev)
     per_cu = ctypes.c_int(0)
+    khz = ctypes.c_int(0)
     with torch.cuda.device(dev):
         stream = _hip.stream_handle(dev)
 
-        def launch():
+        def launch(slot):
+            ptr = None if slot is None else clocks[slot].data_ptr()
             rc = lib.isa_ekv_probe_lds_gather(int(window_records), int(record_bytes), int(iterations),
-                                              out.data_ptr(), out.numel(), ctypes.byref(per_cu), stream)
+                                              out.data_ptr(), out.numel(), ctypes.byref(per_cu), ptr,
+                                              ctypes.byref(khz), stream)
             _hip.check(rc, "isa_ekv_probe_lds_gather")
 
-        launch()
+        launch(None)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(repeats):
-            launch()
+        for r in range(repeats):
+            launch(r if clock is not None else None)
         e1.record()
         torch.cuda.synchronize(dev)
     ms = e0.elapsed_time(e1) / repeats
+    if clock is not None and khz.value > 0:
+        c = clocks.reshape(-1, 2).double()
+        ghz = c[:, 0] / (c[:, 1] / (khz.value * 1e3)) / 1e9
+        clock["ghz"] = float(ghz.median())
+        clock["wall_clock_khz"] = khz.value
     return ms * 1e6 / per_cu.value

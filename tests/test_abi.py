@@ -63,10 +63,10 @@ def _err(lib) -> str:
 def test_lds_probe_rejects_bad_arguments_before_launch():
     lib = _hip.load()
     fake = ctypes.c_void_p(16)
-    assert lib.isa_ekv_probe_lds_gather(64, 12, 1, fake, 1 << 20, None, None) == -1 and "record_bytes" in _err(lib)
-    assert lib.isa_ekv_probe_lds_gather(0, 8, 1, fake, 1 << 20, None, None) == -1 and "window_records" in _err(lib)
-    assert lib.isa_ekv_probe_lds_gather(4097, 16, 1, fake, 1 << 20, None, None) == -1 and "[1, 4096]" in _err(lib)
-    assert lib.isa_ekv_probe_lds_gather(64, 8, 0, fake, 1 << 20, None, None) == -1 and "iterations" in _err(lib)
+    assert lib.isa_ekv_probe_lds_gather(64, 12, 1, fake, 1 << 20, None, None, None, None) == -1 and "record_bytes" in _err(lib)
+    assert lib.isa_ekv_probe_lds_gather(0, 8, 1, fake, 1 << 20, None, None, None, None) == -1 and "window_records" in _err(lib)
+    assert lib.isa_ekv_probe_lds_gather(4097, 16, 1, fake, 1 << 20, None, None, None, None) == -1 and "[1, 4096]" in _err(lib)
+    assert lib.isa_ekv_probe_lds_gather(64, 8, 0, fake, 1 << 20, None, None, None, None) == -1 and "iterations" in _err(lib)
 
 
 def test_forward_rejects_bad_arguments_before_launch():

@@ -43,3 +43,8 @@ def test_bench_json_line(cuda_device, capsys, monkeypatch):
     assert 0 < roof["frac"] < 2 and roof["achieved"] > 0
     lds = roof["lds"]
     assert lds["window_records"] >= 1 and lds["ns_per_gather_per_cu"] > 0
+    assert 0 < lds["conflict_free_ns_per_gather_per_cu"] <= 1.05 * lds["ns_per_gather_per_cu"]
+    assert lds["conflict_free_frac"]["forward"] > 0 and lds["conflict_free_frac"]["backward"] > 0
+    assert rec["ms_per_step_median"] > 0
+    clock = roof["sustained_clock"]
+    assert 0.5 < clock["ghz"] < 3.5, clock  # the shader clock, in GHz
