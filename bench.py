@@ -99,9 +99,9 @@ def cpu_baseline(layers, target_s: float) -> dict:
             return time.perf_counter() - t0
 
         run(2)  # warm-up
-        dt = run(4)
+        dt = run(32)  # the per-token cost grows with the chunk temporaries: size from 32 tokens
         # scale the sample to this layer's share of the CPU time budget
-        want = max(4, min(4096, int(4 * target_s / len(layers) / max(dt, 1e-3))))
+        want = max(8, min(4096, int(32 * target_s / len(layers) / max(dt, 1e-3))))
         dt = run(want)
         cells = 2.0 * want * k_in * o_out
         total_cells += cells
