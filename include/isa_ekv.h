@@ -117,8 +117,10 @@ size_t isa_ekv_backward_workspace(int64_t M, int64_t K, int64_t O, int n_entries
  * binding.cpp:61 `grad_w_shared` (ekv_cuda.cu:296-341, :530-574), i.e. the calls made by
  * cuda_backend.shared_backward (cuda_backend.py:50-99). n_entries <= 4194304: tables up to
  * 8192 entries (the reference's shared-backward limit, which the Python layer keeps where
- * CUDA_SHARED_BACKWARD is set) are held in LDS, larger ones read from global memory, the
- * counterpart of the reference's Triton backward (ekv_lut_triton.py:193-218). */
+ * CUDA_SHARED_BACKWARD is set) are held in LDS whole, up to 16384 as two passes that each hold
+ * one half of the records (the derivative table, then the current table), larger ones are
+ * read from global memory, the counterpart of the reference's Triton backward
+ * (ekv_lut_triton.py:193-218). */
 int isa_ekv_backward(const float* x, const float* vth_pos, const float* vth_neg, const float* grad_out,
                      const void* lut_bwd, int64_t M, int64_t K, int64_t O, int n_entries, float delta_min,
                      float delta_max, float v_sat, float* grad_x, float* grad_vth_pos, float* grad_vth_neg,

@@ -1502,7 +1502,133 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
     }
 }
 
-// LUT backward with the table in global memory (tables past kMaxEntriesBwd: the reference's
+// ----------------------------------------------------------------------------------
+// Backward for tables past the one-table LDS limit, up to kMaxEntriesBwdHalf entries: two
+// launches, each holding one 8-byte half of every record in LDS (131 KB at 16384 entries, one
+// block per CU). The D pass gathers {A_D, dD} and forms dVth and dX's main term
+// sum_o G r (L_D(d+) - L_D(d-)); the I pass gathers {A_I, dI} and forms dX's other term
+// -r^2/V_sat sum_o G (L_I(d+) - L_I(d-)). Each writes its own plane of dX partials per output
+// block, which dx_reduce_kernel sums with the others in plane order. The same tiling, prefetch
+// and lane-exchange reduction as bwd_body with two inputs per wave.
+// ----------------------------------------------------------------------------------
+
+constexpr int kMaxEntriesBwdHalf = 16384;
+
+template <int HALF, bool NEED_X, bool NEED_W, bool CLAMP>
+__device__ inline void bwd_body_half(const BwdArgs& a, const float2* tab, int item) {
+    constexpr int KR = kBwdKR, ORR = kBwdORR;
+    static_assert(KR == 2, "the half-table passes reduce two inputs per wave");
+    constexpr bool DVTH = HALF == 0 && NEED_W;
+    const int lane = threadIdx.x & 63;
+    const int kb = item % a.n_kb;
+    const int rest = item / a.n_kb;
+    const int ob = rest % a.n_ob;
+    const int sp = rest / a.n_ob;
+    const int o_lane = ob * 64 * ORR + lane * ORR;
+    const int k0 = kb * KR;
+    const int m_begin = sp * a.m_chunk;
+    const int m_end = min(a.M, m_begin + a.m_chunk);
+
+    float2 w[KR][ORR];
+#pragma unroll
+    for (int kk = 0; kk < KR; ++kk) {
+        const float4* src = reinterpret_cast<const float4*>(a.wsT + (size_t)(k0 + kk) * a.Op + o_lane);
+#pragma unroll
+        for (int j = 0; j < ORR / 2; ++j) {
+            const float4 v = src[j];
+            w[kk][2 * j] = make_float2(v.x, v.y);
+            w[kk][2 * j + 1] = make_float2(v.z, v.w);
+        }
+    }
+    float accp[KR][ORR], accn[KR][ORR];
+#pragma unroll
+    for (int kk = 0; kk < KR; ++kk)
+#pragma unroll
+        for (int j = 0; j < ORR; ++j) accp[kk][j] = accn[kk][j] = 0.0f;
+    const int row_kk = wave_rows_input2();  // input of this lane's row total
+    const float4* xbase = a.xrec + k0;
+    const float* gbase = a.grad + o_lane;
+    float4 xn[KR];
+    float gn[ORR];
+    auto fetch = [&](int m) {
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) xn[kk] = load_uniform4(xbase + (size_t)m * a.Kp + kk);
+        const float4 g4 = *reinterpret_cast<const float4*>(gbase + (size_t)m * a.ldg);
+        gn[0] = g4.x; gn[1] = g4.y; gn[2] = g4.z; gn[3] = g4.w;
+    };
+    fetch(m_begin);
+    float* dx_plane = a.dx_part + (size_t)(HALF * a.n_ob + ob) * a.M * a.K;
+#pragma unroll 1
+    for (int m = m_begin; m < m_end; ++m) {
+        float4 xcur[KR];
+        float g[ORR];
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) xcur[kk] = xn[kk];
+#pragma unroll
+        for (int j = 0; j < ORR; ++j) g[j] = gn[j];
+        fetch(min(m + 1, m_end - 1));
+        float tv[KR];
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) {
+            const float4 xv = xcur[kk];
+            float x1 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < ORR; ++j) {
+                const float cp = coord<CLAMP>(xv.x, w[kk][j].x, a.cmin, a.cmax);
+                const float cn = coord<CLAMP>(xv.x, w[kk][j].y, a.cmin, a.cmax);
+                const float2 ep = tab[(unsigned)cp];
+                const float2 en = tab[(unsigned)cn];
+                const float vp = fmaf(cp, ep.y, ep.x), vn = fmaf(cn, en.y, en.x);
+                const float gr = g[j] * xv.y;
+                if (NEED_X) x1 = fmaf(gr, vp - vn, x1);
+                if (DVTH) {
+                    accp[kk][j] = fmaf(gr, vp, accp[kk][j]);
+                    accn[kk][j] = fmaf(gr, vn, accn[kk][j]);
+                }
+            }
+            tv[kk] = HALF == 0 ? x1 : x1 * xv.z;  // the I pass carries -r/V_sat
+        }
+        if (NEED_X) {
+            const float sum = wave_sum_rows2(tv[0], tv[1]);
+            const int k = k0 + row_kk;
+            if ((lane & 31) == 0 && k < a.K) dx_plane[(size_t)m * a.K + k] = sum;
+        }
+    }
+    if (DVTH) {
+        float* dst_p = a.dv_part + (size_t)sp * 2 * a.Kp * a.Op;
+        float* dst_n = dst_p + (size_t)a.Kp * a.Op;
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) {
+            float* pp = dst_p + (size_t)(k0 + kk) * a.Op + o_lane;
+            float* pn = dst_n + (size_t)(k0 + kk) * a.Op + o_lane;
+#pragma unroll
+            for (int j = 0; j < ORR; ++j) {
+                pp[j] = accp[kk][j];
+                pn[j] = accn[kk][j];
+            }
+        }
+    }
+}
+
+template <int HALF, bool NEED_X, bool NEED_W>
+__global__ __launch_bounds__(1024) void bwd_half_kernel(BwdArgs a) {
+    extern __shared__ float2 s_half[];
+    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
+        const float4 rec = a.lut[i];
+        s_half[i] = HALF == 0 ? make_float2(rec.z, rec.w) : make_float2(rec.x, rec.y);
+    }
+    const bool fast = coords_in_padded_range(a.partials, a.NP);
+    __syncthreads();
+    const int waves = blockDim.x >> 6;
+    const int item = blockIdx.x * waves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (item >= a.n_items) return;
+    if (fast)
+        bwd_body_half<HALF, NEED_X, NEED_W, false>(a, s_half, item);
+    else
+        bwd_body_half<HALF, NEED_X, NEED_W, true>(a, s_half, item);
+}
+
+// LUT backward with the table in global memory (tables past kMaxEntriesBwdHalf: the reference's
 // Triton backward, ekv_lut_triton.py:193-218, for CUDA_SHARED_BACKWARD off): interleaved
 // records read through the caches, lane-exchange dX (LDS holds the transpose buffers only
 // for the dVth-only launch, which has no dX).
@@ -2165,7 +2291,7 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
 struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
-    bool grad_padded, split, lane_red, gtab;
+    bool grad_padded, split, lane_red, gtab, halves;
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
         bytes, lds_bytes;
 };
@@ -2185,15 +2311,18 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     const int mb = kRedSlots / kr;  // tokens per dX batch
     p.n_kb = (int)(p.Kp / kr);
     const size_t red_bytes = (size_t)kRedSlots * kRedStride * 4;
-    p.gtab = !exact && n_entries > kMaxEntriesBwd;  // table read from global memory
-    p.split = !exact && !p.gtab && ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
-    const size_t lut_bytes =
-        exact || p.gtab ? 0 : (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
+    p.gtab = !exact && n_entries > kMaxEntriesBwdHalf;  // table read from global memory
+    // past the one-table limit: a D pass and an I pass, each with one record half in LDS
+    p.halves = !exact && !p.gtab && n_entries > kMaxEntriesBwd;
+    p.split = !exact && !p.gtab && !p.halves && ISA_EKV_BWD_SPLIT && lut_records(n_entries) <= kSplitRecords;
+    const size_t lut_bytes = exact || p.gtab ? 0
+                             : p.halves     ? (size_t)lut_records(n_entries) * 8
+                                            : (size_t)(p.split ? kSplitRecords : lut_records(n_entries)) * 16;
     // dX reduction across the wave: lane exchanges (no LDS; measured 5% faster at N = 4096
     // and, with the 8192-entry table, the only way to keep 16 waves per block), or the LDS
     // transpose buffers
     p.lane_red = !exact && need_x &&
-                 (p.gtab || ISA_EKV_BWD_LANE_RED == 1 ||
+                 (p.gtab || p.halves || ISA_EKV_BWD_LANE_RED == 1 ||
                   (ISA_EKV_BWD_LANE_RED == 2 && lut_bytes + 16 * red_bytes > (size_t)kLdsBytes));
     const size_t per_wave = p.lane_red ? 0 : red_bytes;
     int wpb = 16;
@@ -2266,8 +2395,8 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     off += 256;
     p.off_gpad = off;
     if (p.grad_padded) off += (size_t)round_up((int64_t)M * p.Op * 4, 256);
-    p.off_dx = off;
-    if (need_x) off += (size_t)round_up((int64_t)p.n_ob * M * (K > 0 ? K : 1) * 4, 256);
+    p.off_dx = off;  // the half-table passes write a plane each
+    if (need_x) off += (size_t)round_up((int64_t)(p.halves ? 2 : 1) * p.n_ob * M * (K > 0 ? K : 1) * 4, 256);
     p.off_dv = off;
     if (need_w) off += (size_t)round_up((int64_t)p.n_split * 2 * p.Kp * p.Op * 4, 256);
     p.off_glue = off;  // col_part [kGlueBlocks][2][Op], r_part [kGlueBlocks][Op/256], aff_part [kDxReduceBlocks]
@@ -2385,6 +2514,18 @@ void launch_backward_copies(bool split, bool need_w, dim3 grid, dim3 block, size
             hipLaunchKernelGGL((bwd_kernel<true, false, false, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLdsI,
                                s, ba2);
     }
+}
+
+// The half-table backward: the D pass (dVth and, with dX, its main term), then the I pass.
+void launch_backward_halves(bool need_x, bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                            const BwdArgs& ba) {
+    if (need_x && need_w)
+        hipLaunchKernelGGL((bwd_half_kernel<0, true, true>), grid, block, lds, s, ba);
+    else if (need_x)
+        hipLaunchKernelGGL((bwd_half_kernel<0, true, false>), grid, block, lds, s, ba);
+    else
+        hipLaunchKernelGGL((bwd_half_kernel<0, false, true>), grid, block, lds, s, ba);
+    if (need_x) hipLaunchKernelGGL((bwd_half_kernel<1, true, false>), grid, block, lds, s, ba);
 }
 
 void launch_backward(bool exact, bool gtab, bool need_x, bool need_w, bool split, bool lane_red, dim3 grid,
@@ -2769,7 +2910,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
 // (the 8192-entry ones) take the copies when the coordinate window the launch reaches fits
 // that length, which the device decides.
 bool bwd_may_use_copies(const BwdPlan& p, bool exact, bool need_x) {
-    return kBwdORR == kFwdORR && !exact && !p.gtab && p.lane_red && need_x &&
+    return kBwdORR == kFwdORR && !exact && !p.gtab && !p.halves && p.lane_red && need_x &&
            (p.split ? p.lds_bytes <= kBwdTwoCopiesLds / 2 : true) && p.waves_per_block == 16;
 }
 
@@ -2903,7 +3044,9 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     }
     ProfiledLaunch* prof;
     prof_start(s, 1, &prof);
-    if (copies)
+    if (p.halves)
+        launch_backward_halves(need_x, need_w, grid, block, p.lds_bytes, s, ba);
+    else if (copies)
         launch_backward_copies(p.split, need_w, grid, block, p.lds_bytes, s, ba);
     else
         launch_backward(cs.exact, p.gtab, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
@@ -2913,7 +3056,8 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     if (need_x) {
         const float* aff = glue ? glue->in_affine : nullptr;
         hipLaunchKernelGGL(dx_reduce_kernel, dim3(kDxReduceBlocks), dim3(256), 0, s,
-                           reinterpret_cast<const float*>(ws + p.off_dx), p.n_ob, M * K, scale, grad_x, x, aff,
+                           reinterpret_cast<const float*>(ws + p.off_dx), (p.halves ? 2 : 1) * p.n_ob, M * K, scale,
+                           grad_x, x, aff,
                            glue ? glue->in_lo : 0.0f, glue ? glue->in_hi : 0.0f, aff_part);
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
