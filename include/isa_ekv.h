@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 8
+#define ISA_EKV_ABI_VERSION 9
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -159,8 +159,11 @@ int isa_ekv_exact_backward(const float* x, const float* vth_pos, const float* vt
  * and the backward's prep and reductions; every op keeps its own rounding).
  * Forward:  v = clamp(x * in_affine[0] + in_affine[1], in_lo, in_hi)      (if in_affine)
  *           idiff = isa_ekv_forward(v, ...)                               (clamped to idiff_min/max)
- *           y = clamp(idiff * r_tia[0], y_lo, y_hi)                       (if r_tia)
+ *           y = clamp(idiff * r, y_lo, y_hi)                              (if r_tia)
  *           out = y * adc_scale[o] + adc_shift[o]                         (if adc_scale)
+ * with the TIA gain r = r_tia[0], or, when r_log_scale is set, CIMLinear's learnable gain
+ *           r = r_tia[0] * exp(clamp(r_log_scale[0], r_log_lo, r_log_hi))  (cim.py:74-77;
+ *           r_tia then holds r_tia_base)
  * Output statistics of CIMLinear.forward's GPU branch (cim.py:194-198), on y (y = idiff
  * without r_tia), after the forward in stream order:
  *           stat_abs_max[0] = maximum(stat_abs_max[0], max |y|)          (NaN propagates)
@@ -175,15 +178,19 @@ typedef struct isa_ekv_glue {
     const float* adc_shift; /* [O], required with adc_scale */
     float* stat_abs_max;    /* [1] fp32, forward only */
     double* stat_total;     /* [1] fp64, forward only */
+    const float* r_log_scale; /* [1], with r_tia: learnable log gain */
+    float r_log_lo, r_log_hi;
 } isa_ekv_glue;
 
 /* Gradients of the glue parameters written by isa_ekv_layer_backward (device memory; each
  * may be null when its parameter is absent or needs no gradient). */
 typedef struct isa_ekv_glue_grads {
-    float* in_affine; /* [2] d{scale, shift} */
-    float* r_tia;     /* [1] */
-    float* adc_scale; /* [O] */
-    float* adc_shift; /* [O] */
+    float* in_affine;   /* [2] d{scale, shift} */
+    float* r_tia;       /* [1] d r (the gain) */
+    float* adc_scale;   /* [O] */
+    float* adc_shift;   /* [O] */
+    float* r_log_scale; /* [1] (glue with r_log_scale): d r * r_tia[0] * exp(clamp(.)), 0 where
+                           the clamp is active, as autograd through cim.py:77 */
 } isa_ekv_glue_grads;
 
 /* Workspace bytes for isa_ekv_layer_forward / isa_ekv_layer_backward. */
@@ -284,6 +291,17 @@ int isa_ekv_profile_end(double* ms, int* launches);
 #define ISA_EKV_PLAN_INFO_LEN 7
 int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x, int need_grad_w,
                       int64_t* info, int n_info);
+
+/* Process-wide planning option (no reference counterpart; the reference has no plans).
+ * Sets `option` to `value` and writes its former value to *previous (nullable); value < 0
+ * only reads it. Options:
+ *   ISA_EKV_OPT_COPY_MIN_CELLS: LUT calls of fewer cells M*K*O never use the second table
+ *     copy, nor enqueue its assignment pass (default 2^28: below that the extra launch costs
+ *     more than the copy saves). 0 lets every call consider it.
+ * Plans (and so workspace sizes) depend on the options: query workspace sizes after setting
+ * them, and do not change them while calls are in flight. */
+#define ISA_EKV_OPT_COPY_MIN_CELLS 1
+int isa_ekv_set_option(int option, int64_t value, int64_t* previous);
 
 /* Measurement aid, no reference counterpart: launches two 1024-thread blocks per CU, each
  * issuing 16 waves x 8 x `iterations` random LDS gathers of `record_bytes` (8: ds_read_b64,

@@ -45,6 +45,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -117,6 +118,15 @@ constexpr int kSplitRecords = 4096 + 2 * kPad;
 __host__ __device__ inline int lut_records(int n) { return n + 2 * kPad; }
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int64_t kCUs = 256;  // MI355X compute units (a fixed plan input: workspace sizes must not depend on the device)
+
+// Planning option ISA_EKV_OPT_COPY_MIN_CELLS: LUT calls of fewer cells never consider the
+// second table copy, whose assignment pass (and, in the backward, second main launch) costs
+// a small call more than the copy can save.
+std::atomic<int64_t> g_copy_min_cells{(int64_t)1 << 28};
+
+bool copies_pay(int64_t M, int64_t K, int64_t O) {
+    return (double)M * (double)K * (double)O >= (double)g_copy_min_cells.load(std::memory_order_relaxed);
+}
 
 thread_local char g_last_error[512] = "";
 
@@ -372,12 +382,12 @@ __device__ inline void store_token(float* dst, int64_t e, float c, float r, floa
 }
 
 template <int REC, bool EXACT>
-__device__ inline void prep_tokens(const PrepArgs& a, float& lo, float& hi) {
+__device__ inline void prep_tokens(const PrepArgs& a, int b, float& lo, float& hi) {
     const float aff_s = a.in_affine ? a.in_affine[0] : 1.0f;
     const float aff_b = a.in_affine ? a.in_affine[1] : 0.0f;
     const int64_t total = a.M * a.Kp;
     const int64_t chunk = 4 * (int64_t)blockDim.x;
-    for (int64_t base = (int64_t)blockIdx.x * chunk; base < total; base += (int64_t)kPrepBlocksX * chunk) {
+    for (int64_t base = (int64_t)b * chunk; base < total; base += (int64_t)kPrepBlocksX * chunk) {
         int64_t q = base + threadIdx.x;
         int64_t m, k;
         if (total <= 0xffffffffll) {
@@ -436,29 +446,30 @@ __device__ inline void prep_tokens(const PrepArgs& a, float& lo, float& hi) {
     }
 }
 
-__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
-    if (a.stat_bits && blockIdx.x == 0 && threadIdx.x == 0) *a.stat_bits = 0u;
+// Prep block b of kPrepBlocksX + kPrepBlocksW (token side, then threshold side).
+__device__ inline void prep_block(const PrepArgs& a, int b) {
+    if (a.stat_bits && b == 0 && threadIdx.x == 0) *a.stat_bits = 0u;
     float lo = INFINITY, hi = -INFINITY;
-    if (blockIdx.x < kPrepBlocksX) {
+    if (b < kPrepBlocksX) {
         if (a.exact) {
             if (a.rec_floats == 2)
-                prep_tokens<2, true>(a, lo, hi);
+                prep_tokens<2, true>(a, b, lo, hi);
             else
-                prep_tokens<4, true>(a, lo, hi);
+                prep_tokens<4, true>(a, b, lo, hi);
         } else {
             if (a.rec_floats == 2)
-                prep_tokens<2, false>(a, lo, hi);
+                prep_tokens<2, false>(a, b, lo, hi);
             else
-                prep_tokens<4, false>(a, lo, hi);
+                prep_tokens<4, false>(a, b, lo, hi);
         }
-        block_minmax(lo, hi, &a.partials[blockIdx.x]);
+        block_minmax(lo, hi, &a.partials[b]);
         return;
     }
     // threshold side: 64(o) x 32(k) tiles of raw thresholds transposed through LDS
     __shared__ float2 tile[32][65];
     const int64_t n_ot = a.Op / 64, n_kt = (a.Kp + 31) / 32;  // Op: multiple of 256; Kp: of 8
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
-    for (int64_t t = blockIdx.x - kPrepBlocksX; t < n_ot * n_kt; t += kPrepBlocksW) {
+    for (int64_t t = b - kPrepBlocksX; t < n_ot * n_kt; t += kPrepBlocksW) {
         const int64_t ot = t % n_ot, kt = t / n_ot;
         // load: rows o (64), cols k (32), coalesced along k
         for (int rr = ty; rr < 64; rr += 8) {
@@ -501,8 +512,10 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
         }
         __syncthreads();
     }
-    block_minmax(lo, hi, &a.partials[blockIdx.x]);
+    block_minmax(lo, hi, &a.partials[b]);
 }
+
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) { prep_block(a, blockIdx.x); }
 
 // Range of the prep kernel's coordinates: token side (xlo, xhi), threshold side (wlo, whi),
 // wave-uniform.
@@ -792,7 +805,9 @@ struct FwdArgs {
     float k2, c2;           // exact: 2^(-V_D a), V_D a
     // optional epilogue (layer glue): idiff is stored when given; out = glue(idiff)
     float* idiff;           // [M][O]
-    const float* r_tia;     // device scalar: y = clamp(idiff * r_tia, y_lo, y_hi)
+    const float* r_tia;     // device scalar: y = clamp(idiff * r, y_lo, y_hi), r = tia_gain(...)
+    const float* r_log_scale;
+    float r_log_lo, r_log_hi;
     float y_lo, y_hi;
     const float* adc_scale; // device [O]: out = y * adc_scale[o] + adc_shift[o]
     const float* adc_shift;
@@ -812,6 +827,18 @@ struct FwdTile {
     int k_lo, k_hi;    // padded-input range summed by this wave
     float* split_out;  // K split: this split's [M][O] partial sums (null: full sums, epilogue here)
 };
+
+// The TIA gain: r_tia[0], or CIMLinear's learnable gain r_tia_base * exp(clamp(log_scale,
+// lo, hi)) (cim.py:74-77) with the same ops in the same order (clamp keeping NaN, the
+// library expf, one rounded product). Wave-uniform.
+__device__ inline float tia_gain(const float* r_tia, const float* log_scale, float lo, float hi) {
+#pragma clang fp contract(off)
+    const float base = load_uniform1(r_tia);
+    if (!log_scale) return base;
+    const float ls = load_uniform1(log_scale);
+    const float c = ls != ls ? ls : fminf(fmaxf(ls, lo), hi);
+    return base * expf(c);
+}
 
 // TIA gain and output clamp (cim.py:190-193) and the ADC affine (cim.py:243), applied to one
 // output value: each tensor op's rounding kept (no contraction), NaN kept as torch.clamp does.
@@ -905,7 +932,7 @@ __device__ inline void fwd_body(const FwdArgs& a, const Cell cell, const float2*
     }
     if (a.glue) {
         const bool has_r = a.r_tia != nullptr;
-        const float r = has_r ? load_uniform1(a.r_tia) : 1.0f;
+        const float r = has_r ? tia_gain(a.r_tia, a.r_log_scale, a.r_log_lo, a.r_log_hi) : 1.0f;
         unsigned ymax = 0;
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
@@ -998,7 +1025,7 @@ __device__ inline bool fwd_tile(const FwdArgs& a, int MR, FwdTile& t) {
 // copy (they read the same record for most tokens: a broadcast), otherwise the copy whose
 // bank pair (floor coordinate, and its neighbour for the tokens whose fraction crosses the
 // threshold's) has the smaller expected load so far. Copy-1 thresholds are stored as
-// ws - T1 (so c' = xs - ws' = c + T1). Writes nothing unless the launch is in copy mode.
+// ws - T1 (so c' = xs - ws' = c + T1). Changes no record unless the launch is in copy mode.
 constexpr int kAssignThreads = 128;
 
 // Records [lo, lo + n) of the padded table hold every record the clamp-free loop reads, with
@@ -1010,28 +1037,32 @@ __device__ inline void coord_window(const CoordRange& c, int NP, int& lo, int& n
     n = __builtin_amdgcn_readfirstlane(h - l + 1);
 }
 
-// The launch's table-copy mode (fwd_copies_mode) as a word for the launches that follow;
-// tables longer than max_window records also need their coordinate window to fit it.
-__global__ __launch_bounds__(64) void copy_mode_kernel(const float2* __restrict__ partials, int NP, int max_window,
-                                                       int* mode_word) {
+// The launch's table-copy mode (fwd_copies_mode), wave-uniform; tables longer than
+// max_window records also need their coordinate window to fit it.
+__device__ inline bool launch_copy_mode(const float2* __restrict__ partials, int NP, int max_window) {
     bool on = fwd_copies_mode(partials, NP);
     if (on && NP > max_window) {
         int lo, n;
         coord_window(read_coord_range(partials), NP, lo, n);
         on = n <= max_window;
     }
-    if (threadIdx.x == 0) *mode_word = on ? 1 : 0;
+    return on;
 }
 
 // LANES = 32: 8-byte records, gathered by half-waves over 32 bank pairs; LANES = 16: 16-byte
 // records, gathered by quarter-waves over 16 bank quads. Copy 1 sits LANES / 2 bins away.
+// Every wave decides the launch's copy mode from the range partials (launch_copy_mode);
+// block 0 records it in the mode word for the launches that follow.
 template <int LANES>
 __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2* __restrict__ wsT,
-                                                              const int* __restrict__ mode_word, int64_t Kp,
-                                                              int64_t Op, int copy_offset) {
+                                                              const float2* __restrict__ partials, int NP,
+                                                              int max_window, int* __restrict__ mode_word,
+                                                              int64_t Kp, int64_t Op, int copy_offset) {
     static_assert(LANES == 32 || LANES == 16, "half-wave or quarter-wave gathers");
     constexpr int kGroups = 64 / LANES, kMask = LANES - 1;
-    if (__builtin_amdgcn_readfirstlane(*mode_word) == 0) return;
+    const bool on = launch_copy_mode(partials, NP, max_window);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = on ? 1 : 0;
+    if (!on) return;
     __shared__ float s_cnt[LANES][kAssignThreads];  // per-thread bank loads; [bin][thread]: conflict-free
     const int tid = threadIdx.x;
     const int64_t n_ot = Op / (64 * kFwdORR);
@@ -1085,7 +1116,7 @@ __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     if constexpr (!WIN)
         for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
     // fast loop and copy mode from one read of the range partials (as coords_in_padded_range,
-    // fwd_copies_mode and copy_mode_kernel decide them; a second read costs the main loop
+    // fwd_copies_mode and launch_copy_mode decide them; a second read costs the main loop
     // ~50 VGPRs)
     const CoordRange cr = read_coord_range(a.partials);
     const bool fast = __builtin_amdgcn_readfirstlane(
@@ -1630,8 +1661,8 @@ __global__ __launch_bounds__(1024) void bwd_half_kernel(BwdArgs a) {
 
 // LUT backward with the table in global memory (tables past kMaxEntriesBwdHalf: the reference's
 // Triton backward, ekv_lut_triton.py:193-218, for CUDA_SHARED_BACKWARD off): interleaved
-// records read through the caches, lane-exchange dX (LDS holds the transpose buffers only
-// for the dVth-only launch, which has no dX).
+// records read through the caches, lane-exchange dX (no LDS: the dVth-only launch has no dX
+// to reduce).
 template <bool NEED_X, bool NEED_W>
 __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_global_kernel(BwdArgs a) {
     extern __shared__ float4 s_red_global[];
@@ -1856,63 +1887,74 @@ __global__ __launch_bounds__(1024) void bwd_measured_kernel(BwdArgs a) {
 
 // dX[m,k] = scale * sum over output blocks, in block order (deterministic); scale is 1 for
 // the LUT path and the derivative constant of the exact cells. With an input mapping
-// v = clamp(x * s + b) in front of the layer (in_affine), dX is the gradient for v and this
-// kernel applies the mapping's backward (cim.py:37-39 under autograd: mask where
+// v = clamp(x * s + b) in front of the layer (in_affine), dX is the gradient for v and the
+// reduction applies the mapping's backward (cim.py:37-39 under autograd: mask where
 // lo <= x*s + b <= hi, dx = mask * dv * s) and writes per-block partial sums of
-// mask*dv*x (ds) and mask*dv (db) to aff_part[block] for glue_reduce_kernel.
-constexpr int kDxReduceBlocks = 1024;
-
+// mask*dv*x (ds) and mask*dv (db) to aff_part[block] for the glue reduction.
 // range_mask (no in_affine): dx = dv where lo <= x <= hi, else 0 (torch.clamp's backward of
 // the measured path's input clamp).
-__global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict__ part, int n_ob,
-                                                        int64_t n, float scale, float* __restrict__ dx,
-                                                        const float* __restrict__ x, const float* in_affine,
-                                                        float in_lo, float in_hi, float2* __restrict__ aff_part,
-                                                        int range_mask = 0) {
-    const float aff_s = in_affine ? in_affine[0] : 1.0f;
-    const float aff_b = in_affine ? in_affine[1] : 0.0f;
+constexpr int kDxReduceBlocks = 1024;  // blocks of a dX reduction, at most (aff_part entries)
+
+struct DxReduceArgs {
+    const float* part;  // [n_planes][n]
+    int n_planes;
+    int64_t n;          // M * K
+    float scale;
+    float* dx;
+    const float* x;
+    const float* in_affine;
+    float in_lo, in_hi;
+    float2* aff_part;   // [blocks] (in_affine)
+    int range_mask;
+};
+
+// Block b of nb (grid-stride over the elements).
+__device__ inline void dx_reduce_block(const DxReduceArgs& a, int b, int nb) {
+    const float aff_s = a.in_affine ? a.in_affine[0] : 1.0f;
+    const float aff_b = a.in_affine ? a.in_affine[1] : 0.0f;
     float ds = 0.0f, db = 0.0f;
     auto finish = [&](float s, float xv) {
-        s *= scale;
-        if (range_mask) {
-            s = (xv >= in_lo && xv <= in_hi) ? s : 0.0f;
-        } else if (in_affine) {
+        s *= a.scale;
+        if (a.range_mask) {
+            s = (xv >= a.in_lo && xv <= a.in_hi) ? s : 0.0f;
+        } else if (a.in_affine) {
             const float pre = mapped_pre(xv, aff_s, aff_b);
-            const float g = (pre >= in_lo && pre <= in_hi) ? s : 0.0f;
+            const float g = (pre >= a.in_lo && pre <= a.in_hi) ? s : 0.0f;
             ds = fmaf(g, xv, ds);
             db += g;
             s = g * aff_s;
         }
         return s;
     };
-    const bool need_x = range_mask || in_affine;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const bool vec4 = (n & 3) == 0 && (((uintptr_t)part | (uintptr_t)dx) & 15) == 0 &&
-                      (!need_x || ((uintptr_t)x & 15) == 0);
+    const bool need_x = a.range_mask || a.in_affine;
+    const int64_t n = a.n;
+    const int64_t stride = (int64_t)nb * blockDim.x;
+    const bool vec4 = (n & 3) == 0 && (((uintptr_t)a.part | (uintptr_t)a.dx) & 15) == 0 &&
+                      (!need_x || ((uintptr_t)a.x & 15) == 0);
     if (vec4) {  // 16-byte vectors
         const int64_t n4 = n >> 2;
-        const float4* p4 = reinterpret_cast<const float4*>(part);
-        for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n4; e += stride) {
+        const float4* p4 = reinterpret_cast<const float4*>(a.part);
+        for (int64_t e = (int64_t)b * blockDim.x + threadIdx.x; e < n4; e += stride) {
             float4 s = p4[e];
-            for (int b = 1; b < n_ob; ++b) {
-                const float4 v = p4[(size_t)b * n4 + e];
+            for (int q = 1; q < a.n_planes; ++q) {
+                const float4 v = p4[(size_t)q * n4 + e];
                 s.x += v.x;
                 s.y += v.y;
                 s.z += v.z;
                 s.w += v.w;
             }
-            const float4 xv = need_x ? reinterpret_cast<const float4*>(x)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
-            reinterpret_cast<float4*>(dx)[e] =
+            const float4 xv = need_x ? reinterpret_cast<const float4*>(a.x)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+            reinterpret_cast<float4*>(a.dx)[e] =
                 make_float4(finish(s.x, xv.x), finish(s.y, xv.y), finish(s.z, xv.z), finish(s.w, xv.w));
         }
     } else {
-        for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride) {
-            float s = part[e];
-            for (int b = 1; b < n_ob; ++b) s += part[(size_t)b * n + e];
-            dx[e] = finish(s, need_x ? x[e] : 0.0f);
+        for (int64_t e = (int64_t)b * blockDim.x + threadIdx.x; e < n; e += stride) {
+            float s = a.part[e];
+            for (int q = 1; q < a.n_planes; ++q) s += a.part[(size_t)q * n + e];
+            a.dx[e] = finish(s, need_x ? a.x[e] : 0.0f);
         }
     }
-    if (in_affine) {
+    if (a.in_affine) {
         __shared__ float s_ds[4], s_db[4];
         for (int off = 32; off > 0; off >>= 1) {
             ds += __shfl_xor(ds, off);
@@ -1925,51 +1967,65 @@ __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict_
         }
         __syncthreads();
         if (threadIdx.x == 0)
-            aff_part[blockIdx.x] = make_float2((s_ds[0] + s_ds[1]) + (s_ds[2] + s_ds[3]),
-                                               (s_db[0] + s_db[1]) + (s_db[2] + s_db[3]));
+            a.aff_part[b] = make_float2((s_ds[0] + s_ds[1]) + (s_ds[2] + s_ds[3]),
+                                        (s_db[0] + s_db[1]) + (s_db[2] + s_db[3]));
     }
 }
 
+// Blocks of a dX reduction over n elements: enough for one 16-byte vector per thread, at most
+// kDxReduceBlocks.
+int dx_reduce_blocks(int64_t n) {
+    return (int)std::max<int64_t>(1, std::min<int64_t>(kDxReduceBlocks, ((n + 3) / 4 + 255) / 256));
+}
+
+__global__ __launch_bounds__(256) void dx_reduce_kernel(DxReduceArgs a) { dx_reduce_block(a, blockIdx.x, gridDim.x); }
+
 // dVth+[o,k] = -scale * sum_s P[s][0][k][o], dVth-[o,k] = +scale * sum_s P[s][1][k][o]
-// (splits summed in order s = 0, 1, ...). Tiles of 64 outputs x 32 inputs: 16-byte loads
-// along o (a wave reads four 256-byte row segments per plane and split), transposed through
-// LDS, stores along k.
-__global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict__ part, int n_split,
-                                                        int K, int O, int Kp, int Op, float scale,
-                                                        float* __restrict__ dvp, float* __restrict__ dvn) {
-    __shared__ float tile[2][32][65];
-    const int n_ot = (O + 63) / 64, n_kt = (K + 31) / 32;
+// (splits summed in order s = 0, 1, ...). Tiles of 64 outputs x 8 inputs, one thread per
+// (plane, input, 4 outputs): 16-byte loads along o, eight splits' loads in flight per
+// thread, the tile transposed through LDS, stores along k.
+struct DvReduceArgs {
+    const float* part;  // [n_split][2][Kp][Op]
+    int n_split, K, O, Kp, Op;
+    float scale;
+    float* dvp;
+    float* dvn;
+};
+
+constexpr int kDvTileK = 8;
+
+int dv_reduce_tiles(int64_t K, int64_t O) { return (int)(((O + 63) / 64) * ((K + kDvTileK - 1) / kDvTileK)); }
+
+__device__ inline void dv_reduce_block(const DvReduceArgs& a, int b, int nb) {
+    __shared__ float tile[2][kDvTileK][65];
+    const int n_ot = (a.O + 63) / 64, n_kt = (a.K + kDvTileK - 1) / kDvTileK;
     const int t = threadIdx.x;
-    const int c4 = t & 15, row = t >> 4;  // loads: 16 float4 columns x 16 rows
-    const int kl = t & 31, orow = t >> 5;  // stores: 32 inputs x 8 output rows
-    const size_t plane = (size_t)Kp * Op;
-    for (int tile_id = blockIdx.x; tile_id < n_ot * n_kt; tile_id += gridDim.x) {
+    const int c4 = t & 15, row = (t >> 4) & (kDvTileK - 1), plane = t >> 7;  // loads
+    const int kl = t & (kDvTileK - 1), orow = t >> 3;                          // stores: 8 x 32
+    const size_t plane_floats = (size_t)a.Kp * a.Op;
+    const float sg = plane == 0 ? -a.scale : a.scale;
+    for (int tile_id = b; tile_id < n_ot * n_kt; tile_id += nb) {
         const int ot = tile_id % n_ot, kt = tile_id / n_ot;
-        for (int rr = row; rr < 32; rr += 16) {
-            const int k = kt * 32 + rr;
-            float4 sp = make_float4(0.f, 0.f, 0.f, 0.f), sn = sp;
-            if (k < K) {  // ot * 64 + 63 < Op: Op is O rounded up to 256
-                const float4* src = reinterpret_cast<const float4*>(part + (size_t)k * Op + ot * 64 + c4 * 4);
-                const size_t plane4 = plane / 4;
-#pragma unroll 4
-                for (int sidx = 0; sidx < n_split; ++sidx) {
-                    const float4 a = src[(size_t)sidx * 2 * plane4];
-                    const float4 b = src[(size_t)sidx * 2 * plane4 + plane4];
-                    sp.x += a.x; sp.y += a.y; sp.z += a.z; sp.w += a.w;
-                    sn.x += b.x; sn.y += b.y; sn.z += b.z; sn.w += b.w;
-                }
+        const int k = kt * kDvTileK + row;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < a.K) {  // ot * 64 + 63 < Op: Op is O rounded up to 256
+            const float4* src =
+                reinterpret_cast<const float4*>(a.part + plane * plane_floats + (size_t)k * a.Op + ot * 64 + c4 * 4);
+            const size_t split4 = 2 * plane_floats / 4;
+#pragma unroll 8
+            for (int sidx = 0; sidx < a.n_split; ++sidx) {
+                const float4 v = src[(size_t)sidx * split4];
+                acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
             }
-            float* tp = &tile[0][rr][c4 * 4];
-            float* tn = &tile[1][rr][c4 * 4];
-            tp[0] = -sp.x * scale; tp[1] = -sp.y * scale; tp[2] = -sp.z * scale; tp[3] = -sp.w * scale;
-            tn[0] = sn.x * scale; tn[1] = sn.y * scale; tn[2] = sn.z * scale; tn[3] = sn.w * scale;
         }
+        float* tp = &tile[plane][row][c4 * 4];
+        tp[0] = acc.x * sg; tp[1] = acc.y * sg; tp[2] = acc.z * sg; tp[3] = acc.w * sg;
         __syncthreads();
-        for (int orr = orow; orr < 64; orr += 8) {
-            const int o = ot * 64 + orr, k = kt * 32 + kl;
-            if (o < O && k < K) {
-                dvp[(size_t)o * K + k] = tile[0][kl][orr];
-                dvn[(size_t)o * K + k] = tile[1][kl][orr];
+        for (int orr = orow; orr < 64; orr += 32) {
+            const int o = ot * 64 + orr, kk = kt * kDvTileK + kl;
+            if (o < a.O && kk < a.K) {
+                a.dvp[(size_t)o * a.K + kk] = tile[0][kl][orr];
+                a.dvn[(size_t)o * a.K + kk] = tile[1][kl][orr];
             }
         }
         __syncthreads();
@@ -1987,7 +2043,7 @@ __global__ __launch_bounds__(256) void dv_reduce_kernel(const float* __restrict_
 // A block owns a contiguous row range (one of kGlueBlocks) and 256 padded outputs (one of
 // Op / 256): 4 row lanes x 64 output lanes, each thread 4 outputs 64 apart so every load
 // instruction of a wave reads 64 consecutive floats. Per-block partials are combined in
-// block order by glue_reduce_kernel, so every result is reproducible. G_eff is written
+// block order by the glue reduction, so every result is reproducible. G_eff is written
 // [M][Op] with zeros in the padded outputs.
 // ----------------------------------------------------------------------------------
 
@@ -1997,7 +2053,9 @@ struct GlueGradArgs {
     const float* g;          // [M][O]
     const float* idiff;      // [M][O]
     int64_t M, O, Op;
-    const float* r_tia;
+    const float* r_tia;      // the gain is tia_gain(r_tia, r_log_scale, r_log_lo, r_log_hi)
+    const float* r_log_scale;
+    float r_log_lo, r_log_hi;
     float y_lo, y_hi;
     const float* adc_scale;  // [O] or null
     float* geff;             // [M][Op]
@@ -2005,10 +2063,10 @@ struct GlueGradArgs {
     float* r_part;           // [kGlueBlocks * (Op / 256)]
 };
 
-__global__ __launch_bounds__(256) void glue_grad_kernel(GlueGradArgs a) {
+// Glue block (row range rg, output block ob); n_gob = Op / 256 output blocks.
+__device__ inline void glue_grad_block(const GlueGradArgs& a, int rg, int ob, int n_gob) {
     const bool has_r = a.r_tia != nullptr;
-    const float r = has_r ? *a.r_tia : 1.0f;
-    const int rg = blockIdx.x, ob = blockIdx.y;
+    const float r = has_r ? tia_gain(a.r_tia, a.r_log_scale, a.r_log_lo, a.r_log_hi) : 1.0f;
     const int lane_o = threadIdx.x & 63, row_lane = threadIdx.x >> 6;
     const int64_t rows = (a.M + kGlueBlocks - 1) / kGlueBlocks;
     const int64_t m_begin = (int64_t)rg * rows, m_end = m_begin + rows < a.M ? m_begin + rows : a.M;
@@ -2061,51 +2119,86 @@ __global__ __launch_bounds__(256) void glue_grad_kernel(GlueGradArgs a) {
         a.col_part[(size_t)rg * 2 * a.Op + oo] = sa;
         a.col_part[(size_t)rg * 2 * a.Op + a.Op + oo] = sc;
     }
-    if (has_r && threadIdx.x == 0) a.r_part[(size_t)rg * gridDim.y + ob] = (s_r[0] + s_r[1]) + (s_r[2] + s_r[3]);
+    if (has_r && threadIdx.x == 0) a.r_part[(size_t)rg * n_gob + ob] = (s_r[0] + s_r[1]) + (s_r[2] + s_r[3]);
+}
+
+// Grid (kGlueBlocks, Op / 256).
+__global__ __launch_bounds__(256) void glue_grad_kernel(GlueGradArgs a) {
+    glue_grad_block(a, blockIdx.x, blockIdx.y, gridDim.y);
+}
+
+// The table backward's prep and the glue gradient pass in one launch (independent work:
+// the prep reads x and the thresholds, the glue pass G and idiff): blocks
+// [0, kPrepBlocksX + kPrepBlocksW) prep, then, when g.geff is set, kGlueBlocks x (Op / 256)
+// glue blocks, row range fastest.
+__global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a, GlueGradArgs g) {
+    constexpr int kPrep = kPrepBlocksX + kPrepBlocksW;
+    if (blockIdx.x < kPrep) {
+        prep_block(a, blockIdx.x);
+        return;
+    }
+    const int b = blockIdx.x - kPrep;
+    glue_grad_block(g, b % kGlueBlocks, b / kGlueBlocks, (int)(g.Op / 256));
 }
 
 // Final sums of the glue partials in fixed order: d adc_scale/shift[o] over glue blocks,
 // d r_tia over glue blocks and output blocks, d {scale, shift} of the input mapping over
-// dx_reduce blocks. Grid: ceil(O / 64) column blocks (64 outputs x 4 quarters of the glue
-// blocks each, quarters combined in LDS), then one block for the three scalars (strided
-// partial sums per thread, then a tree in LDS).
-__global__ __launch_bounds__(256) void glue_reduce_kernel(const float* __restrict__ col_part,
-                                                          const float* __restrict__ r_part,
-                                                          const float2* __restrict__ aff_part, int64_t O,
-                                                          int64_t Op, float* d_adc_scale, float* d_adc_shift,
-                                                          float* d_r_tia, float* d_affine) {
+// the dX reduction's blocks. Blocks: ceil(O / 64) column blocks (64 outputs x 4 quarters of
+// the glue blocks each, quarters combined in LDS), then one block for the three scalars
+// (strided partial sums per thread, then a tree in LDS).
+struct GlueReduceArgs {
+    const float* col_part;
+    const float* r_part;
+    const float2* aff_part;
+    int n_aff;  // aff_part entries (the dX reduction's blocks)
+    int64_t O, Op;
+    float* d_adc_scale;
+    float* d_adc_shift;
+    float* d_r_tia;
+    float* d_affine;
+    // d r_log_scale = d r * r_tia[0] * exp(clamp(log_scale)) where lo <= log_scale <= hi, else
+    // 0: autograd through cim.py:77 (mul, exp, clamp backward), op by op
+    const float* r_tia;
+    const float* r_log_scale;
+    float r_log_lo, r_log_hi;
+    float* d_r_log_scale;
+};
+
+int glue_reduce_blocks(int64_t O) { return (int)((O + 63) / 64 + 1); }
+
+__device__ inline void glue_reduce_block(const GlueReduceArgs& a, int b) {
     __shared__ float red[3][256];
     const int t = threadIdx.x;
-    const int64_t n_col_blocks = (O + 63) / 64;
-    if ((int64_t)blockIdx.x < n_col_blocks) {
-        if (!d_adc_scale && !d_adc_shift) return;
-        const int64_t o = (int64_t)blockIdx.x * 64 + (t & 63);
+    const int64_t n_col_blocks = (a.O + 63) / 64;
+    if ((int64_t)b < n_col_blocks) {
+        if (!a.d_adc_scale && !a.d_adc_shift) return;
+        const int64_t o = (int64_t)b * 64 + (t & 63);
         constexpr int kQuarter = kGlueBlocks / 4;
         const int b0 = (t >> 6) * kQuarter;
         float sa = 0.0f, sc = 0.0f;
-        if (o < O) {
-            for (int b = b0; b < b0 + kQuarter; ++b) {
-                sa += col_part[(size_t)b * 2 * Op + o];
-                sc += col_part[(size_t)b * 2 * Op + Op + o];
+        if (o < a.O) {
+            for (int q = b0; q < b0 + kQuarter; ++q) {
+                sa += a.col_part[(size_t)q * 2 * a.Op + o];
+                sc += a.col_part[(size_t)q * 2 * a.Op + a.Op + o];
             }
         }
         red[0][t] = sa;
         red[1][t] = sc;
         __syncthreads();
-        if (t < 64 && o < O) {
-            if (d_adc_scale) d_adc_scale[o] = (red[0][t] + red[0][t + 64]) + (red[0][t + 128] + red[0][t + 192]);
-            if (d_adc_shift) d_adc_shift[o] = (red[1][t] + red[1][t + 64]) + (red[1][t + 128] + red[1][t + 192]);
+        if (t < 64 && o < a.O) {
+            if (a.d_adc_scale) a.d_adc_scale[o] = (red[0][t] + red[0][t + 64]) + (red[0][t + 128] + red[0][t + 192]);
+            if (a.d_adc_shift) a.d_adc_shift[o] = (red[1][t] + red[1][t + 64]) + (red[1][t + 128] + red[1][t + 192]);
         }
         return;
     }
-    const int n_rpart = kGlueBlocks * (int)(Op / 256);
+    const int n_rpart = kGlueBlocks * (int)(a.Op / 256);
     float sr = 0.0f, ss = 0.0f, sb = 0.0f;
-    if (d_r_tia)
-        for (int b = t; b < n_rpart; b += 256) sr += r_part[b];
-    if (d_affine)
-        for (int b = t; b < kDxReduceBlocks; b += 256) {
-            ss += aff_part[b].x;
-            sb += aff_part[b].y;
+    if (a.d_r_tia || a.d_r_log_scale)
+        for (int q = t; q < n_rpart; q += 256) sr += a.r_part[q];
+    if (a.d_affine)
+        for (int q = t; q < a.n_aff; q += 256) {
+            ss += a.aff_part[q].x;
+            sb += a.aff_part[q].y;
         }
     red[0][t] = sr;
     red[1][t] = ss;
@@ -2120,12 +2213,39 @@ __global__ __launch_bounds__(256) void glue_reduce_kernel(const float* __restric
         __syncthreads();
     }
     if (t == 0) {
-        if (d_r_tia) d_r_tia[0] = red[0][0];
-        if (d_affine) {
-            d_affine[0] = red[1][0];
-            d_affine[1] = red[2][0];
+        if (a.d_r_tia) a.d_r_tia[0] = red[0][0];
+        if (a.d_r_log_scale) {
+#pragma clang fp contract(off)
+            const float ls = a.r_log_scale[0];
+            const bool pass = ls >= a.r_log_lo && ls <= a.r_log_hi;  // torch.clamp's backward mask
+            const float ge = red[0][0] * a.r_tia[0];                  // mul backward: d r * base
+            a.d_r_log_scale[0] = pass ? ge * expf(ls) : 0.0f;          // exp backward: * exp(ls)
+        }
+        if (a.d_affine) {
+            a.d_affine[0] = red[1][0];
+            a.d_affine[1] = red[2][0];
         }
     }
+}
+
+__global__ __launch_bounds__(256) void glue_reduce_kernel(GlueReduceArgs a) { glue_reduce_block(a, blockIdx.x); }
+
+// The backward's final reductions in one launch: dx_blocks dX blocks, then dv_blocks dVth
+// blocks, then (gl_blocks > 0) the glue sums, which must not need the dX blocks' aff_part
+// (no input mapping). A part with zero blocks is skipped.
+__global__ __launch_bounds__(256) void grad_reduce_kernel(DxReduceArgs dx, int dx_blocks, DvReduceArgs dv,
+                                                          int dv_blocks, GlueReduceArgs gl) {
+    int b = blockIdx.x;
+    if (b < dx_blocks) {
+        dx_reduce_block(dx, b, dx_blocks);
+        return;
+    }
+    b -= dx_blocks;
+    if (b < dv_blocks) {
+        dv_reduce_block(dv, b, dv_blocks);
+        return;
+    }
+    glue_reduce_block(gl, b - dv_blocks);
 }
 
 // ----------------------------------------------------------------------------------
@@ -2237,6 +2357,28 @@ constexpr int64_t kBwdMinSplitTokens = ISA_EKV_BWD_MIN_SPLIT_M;  // tokens per b
 #endif
 constexpr int kFwdMaxSplit = 8;
 constexpr int kFwdMinSplitInputs = ISA_EKV_FWD_MIN_SPLIT_K;  // padded inputs per K split, at least
+// Small-problem plans (too little work for the chip at any MR and K split of the usual plan)
+// weigh a wave's work as its chunk (padded inputs, forward; tokens, backward) plus this much
+// per-wave setup (threshold records, partial-plane stores, pipeline fill), in the same units.
+#ifndef ISA_EKV_FWD_WAVE_COST
+#define ISA_EKV_FWD_WAVE_COST 8
+#endif
+#ifndef ISA_EKV_BWD_ITEM_COST
+#define ISA_EKV_BWD_ITEM_COST 2
+#endif
+// ... and a CU holding one block where it could hold two runs its waves at this percentage of
+// the full rate (fewer waves to hide the LDS and memory latencies)
+#ifndef ISA_EKV_LONE_BLOCK_RATE
+#define ISA_EKV_LONE_BLOCK_RATE 70
+#endif
+
+// Relative duration of a launch of `blocks` equal blocks of `work` units each (at most one
+// round), `resident` blocks fitting a CU: its busiest CU's work at that CU's rate.
+int64_t small_launch_cost(int64_t blocks, int64_t work, int resident) {
+    const int64_t per_cu = (blocks + kCUs - 1) / kCUs;
+    if (per_cu == 1 && resident > 1) return work * 100 / ISA_EKV_LONE_BLOCK_RATE;
+    return per_cu * work;
+}
 
 FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_split = true, int wpb = kFwdWaves) {
     FwdPlan p{};
@@ -2253,15 +2395,36 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
     int sp_max = 1;
     while (allow_split && sp_max < kFwdMaxSplit && p.Kp / (2 * sp_max) >= kFwdMinSplitInputs) sp_max *= 2;
     int split = 1;
+    bool small = false;
     for (p.mr = 8;; p.mr /= 2) {
         const int64_t waves = round_up(M, (int64_t)wpb * p.mr) / p.mr * p.n_ot;
         if (p.mr == 2 || waves * sp_max >= waves_target) {
+            small = waves * sp_max < waves_target;
             while (split < sp_max && waves * split < waves_target) split *= 2;
             break;
         }
     }
     const int64_t tokens_per_block = (int64_t)wpb * p.mr;
     p.n_mt = (int)((M + tokens_per_block - 1) / tokens_per_block);
+    if (small && allow_split) {
+        // Too few waves to cover the chip even at the largest split: one round of blocks at
+        // most, and the launch lasts as long as its busiest CU. Take the split count (any
+        // count up to kFwdMaxSplit whose chunks hold at least 8 padded inputs) that minimises
+        // small_launch_cost of blocks of (chunk + per-wave setup); ties go to fewer splits.
+        const int64_t tiles = (int64_t)p.n_mt * p.n_ot;
+        int64_t best_cost = -1;
+        for (int sp = 1; sp <= kFwdMaxSplit; ++sp) {
+            const int64_t chunk = round_up((p.Kp + sp - 1) / sp, 8);
+            const int64_t n_sp = (p.Kp + chunk - 1) / chunk;
+            if (n_sp != sp) continue;  // the same plan as a smaller count
+            const int64_t cost =
+                small_launch_cost(tiles * n_sp, 100 * (chunk + ISA_EKV_FWD_WAVE_COST), wpb == kFwdWaves ? 2 : 1);
+            if (best_cost < 0 || cost < best_cost) {
+                best_cost = cost;
+                split = sp;
+            }
+        }
+    }
     p.k_chunk = (int)round_up((p.Kp + split - 1) / split, 8);
     p.n_split = (int)((p.Kp + p.k_chunk - 1) / p.k_chunk);
     p.blocks = p.n_mt * p.n_ot * p.n_split;
@@ -2292,6 +2455,7 @@ struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
     bool grad_padded, split, lane_red, gtab, halves;
+    bool copies;  // at least ISA_EKV_OPT_COPY_MIN_CELLS cells: the second table copy may pay
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
         bytes, lds_bytes;
 };
@@ -2324,7 +2488,9 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     p.lane_red = !exact && need_x &&
                  (p.gtab || p.halves || ISA_EKV_BWD_LANE_RED == 1 ||
                   (ISA_EKV_BWD_LANE_RED == 2 && lut_bytes + 16 * red_bytes > (size_t)kLdsBytes));
-    const size_t per_wave = p.lane_red ? 0 : red_bytes;
+    // (a dVth-only launch has no dX to reduce: no buffers, so every gradient subset gets the
+    // same blocks and token splits, and the same dVth sums)
+    const size_t per_wave = p.lane_red || !need_x ? 0 : red_bytes;
     int wpb = 16;
     while (wpb > 1 && lut_bytes + wpb * per_wave > (size_t)kLdsBytes) wpb /= 2;
     p.waves_per_block = wpb;
@@ -2356,7 +2522,9 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     // interleaved tables (past kSplitRecords entries) may run the persistent two-copy launch
     // instead (one 16-wave block per CU, kBwdKRTwoCopies inputs per wave, decided on the
     // device): fill the rounds of both
-    const bool pair = !exact && !p.gtab && !p.split && p.lane_red && wpb == 16 && kBwdORR == kFwdORR;
+    p.copies = copies_pay(M, K, O);
+    const bool pair =
+        !exact && p.copies && !p.gtab && !p.halves && !p.split && p.lane_red && wpb == 16 && kBwdORR == kFwdORR;
     auto fill_pair = [&](int64_t sp) {
         const double f1 = fill_of(sp);
         if (!pair) return f1;
@@ -2373,6 +2541,24 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     while (best_splits < top_splits && fill_pair(best_splits) < best_fill - 0.005) ++best_splits;
     p.m_chunk = (int)round_up((M + best_splits - 1) / best_splits, mb);
     if (p.m_chunk < mb) p.m_chunk = mb;
+    if (!pair && base_items * max_splits < 2 * kCUs * resident * wpb) {
+        // Too few tokens for two full rounds of blocks: the launch lasts as long as its busiest
+        // CU. The token loop masks the tokens past a chunk, so any chunk length works; take
+        // the one (of at least 8 tokens) minimising small_launch_cost of blocks of (chunk +
+        // per-item setup); ties go to fewer splits.
+        const int64_t min_chunk = std::max<int64_t>(8, mb);
+        int64_t best_cost = -1;
+        for (int64_t sp = 1; sp <= (M + min_chunk - 1) / min_chunk; ++sp) {
+            const int64_t chunk = (M + sp - 1) / sp;
+            if ((M + chunk - 1) / chunk != sp) continue;  // the same plan as a smaller count
+            const int64_t blocks = (base_items * sp + wpb - 1) / wpb;
+            const int64_t cost = small_launch_cost(blocks, 100 * (chunk + ISA_EKV_BWD_ITEM_COST), (int)resident);
+            if (best_cost < 0 || cost < best_cost) {
+                best_cost = cost;
+                p.m_chunk = (int)chunk;
+            }
+        }
+    }
     p.n_split = (int)((M + p.m_chunk - 1) / p.m_chunk);
     if (p.n_split < 1) p.n_split = 1;
     p.n_items = (int)(base_items * p.n_split);
@@ -2688,7 +2874,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(FwdArgs a, int clamp_
     const int64_t n = (int64_t)a.M * a.O;
     const int64_t nv = n / VEC;
     const bool has_r = a.glue && a.r_tia != nullptr;
-    const float r = has_r ? load_uniform1(a.r_tia) : 1.0f;
+    const float r = has_r ? tia_gain(a.r_tia, a.r_log_scale, a.r_log_lo, a.r_log_hi) : 1.0f;
     unsigned ymax = 0;
     for (int64_t ev = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; ev < nv; ev += (int64_t)gridDim.x * blockDim.x) {
         float v[VEC], id[VEC];
@@ -2772,7 +2958,8 @@ hipError_t finish_split(const FwdPlan& p, const FwdArgs& fa, bool clamp_out, hip
 // the block's table load, barrier and tail are spread over less work).
 FwdPlan plan_forward_call(bool exact, int n_entries, int64_t M, int64_t K, int64_t O) {
     FwdPlan p = plan_forward(M, K, O, exact, true, kFwdWaves);
-    if (!exact && fwd_copy_lds(n_entries) > kFwdCopyLdsBytes && fwd_copy_lds(n_entries) <= (size_t)kLdsBytes) {
+    if (!exact && copies_pay(M, K, O) && fwd_copy_lds(n_entries) > kFwdCopyLdsBytes &&
+        fwd_copy_lds(n_entries) <= (size_t)kLdsBytes) {
         const FwdPlan p16 = plan_forward(M, K, O, false, true, 2 * kFwdWaves);
         if (p16.k_chunk >= kFwdCopyMinInputs16) p = p16;
     }
@@ -2782,18 +2969,19 @@ FwdPlan plan_forward_call(bool exact, int n_entries, int64_t M, int64_t K, int64
 // Table placement of a LUT forward launch with wpb waves per block: LDS bytes, and the second
 // table copy (copy_offset > 0: the launch may use it, decided on the device from the range
 // partials and recorded in the mode word; copy_window > 0: the copies hold only the
-// coordinate window, of at most that many records).
+// coordinate window, of at most that many records). copies = false (calls below
+// ISA_EKV_OPT_COPY_MIN_CELLS): one copy.
 struct FwdTableCfg {
     bool gtab;  // table read from global memory
     size_t lds;
     int copy_offset, copy_window;
 };
 
-FwdTableCfg fwd_table_cfg(int n_entries, int wpb) {
+FwdTableCfg fwd_table_cfg(int n_entries, int wpb, bool copies) {
     FwdTableCfg t{};
     t.gtab = n_entries > kMaxEntriesFwd;
     t.lds = t.gtab ? 0 : (size_t)lut_records(n_entries) * 8;
-    if (t.gtab) return t;
+    if (t.gtab || !copies) return t;
     // the second table copy (used when the thresholds spread wide) when both copies still
     // leave room for two forward blocks per CU
     int t1 = fwd_copy_offset(n_entries);
@@ -2852,6 +3040,9 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.glue = 1;
         fa.idiff = idiff;
         fa.r_tia = glue->r_tia;
+        fa.r_log_scale = glue->r_log_scale;
+        fa.r_log_lo = glue->r_log_lo;
+        fa.r_log_hi = glue->r_log_hi;
         fa.y_lo = glue->y_lo;
         fa.y_hi = glue->y_hi;
         fa.adc_scale = glue->adc_scale;
@@ -2870,19 +3061,18 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         fa.cmin = (float)kPad;
         fa.cmax = (float)(kPad + cs.n_entries - 1);
         fa.out_scale = 1.0f;
-        const FwdTableCfg tc = fwd_table_cfg(cs.n_entries, p.wpb);
+        const FwdTableCfg tc = fwd_table_cfg(cs.n_entries, p.wpb, copies_pay(M, K, O));
         gtab = tc.gtab;
         lds = tc.lds;
         fa.copy_offset = tc.copy_offset;
         fa.copy_window = tc.copy_window;
         if (tc.copy_offset > 0) {
             int* mode = reinterpret_cast<int*>(ws + p.off_mode);
-            hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, fa.partials, fa.NP,
-                               fa.copy_window > 0 ? fa.copy_window : fa.NP, mode);
             const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
-                               dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp,
-                               p.Op, tc.copy_offset);
+                               dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials,
+                               fa.NP, fa.copy_window > 0 ? fa.copy_window : fa.NP, mode, p.Kp, p.Op,
+                               tc.copy_offset);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward copy assignment launch");
         }
@@ -2910,7 +3100,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
 // (the 8192-entry ones) take the copies when the coordinate window the launch reaches fits
 // that length, which the device decides.
 bool bwd_may_use_copies(const BwdPlan& p, bool exact, bool need_x) {
-    return kBwdORR == kFwdORR && !exact && !p.gtab && !p.halves && p.lane_red && need_x &&
+    return kBwdORR == kFwdORR && !exact && p.copies && !p.gtab && !p.halves && p.lane_red && need_x &&
            (p.split ? p.lds_bytes <= kBwdTwoCopiesLds / 2 : true) && p.waves_per_block == 16;
 }
 
@@ -2928,7 +3118,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     const bool need_w = grad_vth_pos != nullptr || grad_vth_neg != nullptr;
     if (need_w && (grad_vth_pos == nullptr || grad_vth_neg == nullptr))
         return fail(ISA_EKV_EINVAL, "grad_vth_pos and grad_vth_neg must both be given or both be null");
-    const bool need_glue = gg && (gg->in_affine || gg->r_tia || gg->adc_scale || gg->adc_shift);
+    const bool need_glue = gg && (gg->in_affine || gg->r_tia || gg->adc_scale || gg->adc_shift || gg->r_log_scale);
     if (!need_x && !need_w && !need_glue) return 0;
     hipError_t err;
     // degenerate shapes: empty reductions give zero gradients (with glue and K == 0 the
@@ -2942,6 +3132,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         if (gg) {
             zero_fill(gg->in_affine, 2, s);
             zero_fill(gg->r_tia, 1, s);
+            zero_fill(gg->r_log_scale, 1, s);
             zero_fill(gg->adc_scale, O, s);
             zero_fill(gg->adc_shift, O, s);
         }
@@ -2959,25 +3150,31 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     float* r_part = col_part + (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) / 4;
     float2* aff_part =
         reinterpret_cast<float2*>(r_part + (size_t)round_up((int64_t)kGlueBlocks * (p.Op / 256) * 4, 256) / 4);
+    GlueGradArgs ga{};
     if (glue) {
-        GlueGradArgs ga{grad_out, idiff, M, O, p.Op, glue->r_tia, glue->y_lo, glue->y_hi, glue->adc_scale,
-                        reinterpret_cast<float*>(ws + p.off_gpad), col_part, r_part};
-        hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks, (unsigned)(p.Op / 256)), dim3(256), 0, s, ga);
-        err = hipGetLastError();
-        if (err != hipSuccess) return hip_fail(err, "glue grad launch");
+        ga = GlueGradArgs{grad_out, idiff, M, O, p.Op, glue->r_tia, glue->r_log_scale, glue->r_log_lo,
+                          glue->r_log_hi, glue->y_lo, glue->y_hi, glue->adc_scale,
+                          reinterpret_cast<float*>(ws + p.off_gpad), col_part, r_part};
         if (K == 0) {  // nothing reaches x or the thresholds
+            hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks, (unsigned)(p.Op / 256)), dim3(256), 0, s, ga);
             if (gg) zero_fill(gg->in_affine, 2, s);
-            if (gg && (gg->r_tia || gg->adc_scale || gg->adc_shift))
-                hipLaunchKernelGGL(glue_reduce_kernel, dim3((unsigned)((O + 63) / 64 + 1)), dim3(256), 0, s, col_part, r_part,
-                                   aff_part, O, p.Op, gg->adc_scale, gg->adc_shift, gg->r_tia, nullptr);
+            if (gg && (gg->r_tia || gg->adc_scale || gg->adc_shift || gg->r_log_scale)) {
+                const GlueReduceArgs gr{col_part, r_part, aff_part, 0, O, p.Op, gg->adc_scale, gg->adc_shift,
+                                        gg->r_tia, nullptr, glue->r_tia, glue->r_log_scale, glue->r_log_lo,
+                                        glue->r_log_hi, gg->r_log_scale};
+                hipLaunchKernelGGL(glue_reduce_kernel, dim3((unsigned)glue_reduce_blocks(O)), dim3(256), 0, s, gr);
+            }
             err = hipGetLastError();
-            if (err != hipSuccess) return hip_fail(err, "glue reduce launch");
+            if (err != hipSuccess) return hip_fail(err, "glue gradient launch");
             return 0;
         }
     }
+    // the prep, and with the layer glue its gradient pass (G_eff for the main kernel)
     const PrepArgs pa = make_prep(cs, x, vth_pos, vth_neg, M, K, O, p.Kp, p.Op, v_sat, 4, ws, p.off_xrec, p.off_wsT,
                                   p.off_xrec_alt, p.off_wsT_alt, p.off_part, glue);
-    hipLaunchKernelGGL(prep_kernel, dim3(kPrepBlocksX + kPrepBlocksW), dim3(256), 0, s, pa);
+    const int64_t glue_blocks = glue ? (int64_t)kGlueBlocks * (p.Op / 256) : 0;
+    hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)(kPrepBlocksX + kPrepBlocksW + glue_blocks)), dim3(256), 0, s,
+                       pa, ga);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "backward prep launch");
     const float* g = grad_out;
@@ -3028,16 +3225,17 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     const bool copies = bwd_may_use_copies(p, cs.exact, need_x);
     if (copies) {
         int* mode = reinterpret_cast<int*>(ws + p.off_mode);
-        hipLaunchKernelGGL(copy_mode_kernel, dim3(1), dim3(64), 0, s, ba.partials, ba.NP, kSplitRecords, mode);
         // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
         const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * (p.split ? 4 : 8);
         const dim3 agrid((unsigned)((problems + kAssignThreads - 1) / kAssignThreads));
         if (p.split)
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, agrid, dim3(kAssignThreads), 0, s,
-                               reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp, p.Op, kBwdCopyOffset);
+                               reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
+                               p.Kp, p.Op, kBwdCopyOffset);
         else
             hipLaunchKernelGGL(fwd_copy_assign_kernel<16>, agrid, dim3(kAssignThreads), 0, s,
-                               reinterpret_cast<float2*>(ws + p.off_wsT), mode, p.Kp, p.Op, kBwdCopyOffsetI);
+                               reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
+                               p.Kp, p.Op, kBwdCopyOffsetI);
         ba.copy_mode = mode;
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "backward copy assignment launch");
@@ -3053,27 +3251,40 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     err = hipGetLastError();
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "backward launch");
+    // dX and dVth reductions in one launch, with the glue sums unless they need the dX
+    // reduction's input-mapping partials (a second launch then follows)
+    DxReduceArgs dxa{};
+    int dx_blocks = 0;
     if (need_x) {
-        const float* aff = glue ? glue->in_affine : nullptr;
-        hipLaunchKernelGGL(dx_reduce_kernel, dim3(kDxReduceBlocks), dim3(256), 0, s,
-                           reinterpret_cast<const float*>(ws + p.off_dx), (p.halves ? 2 : 1) * p.n_ob, M * K, scale,
-                           grad_x, x, aff,
-                           glue ? glue->in_lo : 0.0f, glue ? glue->in_hi : 0.0f, aff_part);
-        err = hipGetLastError();
-        if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
+        dxa = DxReduceArgs{reinterpret_cast<const float*>(ws + p.off_dx), (p.halves ? 2 : 1) * p.n_ob, M * K, scale,
+                           grad_x, x, glue ? glue->in_affine : nullptr, glue ? glue->in_lo : 0.0f,
+                           glue ? glue->in_hi : 0.0f, aff_part, 0};
+        dx_blocks = dx_reduce_blocks(M * K);
     }
+    DvReduceArgs dva{};
+    int dv_blocks = 0;
     if (need_w) {
-        hipLaunchKernelGGL(dv_reduce_kernel, dim3(2048), dim3(256), 0, s, reinterpret_cast<const float*>(ws + p.off_dv),
-                           p.n_split, (int)K, (int)O, (int)p.Kp, (int)p.Op, scale, grad_vth_pos, grad_vth_neg);
-        err = hipGetLastError();
-        if (err != hipSuccess) return hip_fail(err, "dv reduce launch");
+        dva = DvReduceArgs{reinterpret_cast<const float*>(ws + p.off_dv), p.n_split, (int)K, (int)O, (int)p.Kp,
+                           (int)p.Op, scale, grad_vth_pos, grad_vth_neg};
+        dv_blocks = std::min(dv_reduce_tiles(K, O), 4096);
     }
+    GlueReduceArgs gra{};
+    int gl_blocks = 0;
     if (need_glue) {
-        hipLaunchKernelGGL(glue_reduce_kernel, dim3((unsigned)((O + 63) / 64 + 1)), dim3(256), 0, s, col_part, r_part, aff_part, O,
-                           p.Op, gg->adc_scale, gg->adc_shift, gg->r_tia, gg->in_affine);
-        err = hipGetLastError();
-        if (err != hipSuccess) return hip_fail(err, "glue reduce launch");
+        gra = GlueReduceArgs{col_part, r_part, aff_part, dx_blocks, O, p.Op, gg->adc_scale, gg->adc_shift,
+                             gg->r_tia, gg->in_affine, glue->r_tia, glue->r_log_scale, glue->r_log_lo,
+                             glue->r_log_hi, gg->r_log_scale};
+        gl_blocks = glue_reduce_blocks(O);
     }
+    const bool glue_after = gg && gg->in_affine;  // needs aff_part from the dX blocks
+    const int first_blocks = dx_blocks + dv_blocks + (glue_after ? 0 : gl_blocks);
+    if (first_blocks > 0)
+        hipLaunchKernelGGL(grad_reduce_kernel, dim3((unsigned)first_blocks), dim3(256), 0, s, dxa, dx_blocks, dva,
+                           dv_blocks, gra);
+    if (need_glue && glue_after)
+        hipLaunchKernelGGL(glue_reduce_kernel, dim3((unsigned)gl_blocks), dim3(256), 0, s, gra);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "gradient reduction launch");
     return 0;
 }
 
@@ -3083,11 +3294,16 @@ int check_glue(const isa_ekv_glue* glue, const isa_ekv_glue_grads* gg, bool need
     if (glue->adc_scale && !glue->adc_shift) return fail(ISA_EKV_EINVAL, "adc_scale needs adc_shift");
     if (glue->in_affine && !(glue->in_hi >= glue->in_lo)) return fail(ISA_EKV_EINVAL, "input range needs in_hi >= in_lo");
     if (glue->r_tia && !(glue->y_hi >= glue->y_lo)) return fail(ISA_EKV_EINVAL, "output range needs y_hi >= y_lo");
+    if (glue->r_log_scale && !glue->r_tia) return fail(ISA_EKV_EINVAL, "r_log_scale needs r_tia (the base gain)");
+    if (glue->r_log_scale && !(glue->r_log_hi >= glue->r_log_lo))
+        return fail(ISA_EKV_EINVAL, "log-gain range needs r_log_hi >= r_log_lo");
     if (gg) {
         if (gg->in_affine && !glue->in_affine) return fail(ISA_EKV_EINVAL, "input-mapping gradient without in_affine");
         if (gg->in_affine && !need_x)
             return fail(ISA_EKV_EINVAL, "the input-mapping gradient needs grad_x (it is formed from dX)");
         if (gg->r_tia && !glue->r_tia) return fail(ISA_EKV_EINVAL, "r_tia gradient without r_tia");
+        if (gg->r_log_scale && !glue->r_log_scale)
+            return fail(ISA_EKV_EINVAL, "r_log_scale gradient without r_log_scale");
         if ((gg->adc_scale || gg->adc_shift) && !glue->adc_scale)
             return fail(ISA_EKV_EINVAL, "ADC affine gradient without adc_scale/adc_shift");
     }
@@ -3244,7 +3460,7 @@ int run_measured_backward(const float* x, const short* ids_a, const short* ids_b
     if (err != hipSuccess) return hip_fail(err, "measured prep launch");
     float* col_part = reinterpret_cast<float*>(ws + p.off_glue);
     float* r_part = col_part + (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) / 4;
-    GlueGradArgs ga{grad_out, out_pre, M, O, p.Op, r_tia, out_min, out_max, nullptr,
+    GlueGradArgs ga{grad_out, out_pre, M, O, p.Op, r_tia, nullptr, 0.0f, 0.0f, out_min, out_max, nullptr,
                     reinterpret_cast<float*>(ws + p.off_gpad), col_part, r_part};
     hipLaunchKernelGGL(glue_grad_kernel, dim3(kGlueBlocks, (unsigned)(p.Op / 256)), dim3(256), 0, s, ga);
     err = hipGetLastError();
@@ -3283,10 +3499,9 @@ int run_measured_backward(const float* x, const short* ids_a, const short* ids_b
     err = hipGetLastError();
     prof_stop(s, prof);
     if (err != hipSuccess) return hip_fail(err, "measured backward launch");
-    hipLaunchKernelGGL(dx_reduce_kernel, dim3(kDxReduceBlocks), dim3(256), 0, s,
-                       reinterpret_cast<const float*>(ws + p.off_dx), p.n_ob, M * K, current_scale, grad_x, x,
-                       static_cast<const float*>(nullptr), cb->lookup_min, cb->lookup_max,
-                       static_cast<float2*>(nullptr), 1);
+    const DxReduceArgs dxa{reinterpret_cast<const float*>(ws + p.off_dx), p.n_ob, M * K, current_scale, grad_x, x,
+                           nullptr, cb->lookup_min, cb->lookup_max, nullptr, 1};
+    hipLaunchKernelGGL(dx_reduce_kernel, dim3((unsigned)dx_reduce_blocks(M * K)), dim3(256), 0, s, dxa);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "dx reduce launch");
     return 0;
@@ -3622,7 +3837,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
     int64_t v[ISA_EKV_PLAN_INFO_LEN];
     if (which == ISA_EKV_PLAN_FORWARD) {
         const FwdPlan p = plan_forward_call(false, n_entries, M, K, O);
-        const FwdTableCfg tc = fwd_table_cfg(n_entries, p.wpb);
+        const FwdTableCfg tc = fwd_table_cfg(n_entries, p.wpb, copies_pay(M, K, O));
         v[0] = (int64_t)p.bytes;
         v[1] = tc.copy_offset > 0 ? (int64_t)p.off_mode : -1;
         v[2] = p.n_split;
@@ -3644,6 +3859,13 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
         return fail(ISA_EKV_EINVAL, "unknown plan kind %d", which);
     }
     for (int i = 0; i < n_info; ++i) info[i] = i < ISA_EKV_PLAN_INFO_LEN ? v[i] : 0;
+    return 0;
+}
+
+int isa_ekv_set_option(int option, int64_t value, int64_t* previous) {
+    if (option != ISA_EKV_OPT_COPY_MIN_CELLS) return fail(ISA_EKV_EINVAL, "unknown option %d", option);
+    const int64_t old = value >= 0 ? g_copy_min_cells.exchange(value) : g_copy_min_cells.load();
+    if (previous) *previous = old;
     return 0;
 }
 

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -27,6 +27,7 @@ PLAN_BACKWARD = 1
 PLAN_LAYER_BACKWARD = 2
 PLAN_INFO_LEN = 7
 NOALLOC_MAX_BYTES = 64 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
+OPT_COPY_MIN_CELLS = 1
 
 EXPORTS = (
     "isa_ekv_abi_version",
@@ -56,6 +57,7 @@ EXPORTS = (
     "isa_ekv_profile_end",
     "isa_ekv_probe_lds_gather",
     "isa_ekv_plan_info",
+    "isa_ekv_set_option",
 )
 
 _lock = threading.Lock()
@@ -80,6 +82,9 @@ class Glue(ctypes.Structure):
         ("adc_shift", ctypes.c_void_p),
         ("stat_abs_max", ctypes.c_void_p),
         ("stat_total", ctypes.c_void_p),
+        ("r_log_scale", ctypes.c_void_p),
+        ("r_log_lo", ctypes.c_float),
+        ("r_log_hi", ctypes.c_float),
     ]
 
 
@@ -113,6 +118,7 @@ class GlueGrads(ctypes.Structure):
         ("r_tia", ctypes.c_void_p),
         ("adc_scale", ctypes.c_void_p),
         ("adc_shift", ctypes.c_void_p),
+        ("r_log_scale", ctypes.c_void_p),
     ]
 
 
@@ -182,6 +188,8 @@ def _declare(lib) -> None:
     lib.isa_ekv_probe_lds_gather.restype = ci
     lib.isa_ekv_plan_info.argtypes = [ci, i64, i64, i64, ci, ci, ci, ctypes.POINTER(i64), ci]
     lib.isa_ekv_plan_info.restype = ci
+    lib.isa_ekv_set_option.argtypes = [ci, i64, ctypes.POINTER(i64)]
+    lib.isa_ekv_set_option.restype = ci
 
 
 def load(path: Path | None = None):
@@ -234,5 +242,35 @@ class KernelTimer:
         return False
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The hipStream_t of the device's current stream (the raw handle without building a
+    torch.cuda.Stream object where torch offers it: a few microseconds per call)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class on_device:
+    """torch.cuda.device(device) that skips the device switch when it is already current."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, device):
+        device = device if isinstance(device, torch.device) else torch.device(device)
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = -1
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.index:
+            self.prev = cur
+            torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev >= 0:
+            torch.cuda.set_device(self.prev)
+        return False

@@ -38,14 +38,16 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def _workspace(nbytes: int, device: torch.device, given: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """The call's workspace: `given` (a caller's uint8 device buffer, checked) or a new one."""
+    """The call's workspace: `given` (a caller's uint8 device buffer, checked) or a new one of
+    `nbytes` (the workspace query's bound). A given buffer's size is checked by the library
+    against the call's own plan (plan_info's workspace_bytes), which the bound may exceed."""
     if given is None:
         return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
     _require_cuda(given, "workspace")
     if given.dtype != torch.uint8 or not given.is_contiguous() or given.device != device:
         raise RuntimeError(f"workspace must be a contiguous uint8 tensor on {device}")
-    if given.numel() < nbytes or given.data_ptr() % 256:
-        raise RuntimeError(f"workspace needs {int(nbytes)} bytes at a 256-byte aligned address")
+    if given.data_ptr() % 256:
+        raise RuntimeError("workspace must start at a 256-byte aligned address")
     return given
 
 
@@ -68,6 +70,16 @@ def plan_info(kind: str, M: int, K: int, O: int, n_entries: int, need_grad_x: bo
     return dict(zip(keys, (int(v) for v in info)))
 
 
+def copy_min_cells(value: Optional[int] = None) -> int:
+    """The library's ISA_EKV_OPT_COPY_MIN_CELLS (calls of fewer cells M*K*O run one table
+    copy); sets it when value is given. Returns the value before the call."""
+    lib = _hip.load()
+    prev = ctypes.c_int64()
+    rc = lib.isa_ekv_set_option(_hip.OPT_COPY_MIN_CELLS, -1 if value is None else int(value), ctypes.byref(prev))
+    _hip.check(rc, "isa_ekv_set_option")
+    return int(prev.value)
+
+
 def copy_mode(workspace: torch.Tensor, plan: dict) -> Optional[int]:
     """After a call that used `workspace` (and synchronised), whether its main kernel ran with
     the second table copy (1) or one copy (0); None when the plan has no second copy."""
@@ -85,7 +97,7 @@ def build_plain_tables(params: Tuple[float, float, float, float], delta_min: flo
     layout = _hip.LUT_PLAIN_BF16 if bf16 else _hip.LUT_PLAIN_F32
     buf = torch.empty(2 * size, dtype=dtype, device=device)
     arr = (ctypes.c_double * 4)(*[float(v) for v in params])
-    with torch.cuda.device(device):
+    with _hip.on_device(device):
         rc = lib.isa_ekv_lut_build(arr, float(delta_min), float(delta_max), int(size), layout, buf.data_ptr(),
                                    _hip.stream_handle(device))
     _hip.check(rc, "isa_ekv_lut_build")
@@ -108,7 +120,7 @@ def pack_tables(table_i: torch.Tensor, table_ddelta: Optional[torch.Tensor], lay
         raise RuntimeError("table_i and table_ddelta must have the same LUT_DELTA_SIZE")
     out = torch.empty(lib.isa_ekv_lut_bytes(n, layout), dtype=torch.uint8, device=table_i.device)
     dtype_code = 1 if src == _hip.LUT_PLAIN_BF16 else 0
-    with torch.cuda.device(table_i.device):
+    with _hip.on_device(table_i.device):
         rc = lib.isa_ekv_lut_pack(table_i.data_ptr(), table_ddelta.data_ptr(), n, dtype_code, layout,
                                   out.data_ptr(), _hip.stream_handle(table_i.device))
     _hip.check(rc, "isa_ekv_lut_pack")
@@ -145,7 +157,7 @@ def lut_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, fwd_rec
     x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
     ws_bytes = lib.isa_ekv_forward_workspace(M, K, O)
     ws = _workspace(ws_bytes, dev, workspace)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), fwd_records.data_ptr(), M, K, O,
                                  int(n_entries), float(delta_min), float(delta_max), float(v_sat),
                                  float(out_min), float(out_max), out.data_ptr(), ws.data_ptr(), ws.numel(),
@@ -172,7 +184,7 @@ def lut_forward_noalloc(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor,
     if n_entries > MAX_ENTRIES:
         raise RuntimeError(f"LUT forward supports LUT_DELTA_SIZE <= {MAX_ENTRIES}")
     dev = x.device
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_forward_noalloc(_ptr(x), _ptr(wpos), _ptr(wneg), fwd_records.data_ptr(), M, K, O,
                                          int(n_entries), float(delta_min), float(delta_max), float(v_sat),
                                          float(out_min), float(out_max), out.data_ptr(), _hip.stream_handle(dev))
@@ -200,7 +212,7 @@ def lut_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad_o
     x32, wp32, wn32, g32 = (as_kernel_f32(t) for t in (x, wpos, wneg, grad_out))
     ws_bytes = lib.isa_ekv_backward_workspace(M, K, O, int(n_entries), int(need_grad_x), int(need_grad_w))
     ws = _workspace(ws_bytes, dev, workspace)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_backward(_ptr(x32), _ptr(wp32), _ptr(wn32), _ptr(g32), bwd_records.data_ptr(), M, K, O,
                                   int(n_entries), float(delta_min), float(delta_max), float(v_sat),
                                   _ptr(gx), _ptr(gp), _ptr(gn), ws.data_ptr(), ws.numel(),
@@ -225,7 +237,7 @@ def exact_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor,
         return out
     x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
     ws = _workspace(lib.isa_ekv_exact_forward_workspace(M, K, O), dev)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_exact_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), M, K, O, _exact_params(params),
                                        float(v_sat), out.data_ptr(), ws.data_ptr(), ws.numel(),
                                        _hip.stream_handle(dev))
@@ -249,7 +261,7 @@ def exact_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad
         return gx, gp, gn
     x32, wp32, wn32, g32 = (as_kernel_f32(t) for t in (x, wpos, wneg, grad_out))
     ws = _workspace(lib.isa_ekv_exact_backward_workspace(M, K, O, int(need_grad_x), int(need_grad_w)), dev)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_exact_backward(_ptr(x32), _ptr(wp32), _ptr(wn32), _ptr(g32), M, K, O,
                                         _exact_params(params), float(v_sat), _ptr(gx), _ptr(gp), _ptr(gn),
                                         ws.data_ptr(), ws.numel(), _hip.stream_handle(dev))
@@ -258,7 +270,7 @@ def exact_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, grad
 
 
 def _glue_struct(in_affine, in_range, r_tia, y_range, adc_scale, adc_shift, stat_abs_max=None,
-                 stat_total=None) -> "_hip.Glue":
+                 stat_total=None, r_log_scale=None, r_log_range=(0.0, 0.0)) -> "_hip.Glue":
     g = _hip.Glue()
     g.in_affine = _ptr(in_affine)
     g.in_lo, g.in_hi = (float(v) for v in in_range)
@@ -268,6 +280,8 @@ def _glue_struct(in_affine, in_range, r_tia, y_range, adc_scale, adc_shift, stat
     g.adc_shift = _ptr(adc_shift)
     g.stat_abs_max = _ptr(stat_abs_max)
     g.stat_total = _ptr(stat_total)
+    g.r_log_scale = _ptr(r_log_scale)
+    g.r_log_lo, g.r_log_hi = (float(v) for v in r_log_range)
     return g
 
 
@@ -299,12 +313,15 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
                       r_tia: Optional[torch.Tensor] = None, y_range=(-4.0, 4.0),
                       adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None,
                       stat_abs_max: Optional[torch.Tensor] = None, stat_total: Optional[torch.Tensor] = None,
+                      r_log_scale: Optional[torch.Tensor] = None, r_log_range=(-2.0, 2.0),
                       workspace: Optional[torch.Tensor] = None):
     """(out, idiff) of the LUT projection with its glue fused: x -> clamp(x*s + b) ->
-    Idiff (clamped to [idiff_min, idiff_max]) -> y = clamp(Idiff * r_tia) -> y * adc_scale +
-    adc_shift. stat_abs_max (fp32) and stat_total (fp64), one element each, are CIMLinear's
-    output statistics (cim.py:194-198), updated in place: maximum with max|y|, plus M * O.
-    workspace: optional caller buffer."""
+    Idiff (clamped to [idiff_min, idiff_max]) -> y = clamp(Idiff * r) -> y * adc_scale +
+    adc_shift, with the gain r = r_tia, or r_tia * exp(clamp(r_log_scale, *r_log_range)) when
+    r_log_scale is given (CIMLinear's r_tia_base and learnable log scale). stat_abs_max (fp32)
+    and stat_total (fp64), one element each, are CIMLinear's output statistics
+    (cim.py:194-198), updated in place: maximum with max|y|, plus M * O. workspace: optional
+    caller buffer."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
     if n_entries > MAX_ENTRIES:
@@ -312,6 +329,9 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
     dev = x.device
     aff = _glue_operand(in_affine, 2, "in_affine", dev)
     r = _glue_operand(r_tia, 1, "r_tia", dev)
+    r_ls = _glue_operand(r_log_scale, 1, "r_log_scale", dev)
+    if r_ls is not None and r is None:
+        raise RuntimeError("r_log_scale needs r_tia (the base gain)")
     a_s = _glue_operand(adc_scale, O, "adc_scale", dev)
     a_c = _glue_operand(adc_shift, O, "adc_shift", dev)
     if (a_s is None) != (a_c is None):
@@ -323,9 +343,9 @@ def lut_layer_forward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, f
     if M == 0 or O == 0:
         return out, idiff
     x32, wp32, wn32 = as_kernel_f32(x), as_kernel_f32(wpos), as_kernel_f32(wneg)
-    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c, s_max, s_tot)
+    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c, s_max, s_tot, r_ls, r_log_range)
     ws = _workspace(lib.isa_ekv_layer_forward_workspace(M, K, O), dev, workspace)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_layer_forward(_ptr(x32), _ptr(wp32), _ptr(wn32), fwd_records.data_ptr(), M, K, O,
                                        int(n_entries), float(delta_min), float(delta_max), float(v_sat),
                                        float(idiff_min), float(idiff_max), ctypes.byref(glue), idiff.data_ptr(),
@@ -341,10 +361,11 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
                        r_tia: Optional[torch.Tensor] = None, y_range=(-4.0, 4.0),
                        adc_scale: Optional[torch.Tensor] = None, adc_shift: Optional[torch.Tensor] = None,
                        need_in_affine: bool = False, need_r_tia: bool = False, need_adc: bool = False,
-                       workspace: Optional[torch.Tensor] = None):
+                       r_log_scale: Optional[torch.Tensor] = None, r_log_range=(-2.0, 2.0),
+                       need_r_log_scale: bool = False, workspace: Optional[torch.Tensor] = None):
     """Gradients of lut_layer_forward's out: dict with dx, dvth_pos, dvth_neg, d_in_affine,
-    d_r_tia, d_adc_scale, d_adc_shift (None where not requested), all fp32. workspace:
-    optional caller buffer."""
+    d_r_tia (for the gain r), d_r_log_scale, d_adc_scale, d_adc_shift (None where not
+    requested), all fp32. workspace: optional caller buffer."""
     lib = _hip.load()
     M, K, O = _check_operands(x, wpos, wneg)
     _require_cuda(grad_out, "grad_out")
@@ -355,6 +376,9 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
     dev = x.device
     aff = _glue_operand(in_affine, 2, "in_affine", dev)
     r = _glue_operand(r_tia, 1, "r_tia", dev)
+    r_ls = _glue_operand(r_log_scale, 1, "r_log_scale", dev)
+    if r_ls is not None and r is None:
+        raise RuntimeError("r_log_scale needs r_tia (the base gain)")
     a_s = _glue_operand(adc_scale, O, "adc_scale", dev)
     a_c = _glue_operand(adc_shift, O, "adc_shift", dev)
     need_in_affine = need_in_affine and aff is not None
@@ -366,6 +390,7 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
         "dvth_neg": torch.empty((O, K), **f32) if need_grad_w else None,
         "d_in_affine": torch.empty(2, **f32) if need_in_affine else None,
         "d_r_tia": torch.empty(1, **f32) if (need_r_tia and r is not None) else None,
+        "d_r_log_scale": torch.empty(1, **f32) if (need_r_log_scale and r_ls is not None) else None,
         "d_adc_scale": torch.empty(O, **f32) if (need_adc and a_s is not None) else None,
         "d_adc_shift": torch.empty(O, **f32) if (need_adc and a_s is not None) else None,
     }
@@ -374,13 +399,14 @@ def lut_layer_backward(x: torch.Tensor, wpos: torch.Tensor, wneg: torch.Tensor, 
     grads.r_tia = _ptr(res["d_r_tia"])
     grads.adc_scale = _ptr(res["d_adc_scale"])
     grads.adc_shift = _ptr(res["d_adc_shift"])
-    if not (need_x or need_grad_w or any(res[k] is not None for k in ("d_r_tia", "d_adc_scale"))):
+    grads.r_log_scale = _ptr(res["d_r_log_scale"])
+    if not (need_x or need_grad_w or any(res[k] is not None for k in ("d_r_tia", "d_r_log_scale", "d_adc_scale"))):
         return res
     x32, wp32, wn32, g32, id32 = (as_kernel_f32(t) for t in (x, wpos, wneg, grad_out, idiff))
-    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c)
+    glue = _glue_struct(aff, in_range, r, y_range, a_s, a_c, r_log_scale=r_ls, r_log_range=r_log_range)
     ws = _workspace(lib.isa_ekv_layer_backward_workspace(M, K, O, int(n_entries), int(need_x), int(need_grad_w)), dev,
                     workspace)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_layer_backward(_ptr(x32), _ptr(wp32), _ptr(wn32), _ptr(g32), _ptr(id32),
                                         bwd_records.data_ptr(), M, K, O, int(n_entries), float(delta_min),
                                         float(delta_max), float(v_sat), ctypes.byref(glue), _ptr(res["dx"]),
@@ -451,7 +477,7 @@ def measured_forward(x: torch.Tensor, ids_a: torch.Tensor, ids_b: Optional[torch
         return out, pre
     x32 = as_kernel_f32(x)
     ws = _workspace(lib.isa_ekv_measured_forward_workspace(M, K, O, cb.n_seg, cb.n_rows), dev)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_measured_forward(_ptr(x32), a16.data_ptr(), _ptr(b16), M, K, O, ctypes.byref(cb),
                                           float(current_scale), r.data_ptr(), float(out_min), float(out_max),
                                           pre.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
@@ -480,7 +506,7 @@ def measured_backward(x: torch.Tensor, ids_a: torch.Tensor, ids_b: Optional[torc
     gx = torch.empty((M, K), dtype=torch.float32, device=dev)
     x32, g32, p32 = as_kernel_f32(x), as_kernel_f32(grad_out), as_kernel_f32(out_pre)
     ws = _workspace(lib.isa_ekv_measured_backward_workspace(M, K, O, cb.n_seg, cb.n_rows), dev)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         rc = lib.isa_ekv_measured_backward(_ptr(x32), a16.data_ptr(), _ptr(b16), M, K, O, ctypes.byref(cb),
                                            float(current_scale), _ptr(g32), _ptr(p32), r.data_ptr(),
                                            float(out_min), float(out_max), gx.data_ptr(), ws.data_ptr(), ws.numel(),
@@ -505,7 +531,7 @@ def probe_lds_gather(window_records: int, record_bytes: int = 8, iterations: int
     clocks = torch.zeros((repeats, 2 * cus, 2), dtype=torch.int64, device=dev)
     per_cu = ctypes.c_int(0)
     khz = ctypes.c_int(0)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         stream = _hip.stream_handle(dev)
 
         def launch(slot):

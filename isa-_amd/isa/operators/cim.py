@@ -187,8 +187,12 @@ class CIMLinear(nn.Module):
         assert in_f == self.in_features
         flat = x.reshape(b * n, in_f)
         stats = (self._stat_abs_max, self._stat_total) if self.track_output_stats else None
+        # the gain r_tia_base * exp(clamp(r_tia_log_scale)) (the r_tia property) is formed in
+        # the library, which returns the log scale's gradient
+        lo = float(self.cfg.get("R_TIA_LOG_SCALE_MIN", -2.0))
+        hi = float(self.cfg.get("R_TIA_LOG_SCALE_MAX", 2.0))
         out = fused_cim_layer(flat, self.vth_pos, self.vth_neg, self.cfg, in_affine=in_affine, in_range=in_range,
-                              r_tia=self.r_tia.to(device=x.device, dtype=torch.float32).reshape(1),
+                              r_tia=self.r_tia_base, r_log_scale=self.r_tia_log_scale, r_log_range=(lo, hi),
                               adc_scale=adc_scale, adc_shift=adc_shift, stats=stats)
         return out.reshape(b, n, self.out_features)
 

@@ -147,6 +147,12 @@ def test_layer_entry_points_reject_bad_glue_before_launch():
     g.r_tia, g.y_lo, g.y_hi = 16, 4.0, -4.0
     assert fwd(ctypes.byref(g)) == -1 and "y_hi" in _err(lib)
     g = _hip.Glue()
+    g.r_log_scale, g.r_log_lo, g.r_log_hi = 16, -2.0, 2.0
+    assert fwd(ctypes.byref(g)) == -1 and "needs r_tia" in _err(lib)
+    g.r_tia, g.y_lo, g.y_hi = 16, -4.0, 4.0
+    g.r_log_lo, g.r_log_hi = 2.0, -2.0
+    assert fwd(ctypes.byref(g)) == -1 and "r_log_hi" in _err(lib)
+    g = _hip.Glue()
     assert fwd(ctypes.byref(g)) == -1 and "workspace too small" in _err(lib)
 
     def bwd(glue, grads, gx=fake, idiff=fake):
@@ -157,6 +163,11 @@ def test_layer_entry_points_reject_bad_glue_before_launch():
     gg = _hip.GlueGrads()
     gg.r_tia = 16
     assert bwd(ctypes.byref(g), ctypes.byref(gg)) == -1 and "r_tia gradient without r_tia" in _err(lib)
+    g.r_tia, g.y_lo, g.y_hi = 16, -4.0, 4.0
+    gg = _hip.GlueGrads()
+    gg.r_log_scale = 16
+    assert bwd(ctypes.byref(g), ctypes.byref(gg)) == -1 and "r_log_scale gradient without" in _err(lib)
+    g = _hip.Glue()
     g.in_affine, g.in_lo, g.in_hi = 16, 0.0, 4.0
     gg = _hip.GlueGrads()
     gg.in_affine = 16
@@ -243,7 +254,8 @@ def test_plan_info_reports_the_call_plans():
     # 8192 entries, 768 inputs per wave: both copies in one 16-wave block per CU
     f8 = ops.plan_info("forward", 8192, 768, 3072, 8192)
     assert f8["waves_per_block"] == 16 and f8["mode_offset"] >= 0
-    # 16384 entries: one LDS copy in the forward, global-memory backward, no mode word
+    # 16384 entries: one LDS copy in the forward, two half-table passes in the backward, no
+    # mode word
     assert ops.plan_info("forward", 8192, 768, 3072, 16384)["mode_offset"] == -1
     assert ops.plan_info("backward", 8192, 768, 3072, 16384)["mode_offset"] == -1
     # a dVth-only backward runs no copy pair
@@ -251,3 +263,30 @@ def test_plan_info_reports_the_call_plans():
     info = (ctypes.c_int64 * 7)()
     assert lib.isa_ekv_plan_info(9, 1, 1, 1, 4096, 1, 1, info, 7) == -1 and "plan kind" in _err(lib)
     assert lib.isa_ekv_plan_info(0, 1, 1, 1, 0, 1, 1, info, 7) == -1 and "LUT_DELTA_SIZE" in _err(lib)
+
+
+def test_small_calls_plan_one_table_copy_and_one_round():
+    """Calls below ISA_EKV_OPT_COPY_MIN_CELLS (default 2^28 cells) plan no second table copy;
+    isa_ekv_set_option moves the threshold. Small plans keep to one round of blocks."""
+    from isa.kernels.transformer_ffn import ops
+
+    lib = _hip.load()
+    prev = ops.copy_min_cells()
+    assert prev == 1 << 28
+    shape = (520, 192, 768, 4096)  # the ViT-S up-projection: 7.7e7 cells
+    assert ops.plan_info("forward", *shape)["mode_offset"] == -1
+    assert ops.plan_info("layer_backward", *shape)["mode_offset"] == -1
+    try:
+        assert ops.copy_min_cells(0) == 1 << 28
+        assert ops.plan_info("forward", *shape)["mode_offset"] >= 0
+        assert ops.plan_info("backward", *shape)["mode_offset"] >= 0
+    finally:
+        ops.copy_min_cells(prev)
+    assert ops.copy_min_cells() == prev
+    for kind in ("forward", "backward", "layer_backward"):
+        for m, k, o in ((520, 192, 768), (520, 768, 192), (64, 200, 300)):
+            plan = ops.plan_info(kind, m, k, o, 4096)
+            per_cu = 2 if plan["waves_per_block"] * 64 * 2 <= 2048 else 1
+            assert plan["blocks"] <= per_cu * 256, (kind, m, k, o, plan)
+    assert lib.isa_ekv_set_option(7, 0, None) == -1 and "option" in _err(lib)
+

@@ -59,7 +59,7 @@ def test_cimlinear_parameters_and_init():
     sd = layer.state_dict()
     assert set(sd) == {"vth_pos", "vth_neg", "r_tia_base", "r_tia_log_scale"}
     assert layer.vth_pos.shape == (40, 24) and layer.vth_neg.shape == (40, 24)
-    assert float(layer.r_tia) == pytest.approx(1e5)
+    assert float(layer.r_tia.detach()) == pytest.approx(1e5)
     eps = 0.5 * 2.0 * cfg["n"] * cfg["U_T"]
     torch.manual_seed(0)
     ref_p = torch.empty(40, 24).uniform_(-eps, eps).add_(2.5)
@@ -70,9 +70,9 @@ def test_cimlinear_parameters_and_init():
         layer.r_tia_log_scale.fill_(5.0)
     layer.clamp_vth()
     assert float(layer.vth_pos.max()) == 5.0
-    assert float(layer.r_tia) == pytest.approx(1e5 * torch.exp(torch.tensor(2.0)).item(), rel=1e-6)
+    assert float(layer.r_tia.detach()) == pytest.approx(1e5 * torch.exp(torch.tensor(2.0)).item(), rel=1e-6)
     layer.set_r_tia(3e4)
-    assert float(layer.r_tia) == pytest.approx(3e4)
+    assert float(layer.r_tia.detach()) == pytest.approx(3e4)
     layer.reset_vth(center=1.0, eps_k=0.5, symmetric=True, mode="centered_symmetric")
     assert torch.allclose(layer.vth_pos + layer.vth_neg, torch.full_like(layer.vth_pos, 2.0), atol=1e-6)
 

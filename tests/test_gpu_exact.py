@@ -188,7 +188,7 @@ def test_cimlinear_exact_dispatch(cuda_device):
     X = x.detach().double().cpu().reshape(-1, 48)
     wp, wn = layer.vth_pos.detach().double().cpu(), layer.vth_neg.detach().double().cpu()
     idiff = exact.diff_current_f64(X, wp, wn, cfg).numpy()
-    r = float(layer.r_tia)
+    r = float(layer.r_tia.detach())
     pre = idiff * r
     ref = np.clip(pre, -4.0, 4.0)
     assert oracle.normwise_error(out.detach().double().cpu().numpy().reshape(-1, 96), ref) <= FWD_TOL

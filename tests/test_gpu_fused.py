@@ -47,7 +47,7 @@ def _compare(a, b, exact_names):
             assert torch.allclose(ga[name], gb[name], rtol=1e-3, atol=1e-5 * float(gb[name].abs().max()) + 1e-30), name
 
 
-@pytest.mark.parametrize("log_scale", [0.3, 1.6])  # 1.6 drives many outputs into both clamps
+@pytest.mark.parametrize("log_scale", [0.3, 1.6, 2.5])  # 1.6: many outputs in both clamps; 2.5: past the log-scale clamp
 def test_physical_ffn_fused_equals_unfused(cuda_device, log_scale):
     from isa.operators.cim import PhysicalFFN
 
@@ -71,6 +71,10 @@ def test_physical_ffn_fused_equals_unfused(cuda_device, log_scale):
     for name in ("input_mapping.scale", "input_mapping.shift", "fc1.r_tia_log_scale", "fc2.r_tia_log_scale",
                  "adc_affine_scale", "adc_affine_shift"):
         assert name in fused[1], name
+    if log_scale > 2.0:  # past R_TIA_LOG_SCALE_MAX: the clamp passes no gradient
+        assert float(fused[1]["fc1.r_tia_log_scale"]) == 0.0
+    else:
+        assert float(fused[1]["fc1.r_tia_log_scale"]) != 0.0
 
 
 def test_hybrid_ffn_and_cimlinear_fused_equal_unfused(cuda_device):

@@ -53,7 +53,7 @@ def test_physical_ffn_autograd(cuda_device):
     s, b = float(ffn.input_mapping.scale.detach()), float(ffn.input_mapping.shift.detach())
     pre0 = X * s + b
     v = np.clip(pre0, 0.0, 4.0)
-    r1, r2 = float(ffn.fc1.r_tia), float(ffn.fc2.r_tia)
+    r1, r2 = float(ffn.fc1.r_tia.detach()), float(ffn.fc2.r_tia.detach())
     W1p, W1n, W2p, W2n = (_np(t) for t in (ffn.fc1.vth_pos, ffn.fc1.vth_neg, ffn.fc2.vth_pos, ffn.fc2.vth_neg))
     i1 = _oracle_layer(v.astype(np.float32), W1p, W1n, cfg)
     h = np.clip(i1 * r1, -4.0, 4.0)
@@ -98,7 +98,7 @@ def test_hybrid_ffn_autograd(cuda_device):
     out.backward(g)
     X = _np(x).reshape(-1, D)
     v = np.clip(X, 0.0, 4.0)
-    r1 = float(ffn.fc1.r_tia)
+    r1 = float(ffn.fc1.r_tia.detach())
     W1p, W1n = _np(ffn.fc1.vth_pos), _np(ffn.fc1.vth_neg)
     i1 = _oracle_layer(v.astype(np.float32), W1p, W1n, cfg)
     h = np.clip(i1 * r1, -4.0, 4.0)

@@ -21,6 +21,18 @@ FWD_TOL = 1e-4
 BWD_TOL = 1e-3
 
 
+@pytest.fixture(autouse=True)
+def _small_calls_consider_table_copies():
+    """The shapes here are far below the library's copy threshold (ISA_EKV_OPT_COPY_MIN_CELLS):
+    let them take the second table copy as large calls do, so that its kernels are checked
+    against the oracle."""
+    from isa.kernels.transformer_ffn import ops
+
+    prev = ops.copy_min_cells(0)
+    yield
+    ops.copy_min_cells(prev)
+
+
 def _dev_run(x, vp, vn, grad, cfg, dev, need_x=True, need_w=True, out_min=-4.0, out_max=4.0, modes=None):
     """Forward and backward through the C ABI. modes: a dict that receives the table-copy mode
     each main kernel ran in ("fwd", "bwd": 1 two copies, 0 one copy, None no second copy)."""
