@@ -105,6 +105,9 @@ constexpr int kMaxEntriesGlobal = 1 << 22;
 #ifndef ISA_EKV_BWD_MIN_BLOCKS
 #define ISA_EKV_BWD_MIN_BLOCKS 2  // table-backward blocks per CU the VGPR budget is held to (64 VGPRs at 2)
 #endif
+// The waves per SIMD that budget means for 16-wave blocks (the second __launch_bounds__
+// argument is waves per SIMD, which caps the VGPRs at 512 / that many)
+constexpr int kBwdWavesPerEU = ISA_EKV_BWD_MIN_BLOCKS * 16 / 4;
 #ifndef ISA_EKV_BWD_LANE_RED
 #define ISA_EKV_BWD_LANE_RED 1  // dX reduction: 0 LDS buffers, 1 lane exchanges, 2 lane exchanges when the table crowds LDS
 #endif
@@ -517,24 +520,58 @@ __device__ inline void prep_block(const PrepArgs& a, int b) {
 
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) { prep_block(a, blockIdx.x); }
 
+// Copies elements [0, n) of src into LDS through store(i, value), the block's threads taking
+// every blockDim.x-th element and issuing BATCH loads before their stores (a strided loop that
+// stores each load before issuing the next waits out one memory latency per element).
+template <int BATCH, typename T, typename Store>
+__device__ inline void stage_to_lds(const T* __restrict__ src, int n, Store store) {
+    for (int base = threadIdx.x; base < n; base += BATCH * (int)blockDim.x) {
+        T v[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const int i = base + j * (int)blockDim.x;
+            if (i < n) v[j] = src[i];
+        }
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const int i = base + j * (int)blockDim.x;
+            if (i < n) store(i, v[j]);
+        }
+    }
+}
+
 // Range of the prep kernel's coordinates: token side (xlo, xhi), threshold side (wlo, whi),
 // wave-uniform.
 struct CoordRange {
     float xlo, xhi, wlo, whi;
 };
 
+// Every lane issues its loads (16-byte pairs of partials) in two rounds of five, each round's
+// before its first use: two memory latencies per call, where a loop that consumes each load
+// before the next waits out twenty, at 20 VGPRs.
 __device__ inline CoordRange read_coord_range(const float2* __restrict__ partials) {
+    static_assert(kPrepBlocksX % 256 == 0 && kPrepBlocksW % 256 == 0, "two rounds of 16-byte pairs per lane");
+    constexpr int NX = kPrepBlocksX / 256, NW = kPrepBlocksW / 256;  // loads per lane and round
     const int lane = threadIdx.x & 63;
+    const float4* p4 = reinterpret_cast<const float4*>(partials);  // 256-byte aligned workspace slot
     float xlo = INFINITY, xhi = -INFINITY, wlo = INFINITY, whi = -INFINITY;
-    for (int i = lane; i < kPrepBlocksX; i += 64) {
-        const float2 p = partials[i];
-        xlo = fminf(xlo, p.x);
-        xhi = fmaxf(xhi, p.y);
-    }
-    for (int i = lane; i < kPrepBlocksW; i += 64) {
-        const float2 p = partials[kPrepBlocksX + i];
-        wlo = fminf(wlo, p.x);
-        whi = fmaxf(whi, p.y);
+#pragma unroll
+    for (int round = 0; round < 2; ++round) {
+        float4 px[NX], pw[NW];
+#pragma unroll
+        for (int j = 0; j < NX; ++j) px[j] = p4[lane + 64 * (round * NX + j)];
+#pragma unroll
+        for (int j = 0; j < NW; ++j) pw[j] = p4[kPrepBlocksX / 2 + lane + 64 * (round * NW + j)];
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            xlo = fminf(xlo, fminf(px[j].x, px[j].z));
+            xhi = fmaxf(xhi, fmaxf(px[j].y, px[j].w));
+        }
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            wlo = fminf(wlo, fminf(pw[j].x, pw[j].z));
+            whi = fmaxf(whi, fmaxf(pw[j].y, pw[j].w));
+        }
     }
     for (int off = 32; off > 0; off >>= 1) {
         xlo = fminf(xlo, __shfl_xor(xlo, off));
@@ -1107,14 +1144,23 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
     }
 }
 
+// The whole table (float2 records) into LDS, two records per 16-byte load when n is even.
+__device__ inline void stage_table2(float2* dst, const float2* __restrict__ src, int n) {
+    if ((n & 1) == 0) {
+        float4* d4 = reinterpret_cast<float4*>(dst);
+        stage_to_lds<8>(reinterpret_cast<const float4*>(src), n / 2, [&](int i, float4 v) { d4[i] = v; });
+    } else {
+        stage_to_lds<8>(src, n, [&](int i, float2 v) { dst[i] = v; });
+    }
+}
+
 // WIN: the launch may hold two copies of only the coordinate window (tables whose two full
 // copies do not fit); the range is then read before the table load. Without WIN the load
 // comes first (reading the range first costs the 4096-entry kernels ~1%).
 template <int MR, bool SPLITS, bool WIN = false>
 __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
-    if constexpr (!WIN)
-        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
+    if constexpr (!WIN) stage_table2(s_lut_fwd, a.lut, a.NP);
     // fast loop and copy mode from one read of the range partials (as coords_in_padded_range,
     // fwd_copies_mode and launch_copy_mode decide them; a second read costs the main loop
     // ~50 VGPRs)
@@ -1130,16 +1176,15 @@ __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
             copies = n_rec <= a.copy_window;
             if (!copies) lo = 0, n_rec = a.NP;
         }
-        if (!copies)
-            for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_lut_fwd[i] = a.lut[i];
+        if (!copies) stage_table2(s_lut_fwd, a.lut, a.NP);
     }
     if (copies) {  // record i of copy 1 holds {A - T1 dT, dT}: fma(c + T1, dT, A') = fma(c, dT, A)
         const float t1 = (float)a.copy_offset;
-        for (int i = threadIdx.x; i < n_rec; i += blockDim.x) {
-            const float2 r = a.lut[lo + i];
+        const int t1i = a.copy_offset;
+        stage_to_lds<8>(a.lut + lo, n_rec, [&](int i, float2 r) {
             if constexpr (WIN) s_lut_fwd[i] = r;
-            s_lut_fwd[a.copy_offset + i] = make_float2(fmaf(-t1, r.y, r.x), r.y);
-        }
+            s_lut_fwd[t1i + i] = make_float2(fmaf(-t1, r.y, r.x), r.y);
+        });
     }
     __syncthreads();
     FwdTile t;
@@ -1460,8 +1505,8 @@ constexpr int kBwdCopyOffsetI = kSplitRecords + 8;
 constexpr size_t kBwdTwoCopiesLds = (size_t)(kBwdCopyOffset + 2 * kSplitRecords) * 8;
 constexpr size_t kBwdTwoCopiesLdsI = (size_t)(kBwdCopyOffsetI + kSplitRecords) * 16;
 
-template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false, int MODE = kBwdAlone>
-__global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdArgs a) {
+template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED, int MODE>
+__device__ inline void bwd_table_body(const BwdArgs& a) {
     static_assert(kSplitRecords % 16 == 0 && kBwdCopyOffsetI % 16 == 8, "copy 1 eight bank quads away");
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
@@ -1481,8 +1526,7 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
     }
     if constexpr (MODE == kBwdOneCopy && !SPLIT)
         if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
-    for (int i = threadIdx.x; i < n_rec; i += blockDim.x) {
-        const float4 rec = a.lut[lo + i];
+    stage_to_lds<8>(a.lut + lo, n_rec, [&](int i, float4 rec) {
         if constexpr (SPLIT) {
             s_split[i] = make_float2(rec.x, rec.y);
             s_split[i + kSplitRecords] = make_float2(rec.z, rec.w);
@@ -1499,7 +1543,8 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
                     make_float4(fmaf(-t1, rec.y, rec.x), rec.y, fmaf(-t1, rec.w, rec.z), rec.w);
             }
         }
-    }
+    });
+    __builtin_amdgcn_sched_barrier(0);  // the range loads after the table loads (VGPRs: one set live)
     const bool fast = coords_in_padded_range(a.partials, a.NP);
     if constexpr (MODE == kBwdOneCopy && SPLIT)
         if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
@@ -1531,6 +1576,19 @@ __global__ __launch_bounds__(1024, ISA_EKV_BWD_MIN_BLOCKS) void bwd_kernel(BwdAr
                 a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
         if (MODE != kBwdTwoCopies) return;
     }
+}
+
+// The one-copy launches hold kBwdWavesPerEU waves per SIMD (two blocks per CU, 64 VGPRs); the
+// two-copy launch runs one block per CU and may use the VGPRs of four waves per SIMD.
+template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false, int MODE = kBwdAlone>
+__global__ __launch_bounds__(1024, kBwdWavesPerEU) void bwd_kernel(BwdArgs a) {
+    static_assert(MODE != kBwdTwoCopies, "bwd_two_copies_kernel");
+    bwd_table_body<NEED_X, NEED_W, SPLIT, LANE_RED, MODE>(a);
+}
+
+template <bool NEED_X, bool NEED_W, bool SPLIT>
+__global__ __launch_bounds__(1024) void bwd_two_copies_kernel(BwdArgs a) {
+    bwd_table_body<NEED_X, NEED_W, SPLIT, true, kBwdTwoCopies>(a);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1644,10 +1702,10 @@ __device__ inline void bwd_body_half(const BwdArgs& a, const float2* tab, int it
 template <int HALF, bool NEED_X, bool NEED_W>
 __global__ __launch_bounds__(1024) void bwd_half_kernel(BwdArgs a) {
     extern __shared__ float2 s_half[];
-    for (int i = threadIdx.x; i < a.NP; i += blockDim.x) {
-        const float4 rec = a.lut[i];
+    stage_to_lds<8>(a.lut, a.NP, [&](int i, float4 rec) {
         s_half[i] = HALF == 0 ? make_float2(rec.z, rec.w) : make_float2(rec.x, rec.y);
-    }
+    });
+    __builtin_amdgcn_sched_barrier(0);
     const bool fast = coords_in_padded_range(a.partials, a.NP);
     __syncthreads();
     const int waves = blockDim.x >> 6;
@@ -1857,7 +1915,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void fwd_measured_kernel(FwdArgs a)
     extern __shared__ float2 s_tab[];
     const float2* tab = reinterpret_cast<const float2*>(a.lut);
     if constexpr (LDS) {
-        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s_tab[i] = tab[i];
+        stage_to_lds<8>(tab, a.NP, [&](int i, float2 v) { s_tab[i] = v; });
         __syncthreads();
         tab = s_tab;
     }
@@ -1872,7 +1930,7 @@ __global__ __launch_bounds__(1024) void bwd_measured_kernel(BwdArgs a) {
     const float2* tab = reinterpret_cast<const float2*>(a.lut);
     if constexpr (LDS) {
         float2* s2 = reinterpret_cast<float2*>(s_mtab);
-        for (int i = threadIdx.x; i < a.NP; i += blockDim.x) s2[i] = tab[i];
+        stage_to_lds<8>(tab, a.NP, [&](int i, float2 v) { s2[i] = v; });
         __syncthreads();
         tab = s2;
     }
@@ -2363,6 +2421,15 @@ constexpr int kFwdMinSplitInputs = ISA_EKV_FWD_MIN_SPLIT_K;  // padded inputs pe
 #ifndef ISA_EKV_FWD_WAVE_COST
 #define ISA_EKV_FWD_WAVE_COST 8
 #endif
+#ifndef ISA_EKV_FWD_INPUT_COST  // forward: per padded input of a wave, in token-input units
+#define ISA_EKV_FWD_INPUT_COST 0
+#endif
+#ifndef ISA_EKV_FWD_SMALL_MR_MIN  // forward small plans: tokens per wave considered
+#define ISA_EKV_FWD_SMALL_MR_MIN 2
+#endif
+#ifndef ISA_EKV_FWD_SMALL_MR_MAX
+#define ISA_EKV_FWD_SMALL_MR_MAX 2
+#endif
 #ifndef ISA_EKV_BWD_ITEM_COST
 #define ISA_EKV_BWD_ITEM_COST 2
 #endif
@@ -2408,20 +2475,27 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
     p.n_mt = (int)((M + tokens_per_block - 1) / tokens_per_block);
     if (small && allow_split) {
         // Too few waves to cover the chip even at the largest split: one round of blocks at
-        // most, and the launch lasts as long as its busiest CU. Take the split count (any
-        // count up to kFwdMaxSplit whose chunks hold at least 8 padded inputs) that minimises
-        // small_launch_cost of blocks of (chunk + per-wave setup); ties go to fewer splits.
-        const int64_t tiles = (int64_t)p.n_mt * p.n_ot;
+        // most, and the launch lasts as long as its busiest CU. Take the tokens per wave and
+        // split count (any count up to kFwdMaxSplit whose chunks hold at least 8 padded
+        // inputs) that minimise small_launch_cost of blocks of waves costing MR x (chunk +
+        // per-wave setup) + chunk x the per-input threshold-record cost; ties go to fewer
+        // tokens per wave, then fewer splits.
         int64_t best_cost = -1;
-        for (int sp = 1; sp <= kFwdMaxSplit; ++sp) {
-            const int64_t chunk = round_up((p.Kp + sp - 1) / sp, 8);
-            const int64_t n_sp = (p.Kp + chunk - 1) / chunk;
-            if (n_sp != sp) continue;  // the same plan as a smaller count
-            const int64_t cost =
-                small_launch_cost(tiles * n_sp, 100 * (chunk + ISA_EKV_FWD_WAVE_COST), wpb == kFwdWaves ? 2 : 1);
-            if (best_cost < 0 || cost < best_cost) {
-                best_cost = cost;
-                split = sp;
+        for (int mr = ISA_EKV_FWD_SMALL_MR_MIN; mr <= ISA_EKV_FWD_SMALL_MR_MAX; mr *= 2) {
+            const int64_t n_mt = (M + (int64_t)wpb * mr - 1) / ((int64_t)wpb * mr);
+            const int64_t tiles = n_mt * p.n_ot;
+            for (int sp = 1; sp <= kFwdMaxSplit; ++sp) {
+                const int64_t chunk = round_up((p.Kp + sp - 1) / sp, 8);
+                const int64_t n_sp = (p.Kp + chunk - 1) / chunk;
+                if (n_sp != sp) continue;  // the same plan as a smaller count
+                const int64_t work = 100 * (mr * (chunk + ISA_EKV_FWD_WAVE_COST) + ISA_EKV_FWD_INPUT_COST * chunk);
+                const int64_t cost = small_launch_cost(tiles * n_sp, work, wpb == kFwdWaves ? 2 : 1);
+                if (best_cost < 0 || cost < best_cost) {
+                    best_cost = cost;
+                    split = sp;
+                    p.mr = mr;
+                    p.n_mt = (int)n_mt;
+                }
             }
         }
     }
@@ -2683,10 +2757,10 @@ void launch_backward_copies(bool split, bool need_w, dim3 grid, dim3 block, size
         else
             hipLaunchKernelGGL((bwd_kernel<true, true, false, true, kBwdOneCopy>), grid, block, lds, s, ba);
         if (split)
-            hipLaunchKernelGGL((bwd_kernel<true, true, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s,
+            hipLaunchKernelGGL((bwd_two_copies_kernel<true, true, true>), grid2, block, kBwdTwoCopiesLds, s,
                                ba2);
         else
-            hipLaunchKernelGGL((bwd_kernel<true, true, false, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLdsI,
+            hipLaunchKernelGGL((bwd_two_copies_kernel<true, true, false>), grid2, block, kBwdTwoCopiesLdsI,
                                s, ba2);
     } else {
         if (split)
@@ -2694,10 +2768,10 @@ void launch_backward_copies(bool split, bool need_w, dim3 grid, dim3 block, size
         else
             hipLaunchKernelGGL((bwd_kernel<true, false, false, true, kBwdOneCopy>), grid, block, lds, s, ba);
         if (split)
-            hipLaunchKernelGGL((bwd_kernel<true, false, true, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLds, s,
+            hipLaunchKernelGGL((bwd_two_copies_kernel<true, false, true>), grid2, block, kBwdTwoCopiesLds, s,
                                ba2);
         else
-            hipLaunchKernelGGL((bwd_kernel<true, false, false, true, kBwdTwoCopies>), grid2, block, kBwdTwoCopiesLdsI,
+            hipLaunchKernelGGL((bwd_two_copies_kernel<true, false, false>), grid2, block, kBwdTwoCopiesLdsI,
                                s, ba2);
     }
 }
