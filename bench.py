@@ -430,6 +430,9 @@ def main() -> int:
     ap.add_argument("--graph", action="store_true",
                     help="time the step as replays of one captured HIP graph (torch.cuda.CUDAGraph): "
                          "no host launch cost; the per-kernel figures come from an eager pass after")
+    ap.add_argument("--engine-thread", action="store_true",
+                    help="run the backward on torch's autograd device thread (its default) instead of the "
+                         "calling thread; the handoff between the two threads costs ~85 us per eager step")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -440,6 +443,14 @@ def main() -> int:
               "over tokens with one all-reduce of dVth per layer). Run with --gpus 1.", file=sys.stderr)
         return 2
 
+    if not args.engine_thread:
+        # The steps run their backward on the calling thread (a documented torch setting that
+        # changes no result): for small layers the wake-up of torch's per-device autograd thread
+        # and the wait for it cost more host time than the library's launches. The CIM configs'
+        # JSON also reports the eager step with the engine thread (host.eager_ms_engine_thread).
+        import torch
+
+        torch.autograd.set_multithreading_enabled(False)
     if args.config == "gptl_train":
         return gpt_train_step(args)
     if args.config == "measured_fc1":
@@ -545,6 +556,21 @@ def main() -> int:
         log(f"[bench] {args.config}: eager step {eager_ms:.3f} ms (host launches included)")
     value = cells_step / (ms * 1e-3)
     median_ms = statistics.median(step_ms) if step_ms else ms
+    host = {"autograd_thread": "engine" if args.engine_thread else "calling"}
+    if graph is None:
+        # the same eager step with the other autograd threading, for comparison (not the value)
+        torch.autograd.set_multithreading_enabled(not args.engine_thread)
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        other = 1e3 * (time.perf_counter() - t0) / args.steps
+        torch.autograd.set_multithreading_enabled(args.engine_thread)
+        host["eager_ms_calling_thread" if args.engine_thread else "eager_ms_engine_thread"] = round(other, 4)
+        log(f"[bench] eager step with the {'calling' if args.engine_thread else 'engine'} thread: {other:.3f} ms")
     log(f"[bench] {args.config}: {ms:.3f} ms/step mean, {median_ms:.3f} median"
         f"{' (graph replay)' if graph is not None else ''} "
         f"(wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
@@ -649,6 +675,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "cpu_lut_oracle": lut_cpu,
+        "host": host,
     }
     print(json.dumps(result), flush=True)
     return 0

@@ -284,11 +284,13 @@ int isa_ekv_profile_end(double* ms, int* launches);
  *       or -1 when the call cannot use a second copy (the word is then not written)
  *   [2] forward: K ranges summed separately (1: no split); backward: token splits
  *   [3] forward: tokens per wave; backward: inputs per wave of the one-copy kernel
- *   [4] main-kernel blocks   [5] waves per block   [6] LDS bytes per block */
+ *   [4] main-kernel blocks   [5] waves per block   [6] LDS bytes per block
+ *   [7] backward with dVth: dVth partial planes (the token splits, or a quarter of them when
+ *       the main kernel's blocks sum groups of four splits); otherwise 0 */
 #define ISA_EKV_PLAN_FORWARD 0
 #define ISA_EKV_PLAN_BACKWARD 1
 #define ISA_EKV_PLAN_LAYER_BACKWARD 2
-#define ISA_EKV_PLAN_INFO_LEN 7
+#define ISA_EKV_PLAN_INFO_LEN 8
 int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries, int need_grad_x, int need_grad_w,
                       int64_t* info, int n_info);
 

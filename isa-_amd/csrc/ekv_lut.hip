@@ -1244,6 +1244,8 @@ struct BwdArgs {
     int M, K, O, Kp, Op, ldg, NP;
     int n_ob, n_kb, n_split, m_chunk;
     int n_items;
+    int dv_group;           // 1: each group of kDvGroup consecutive items (token splits) is summed
+                            // in its block, one dVth partial plane per group (see bwd_item)
     float cmin, cmax;
     float k2, c2;           // exact: 2^(-V_D a), V_D a
 };
@@ -1321,23 +1323,54 @@ __device__ inline int wave_rows_input2() {
     return (int)q[0];
 }
 
+// Token splits summed per block in the grouped order (small plans, where the dVth partial
+// planes would otherwise cost more traffic than the cells' reads).
+constexpr int kDvGroup = 4;
+
+struct BwdItem {
+    int kb, ob, sp;  // input pair, output block, token split
+};
+
+// The work item's coordinates. Default order: inputs vary fastest, so the waves of a block
+// share (output block, token split) and the G row slices they stream are fetched once into
+// the CU's L1 and reused (blocks keep the hardware's round-robin XCD order: grouping one
+// (output block, token split) on one XCD halves fc1's HBM reads of G but slows fc2 as much as
+// it speeds fc1). Grouped order (dv_group): kDvGroup consecutive token splits first, so each
+// group of kDvGroup waves shares (output block, inputs) and its dVth partials are summed in
+// the block.
+__device__ inline BwdItem bwd_item(const BwdArgs& a, int item) {
+    BwdItem it;
+    int rest;
+    if (a.dv_group) {
+        const int sp_lo = item % kDvGroup;
+        rest = item / kDvGroup;
+        it.kb = rest % a.n_kb;
+        rest /= a.n_kb;
+        it.ob = rest % a.n_ob;
+        it.sp = (rest / a.n_ob) * kDvGroup + sp_lo;
+    } else {
+        it.kb = item % a.n_kb;
+        rest = item / a.n_kb;
+        it.ob = rest % a.n_ob;
+        it.sp = rest / a.n_ob;
+    }
+    return it;
+}
+
 // LANE_RED: reduce each token's dX partials across the wave with lane exchanges
 // (wave_sum_rows4) instead of the LDS transpose buffer (red unused), freeing LDS for
 // tables too large to leave room for the buffers of 16 waves.
-template <int KR, bool NEED_X, bool NEED_W, class Cell, bool LANE_RED = false>
+// DVG: the launch may run the grouped order (a.dv_group): dv_lds is then LDS of at least
+// 2 * KR * ORR * 64 floats per wave that the block no longer reads (the table), and every wave
+// of the block calls this with a valid item (the sum takes block barriers).
+template <int KR, bool NEED_X, bool NEED_W, class Cell, bool LANE_RED = false, bool DVG = false>
 __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4* xrec, const float2* wsT,
-                                float* red, int item) {
+                                float* red, int item, float* dv_lds = nullptr) {
     constexpr int ORR = kBwdORR, MB = kRedSlots / KR;
     static_assert(!LANE_RED || KR == 4 || KR == 2, "the lane-exchange reduction sums two or four inputs per wave");
     const int lane = threadIdx.x & 63;
-    // inputs vary fastest: the waves of a block share (output block, token split), so the
-    // G row slices they stream are fetched once into the CU's L1 and reused (blocks keep the
-    // hardware's round-robin XCD order: grouping one (output block, token split) on one XCD
-    // halves fc1's HBM reads of G but slows fc2 as much as it speeds fc1)
-    const int kb = item % a.n_kb;
-    const int rest = item / a.n_kb;
-    const int ob = rest % a.n_ob;
-    const int sp = rest / a.n_ob;
+    const BwdItem it = bwd_item(a, item);
+    const int kb = it.kb, ob = it.ob, sp = it.sp;
     const int o_lane = ob * 64 * ORR + lane * ORR;
     const int k0 = kb * KR;
     const int m_begin = sp * a.m_chunk;
@@ -1470,6 +1503,40 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
         }
     }
     if (NEED_W) {
+        if constexpr (DVG) {
+            if (a.dv_group) {  // block-uniform
+                static_assert(ORR == 4, "one 16-byte slot per lane, input and sign");
+                constexpr int kSlice = 2 * KR * 64;  // float4 slots per wave: [sign][input][lane]
+                __syncthreads();                     // no wave of the block reads the table any more
+                float4* slots = reinterpret_cast<float4*>(dv_lds);
+                float4* mine = slots + (threadIdx.x >> 6) * kSlice;
+#pragma unroll
+                for (int kk = 0; kk < KR; ++kk) {
+                    mine[kk * 64 + lane] = make_float4(accp[kk][0], accp[kk][1], accp[kk][2], accp[kk][3]);
+                    mine[(KR + kk) * 64 + lane] = make_float4(accn[kk][0], accn[kk][1], accn[kk][2], accn[kk][3]);
+                }
+                __syncthreads();
+                // each group's kDvGroup slices summed in split order, one thread per float4 slot
+                const int waves = blockDim.x >> 6;
+                const int slots_out = (waves / kDvGroup) * kSlice;
+                for (int t = threadIdx.x; t < slots_out; t += blockDim.x) {
+                    const int g = t / kSlice, q = t - g * kSlice;
+                    const float4* src = slots + g * kDvGroup * kSlice + q;
+                    float4 sum = src[0];
+#pragma unroll
+                    for (int s2 = 1; s2 < kDvGroup; ++s2) {
+                        const float4 v = src[s2 * kSlice];
+                        sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+                    }
+                    const BwdItem gi = bwd_item(a, (item - (item % waves)) + g * kDvGroup);
+                    const int sign = q / (KR * 64), kk = (q / 64) % KR, ql = q % 64;
+                    float* dst = a.dv_part + ((size_t)(gi.sp / kDvGroup) * 2 + sign) * a.Kp * a.Op +
+                                 (size_t)(gi.kb * KR + kk) * a.Op + gi.ob * 64 * ORR + ql * ORR;
+                    *reinterpret_cast<float4*>(dst) = sum;
+                }
+                return;
+            }
+        }
         float* dst_p = a.dv_part + (size_t)sp * 2 * a.Kp * a.Op;
         float* dst_n = dst_p + (size_t)a.Kp * a.Op;
 #pragma unroll
@@ -1568,12 +1635,15 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
     for (int vb = blockIdx.x;; vb += stride) {
         const int item = vb * waves + wave;
         if (item >= a.n_items) return;
+        // the one-shot launch may sum its blocks' dVth partials in the table's LDS (dv_group)
+        constexpr bool DVG = MODE == kBwdAlone;
+        float* dv_lds = reinterpret_cast<float*>(s_lut_bwd);
         if (fast)
-            bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED>(
-                a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+            bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED, DVG>(
+                a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item, dv_lds);
         else
-            bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED>(
-                a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item);
+            bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED, DVG>(
+                a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item, dv_lds);
         if (MODE != kBwdTwoCopies) return;
     }
 }
@@ -2433,6 +2503,10 @@ constexpr int kFwdMinSplitInputs = ISA_EKV_FWD_MIN_SPLIT_K;  // padded inputs pe
 #ifndef ISA_EKV_BWD_ITEM_COST
 #define ISA_EKV_BWD_ITEM_COST 2
 #endif
+#ifndef ISA_EKV_BWD_SMALL_ROUNDS  // backward plans by the cost model below this many possible rounds
+#define ISA_EKV_BWD_SMALL_ROUNDS 8
+#endif
+constexpr int64_t kBwdSmallRounds = ISA_EKV_BWD_SMALL_ROUNDS;
 // ... and a CU holding one block where it could hold two runs its waves at this percentage of
 // the full rate (fewer waves to hide the LDS and memory latencies)
 #ifndef ISA_EKV_LONE_BLOCK_RATE
@@ -2528,6 +2602,8 @@ FwdPlan plan_forward(int64_t M, int64_t K, int64_t O, bool exact, bool allow_spl
 struct BwdPlan {
     int64_t Kp, Op;
     int n_ob, n_kb, n_split, m_chunk, n_items, waves_per_block, blocks;
+    int dv_planes;  // dVth partial planes: n_split, or n_split / kDvGroup with dv_group
+    bool dv_group;
     bool grad_padded, split, lane_red, gtab, halves;
     bool copies;  // at least ISA_EKV_OPT_COPY_MIN_CELLS cells: the second table copy may pay
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
@@ -2615,14 +2691,23 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     while (best_splits < top_splits && fill_pair(best_splits) < best_fill - 0.005) ++best_splits;
     p.m_chunk = (int)round_up((M + best_splits - 1) / best_splits, mb);
     if (p.m_chunk < mb) p.m_chunk = mb;
-    if (!pair && base_items * max_splits < 2 * kCUs * resident * wpb) {
-        // Too few tokens for two full rounds of blocks: the launch lasts as long as its busiest
-        // CU. The token loop masks the tokens past a chunk, so any chunk length works; take
-        // the one (of at least 8 tokens) minimising small_launch_cost of blocks of (chunk +
-        // per-item setup); ties go to fewer splits.
+    // Problems with too few tokens for many rounds of blocks take their token splits from the
+    // launch cost model instead of the fill rule (whose chunks of whole dX batches leave a
+    // round two-thirds empty at a few rounds)
+    const bool small = !pair && base_items * max_splits < kBwdSmallRounds * kCUs * resident * wpb;
+    // Small plans of the one-shot table kernel sum each block's dVth partials over groups of
+    // kDvGroup token splits in LDS (bwd_item's grouped order), writing a quarter of the planes:
+    // token-split counts are then multiples of kDvGroup, and every block is full.
+    const bool grouped = small && need_w && !exact && !p.gtab && !p.halves && !p.copies && wpb == 16 &&
+                         base_items % (16 / kDvGroup) == 0;
+    if (small) {
+        // The launch lasts as long as its busiest CU. The token loop masks the tokens past a
+        // chunk, so any chunk length works; take the one (of at least 8 tokens) minimising
+        // small_launch_cost of blocks of (chunk + per-item setup); ties go to fewer splits.
         const int64_t min_chunk = std::max<int64_t>(8, mb);
         int64_t best_cost = -1;
         for (int64_t sp = 1; sp <= (M + min_chunk - 1) / min_chunk; ++sp) {
+            if (grouped && sp % kDvGroup) continue;
             const int64_t chunk = (M + sp - 1) / sp;
             if ((M + chunk - 1) / chunk != sp) continue;  // the same plan as a smaller count
             const int64_t blocks = (base_items * sp + wpb - 1) / wpb;
@@ -2637,6 +2722,8 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     if (p.n_split < 1) p.n_split = 1;
     p.n_items = (int)(base_items * p.n_split);
     p.blocks = (p.n_items + wpb - 1) / wpb;
+    p.dv_group = grouped && p.n_split % kDvGroup == 0 && p.n_items % wpb == 0;
+    p.dv_planes = p.dv_group ? p.n_split / kDvGroup : p.n_split;
     p.grad_padded = glue || (O % (64 * kBwdORR)) != 0;
     const size_t xrec_bytes = (size_t)round_up((int64_t)M * p.Kp * 16, 256);
     const size_t wsT_bytes = (size_t)round_up(p.Kp * p.Op * 8, 256);
@@ -2658,7 +2745,7 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     p.off_dx = off;  // the half-table passes write a plane each
     if (need_x) off += (size_t)round_up((int64_t)(p.halves ? 2 : 1) * p.n_ob * M * (K > 0 ? K : 1) * 4, 256);
     p.off_dv = off;
-    if (need_w) off += (size_t)round_up((int64_t)p.n_split * 2 * p.Kp * p.Op * 4, 256);
+    if (need_w) off += (size_t)round_up((int64_t)p.dv_planes * 2 * p.Kp * p.Op * 4, 256);
     p.off_glue = off;  // col_part [kGlueBlocks][2][Op], r_part [kGlueBlocks][Op/256], aff_part [kDxReduceBlocks]
     if (glue)
         off += (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) +
@@ -3284,6 +3371,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     ba.n_split = p.n_split;
     ba.m_chunk = p.m_chunk;
     ba.n_items = p.n_items;
+    ba.dv_group = p.dv_group ? 1 : 0;
     float scale = 1.0f;
     if (cs.exact) {
         ba.k2 = cs.k2;
@@ -3338,7 +3426,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     DvReduceArgs dva{};
     int dv_blocks = 0;
     if (need_w) {
-        dva = DvReduceArgs{reinterpret_cast<const float*>(ws + p.off_dv), p.n_split, (int)K, (int)O, (int)p.Kp,
+        dva = DvReduceArgs{reinterpret_cast<const float*>(ws + p.off_dv), p.dv_planes, (int)K, (int)O, (int)p.Kp,
                            (int)p.Op, scale, grad_vth_pos, grad_vth_neg};
         dv_blocks = std::min(dv_reduce_tiles(K, O), 4096);
     }
@@ -3919,6 +4007,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
         v[4] = p.blocks;
         v[5] = p.wpb;
         v[6] = (int64_t)tc.lds;
+        v[7] = 0;
     } else if (which == ISA_EKV_PLAN_BACKWARD || which == ISA_EKV_PLAN_LAYER_BACKWARD) {
         const bool nx = need_grad_x != 0, nw = need_grad_w != 0;
         const BwdPlan p = plan_backward(M, K, O, n_entries, nx, nw, which == ISA_EKV_PLAN_LAYER_BACKWARD);
@@ -3929,6 +4018,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
         v[4] = p.blocks;
         v[5] = p.waves_per_block;
         v[6] = (int64_t)p.lds_bytes;
+        v[7] = nw ? p.dv_planes : 0;
     } else {
         return fail(ISA_EKV_EINVAL, "unknown plan kind %d", which);
     }

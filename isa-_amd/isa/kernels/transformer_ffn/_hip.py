@@ -25,7 +25,7 @@ LUT_PLAIN_BF16 = 3
 PLAN_FORWARD = 0
 PLAN_BACKWARD = 1
 PLAN_LAYER_BACKWARD = 2
-PLAN_INFO_LEN = 7
+PLAN_INFO_LEN = 8
 NOALLOC_MAX_BYTES = 64 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
 OPT_COPY_MIN_CELLS = 1
 

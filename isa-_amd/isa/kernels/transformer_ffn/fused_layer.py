@@ -64,7 +64,11 @@ class FusedCIMLayerFn(torch.autograd.Function):
             r_log_scale=r_log_scale, r_log_range=r_log_range, need_r_log_scale=bool(need[7]))
 
         def cast(t, like):
-            return None if t is None or like is None else t.reshape(like.shape).to(dtype=like.dtype)
+            if t is None or like is None:
+                return None
+            if t.shape != like.shape:
+                t = t.reshape(like.shape)
+            return t if t.dtype is like.dtype else t.to(dtype=like.dtype)
 
         return (
             cast(res["dx"], x) if need[0] else None,

@@ -27,6 +27,8 @@ def _require_cuda(t: torch.Tensor, name: str) -> None:
 
 def as_kernel_f32(t: torch.Tensor) -> torch.Tensor:
     """fp32, contiguous and 16-byte aligned (a copy only when needed)."""
+    if t.dtype is torch.float32 and t.is_contiguous() and not t.data_ptr() & 15:
+        return t  # the common case, without the conversions' dispatch cost
     t = t.to(dtype=torch.float32).contiguous()
     if t.numel() and t.data_ptr() % 16:
         t = t.clone()
@@ -60,13 +62,15 @@ def plan_info(kind: str, M: int, K: int, O: int, n_entries: int, need_grad_x: bo
     """The library's plan for a LUT call at this shape (isa_ekv_plan_info): workspace bytes,
     the byte offset of the table-copy mode word in the workspace (-1 when the call has none),
     K splits (forward) or token splits (backward), tokens (forward) or inputs (backward) per
-    wave, main-kernel blocks, waves per block and LDS bytes per block."""
+    wave, main-kernel blocks, waves per block, LDS bytes per block and (backward with dVth)
+    the dVth partial planes."""
     lib = _hip.load()
     info = (ctypes.c_int64 * _hip.PLAN_INFO_LEN)()
     rc = lib.isa_ekv_plan_info(_PLAN_KINDS[kind], int(M), int(K), int(O), int(n_entries), int(need_grad_x),
                                int(need_grad_w), info, _hip.PLAN_INFO_LEN)
     _hip.check(rc, "isa_ekv_plan_info")
-    keys = ("workspace_bytes", "mode_offset", "splits", "per_wave", "blocks", "waves_per_block", "lds_bytes")
+    keys = ("workspace_bytes", "mode_offset", "splits", "per_wave", "blocks", "waves_per_block", "lds_bytes",
+            "dv_planes")
     return dict(zip(keys, (int(v) for v in info)))
 
 
@@ -301,7 +305,9 @@ def _glue_operand(t: Optional[torch.Tensor], numel: int, name: str, device) -> O
     _require_cuda(t, name)
     if t.device != device:
         raise RuntimeError(f"{name} must be on {device}")
-    t = as_kernel_f32(t.detach().reshape(-1))
+    # only the data pointer reaches the library: no autograd view is needed
+    if not (t.dtype is torch.float32 and t.is_contiguous() and not t.data_ptr() & 15):
+        t = as_kernel_f32(t.detach().reshape(-1))
     if t.numel() != numel:
         raise RuntimeError(f"{name} must have {numel} elements, got {t.numel()}")
     return t
