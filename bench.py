@@ -70,6 +70,9 @@ def cpu_info() -> str:
         return platform.processor() or "unknown"
 
 
+CPU_BATCH_TOKENS = 64
+
+
 def cpu_baseline(layers, target_s: float) -> dict:
     """The reference's PyTorch CPU path (exact formula, cim.py:201-214 + flash_transistor.py:95-131),
     restated in oracle/exact.py, fwd+bwd on a token sample of every CIM layer of the workload
@@ -99,15 +102,18 @@ def cpu_baseline(layers, target_s: float) -> dict:
             return time.perf_counter() - t0
 
         run(2)  # warm-up
-        dt = run(32)  # the per-token cost grows with the chunk temporaries: size from 32 tokens
-        # scale the sample to this layer's share of the CPU time budget
-        want = max(8, min(4096, int(32 * target_s / len(layers) / max(dt, 1e-3))))
-        dt = run(want)
+        # 64-token batches until this layer's share of the CPU time budget is spent (at least
+        # one): the reference path's per-token cost grows with its batch's temporaries (~6x
+        # from 32 to 736 tokens at fc1), so the batch is fixed and the count bounded by time
+        want, dt = 0, 0.0
+        while want == 0 or dt < target_s / len(layers):
+            dt += run(CPU_BATCH_TOKENS)
+            want += CPU_BATCH_TOKENS
         cells = 2.0 * want * k_in * o_out
         total_cells += cells
         total_s += dt
-        parts.append(f"{k_in}->{o_out} on {want} tokens ({cells:.3e} cell-evals, {dt:.1f} s, "
-                     f"{cells / dt:.3e}/s)")
+        parts.append(f"{k_in}->{o_out} on {want} tokens in batches of {CPU_BATCH_TOKENS} ({cells:.3e} "
+                     f"cell-evals, {dt:.1f} s, {cells / dt:.3e}/s)")
     return {
         "value": total_cells / total_s,
         "unit": "cell-evals/s",
