@@ -70,7 +70,7 @@ def cpu_info() -> str:
         return platform.processor() or "unknown"
 
 
-CPU_BATCH_TOKENS = 64
+CPU_BATCH_TOKENS = 128
 
 
 def cpu_baseline(layers, target_s: float) -> dict:
@@ -102,7 +102,7 @@ def cpu_baseline(layers, target_s: float) -> dict:
             return time.perf_counter() - t0
 
         run(2)  # warm-up
-        # 64-token batches until this layer's share of the CPU time budget is spent (at least
+        # 128-token batches until this layer's share of the CPU time budget is spent (at least
         # one): the reference path's per-token cost grows with its batch's temporaries (~6x
         # from 32 to 736 tokens at fc1), so the batch is fixed and the count bounded by time
         want, dt = 0, 0.0
