@@ -439,6 +439,9 @@ def main() -> int:
     ap.add_argument("--engine-thread", action="store_true",
                     help="run the backward on torch's autograd device thread (its default) instead of the "
                          "calling thread; the handoff between the two threads costs ~85 us per eager step")
+    ap.add_argument("--no-ranked", action="store_true",
+                    help="plan the table backwards without the ranked kernel (isa_ekv_set_option "
+                         "ISA_EKV_OPT_RANKED = 0): the one- or two-copy kernel runs instead")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -457,6 +460,10 @@ def main() -> int:
         import torch
 
         torch.autograd.set_multithreading_enabled(False)
+    if args.no_ranked:
+        from isa.kernels.transformer_ffn import ops
+
+        ops.ranked_backward(False)
     if args.config == "gptl_train":
         return gpt_train_step(args)
     if args.config == "measured_fc1":

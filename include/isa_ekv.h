@@ -280,8 +280,9 @@ int isa_ekv_profile_end(double* ms, int* launches);
  * min(n_info, ISA_EKV_PLAN_INFO_LEN) values (later slots get 0):
  *   [0] workspace bytes
  *   [1] byte offset in the workspace of the table-copy mode word (int32: after the call, 1 when
- *       the main kernel ran with the second, bank-rotated table copy, 0 when with one copy),
- *       or -1 when the call cannot use a second copy (the word is then not written)
+ *       the main kernel ran with the second, bank-rotated table copy, 0 when with one copy,
+ *       2 when the backward ran ranked: see ISA_EKV_OPT_RANKED), or -1 when the call cannot
+ *       use a second copy (the word is then not written)
  *   [2] forward: K ranges summed separately (1: no split); backward: token splits
  *   [3] forward: tokens per wave; backward: inputs per wave of the one-copy kernel
  *   [4] main-kernel blocks   [5] waves per block   [6] LDS bytes per block
@@ -300,9 +301,14 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *   ISA_EKV_OPT_COPY_MIN_CELLS: LUT calls of fewer cells M*K*O never use the second table
  *     copy, nor enqueue its assignment pass (default 2^28: below that the extra launch costs
  *     more than the copy saves). 0 lets every call consider it.
+ *   ISA_EKV_OPT_RANKED: 1 (default) lets table backwards that consider the second copy run
+ *     the ranked backward instead, when their coordinates need no clamp and reach a window of
+ *     at most 3008 table records (decided on the device; mode word 2): each wave's gathers
+ *     then read thresholds dealt to lanes in rank order. 0 never runs it.
  * Plans (and so workspace sizes) depend on the options: query workspace sizes after setting
  * them, and do not change them while calls are in flight. */
 #define ISA_EKV_OPT_COPY_MIN_CELLS 1
+#define ISA_EKV_OPT_RANKED 2
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous);
 
 /* Measurement aid, no reference counterpart: launches two 1024-thread blocks per CU, each

@@ -127,6 +127,9 @@ constexpr int64_t kCUs = 256;  // MI355X compute units (a fixed plan input: work
 // a small call more than the copy can save.
 std::atomic<int64_t> g_copy_min_cells{(int64_t)1 << 28};
 
+// Planning option ISA_EKV_OPT_RANKED: whether table backwards may run the ranked kernel.
+std::atomic<int64_t> g_ranked{1};
+
 bool copies_pay(int64_t M, int64_t K, int64_t O) {
     return (double)M * (double)K * (double)O >= (double)g_copy_min_cells.load(std::memory_order_relaxed);
 }
@@ -1086,6 +1089,10 @@ __device__ inline bool launch_copy_mode(const float2* __restrict__ partials, int
     return on;
 }
 
+// Mode word values: 0 one table copy, 1 the second copy, kModeRanked the ranked backward (whose
+// branch-deal pass runs before the copy assignment and records its decision first).
+constexpr int kModeRanked = 2;
+
 // LANES = 32: 8-byte records, gathered by half-waves over 32 bank pairs; LANES = 16: 16-byte
 // records, gathered by quarter-waves over 16 bank quads. Copy 1 sits LANES / 2 bins away.
 // Every wave decides the launch's copy mode from the range partials (launch_copy_mode);
@@ -1094,9 +1101,13 @@ template <int LANES>
 __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2* __restrict__ wsT,
                                                               const float2* __restrict__ partials, int NP,
                                                               int max_window, int* __restrict__ mode_word,
-                                                              int64_t Kp, int64_t Op, int copy_offset) {
+                                                              int64_t Kp, int64_t Op, int copy_offset,
+                                                              int after_rank) {
     static_assert(LANES == 32 || LANES == 16, "half-wave or quarter-wave gathers");
     constexpr int kGroups = 64 / LANES, kMask = LANES - 1;
+    // a backward whose branch-deal pass chose the ranked launch keeps that mode (this pass
+    // never writes kModeRanked, so every block reads the same decision)
+    if (after_rank && __builtin_amdgcn_readfirstlane(*mode_word) == kModeRanked) return;
     const bool on = launch_copy_mode(partials, NP, max_window);
     if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = on ? 1 : 0;
     if (!on) return;
@@ -1583,7 +1594,7 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
     // the interleaved one runs one block per CU in any case and checks first.)
     int lo = 0, n_rec = a.NP;  // table records held: [lo, lo + n_rec)
     if constexpr (MODE == kBwdTwoCopies) {
-        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) == 0) return;
+        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 1) return;
         // tables past kSplitRecords hold the window the launch's coordinates reach (the mode
         // word is set only when it fits)
         if (a.NP > kSplitRecords) {
@@ -1659,6 +1670,282 @@ __global__ __launch_bounds__(1024, kBwdWavesPerEU) void bwd_kernel(BwdArgs a) {
 template <bool NEED_X, bool NEED_W, bool SPLIT>
 __global__ __launch_bounds__(1024) void bwd_two_copies_kernel(BwdArgs a) {
     bwd_table_body<NEED_X, NEED_W, SPLIT, true, kBwdTwoCopies>(a);
+}
+
+// ----------------------------------------------------------------------------------
+// Ranked backward. A gather instruction's 32-lane halves conflict in the LDS banks when their
+// records spread over more than 32 records, and with lanes along outputs they spread over the
+// whole threshold window (69 records at the initial thresholds). The backward's sums do not
+// care which lane evaluates which (output, sign) branch of an input: dVth± accumulates per
+// branch over tokens, and dX sums every branch of an input per token. So per (input, block of
+// 256 outputs) the branches are re-dealt: residue class c (outputs c + 32 t, t < 8, each with
+// its + and - threshold: 16 branches) goes to lanes c and c + 32, ranked by threshold
+// coordinate, lane c taking ranks 0-7 and lane c + 32 ranks 8-15 as slots 0-7. A gather
+// instruction (one slot) then reads, across a half-wave, one rank of 32 classes: a window of
+// ~30 records instead of ~69 (measured: 1.13 instead of 1.95 ns per gather per CU).
+// The cost is G: a branch's G[m][o] is no longer in its lane's registers. Each block (12
+// waves, 12 consecutive inputs sharing the output block and token range) stages G for 8
+// tokens at a time in LDS, as {G, -G} quads of 4 tokens per output (the sign of a - branch
+// folds into its G), and a lane reads one 16-byte quad per slot and token group: lane c's
+// quads sit in bank quad c mod 16, so the reads are conflict-free. The staged G is read once
+// per block, not once per wave.
+// Each branch accumulates sign * sum_m G r L_D: dVth+ partials as the one-copy kernel (the same
+// products in the same token order, so bitwise the same sums), dVth- partials negated back.
+// ----------------------------------------------------------------------------------
+constexpr int kRankWindow = 3008;   // table records each half of a ranked launch holds
+#ifndef ISA_EKV_RANK_D_GAP
+#define ISA_EKV_RANK_D_GAP 32
+#endif
+// the D halves start kRankDOffset records after the I halves: a multiple of 32 (both halves of
+// a record in one bank pair, as the split tables) that is not one of 64, so the two reads stay
+// two ds_read_b64 with an immediate offset rather than one ds_read2st64_b64
+constexpr int kRankDOffset = kRankWindow + ISA_EKV_RANK_D_GAP;
+constexpr int kRankChunk = 8;       // tokens per G staging round (two groups of four)
+#ifndef ISA_EKV_RANK_WAVES
+#define ISA_EKV_RANK_WAVES 16
+#endif
+// waves (inputs) per ranked block: two blocks per CU at 12 waves leave a wave ~80 VGPRs, room
+// for several tokens' gathers in flight (at 16 waves, 64 VGPRs, one token's at a time)
+constexpr int kRankWaves = ISA_EKV_RANK_WAVES;
+static_assert(kRankWaves >= 8 && kRankWaves <= 16, "eight staging waves per ranked block");
+constexpr int kRankGroupBytes = 2 * 256 * 16;                      // one token group: [sign][256] float4
+constexpr unsigned kRankRingBase = (unsigned)(kRankDOffset + kRankWindow) * 8;  // G ring after the I and D halves
+constexpr size_t kRankLds = (size_t)kRankRingBase + 4 * kRankGroupBytes;  // [buffer][group] x 8 KB
+static_assert(2 * kRankLds <= (size_t)kLdsBytes, "two ranked blocks per CU");
+static_assert((size_t)kRankDOffset * 8 < 65536 && 3 * kRankGroupBytes < 65536, "ds immediate offsets");
+
+struct RankArgs {
+    const float2* wsT;    // [Kp][Op] threshold records {+, -}
+    float* ws_ranked;     // [Kp][n_ob][64 lanes][8 slots] threshold coordinate of each slot's branch
+    unsigned* branch;     // [Kp][n_ob][64 lanes]: slot s in bits 4s..4s+3, t (output c + 32 t) | sign << 3
+    const float2* partials;
+    int* mode_word;
+    int Kp, Op, n_ob, NP;
+};
+
+// Thresholds spread over more table records than this leave a rank's window across 32 classes
+// hundreds of records wide; there the second table copy does better (measured at U[0, 5] V,
+// 1576 records: 13.5 ms ranked against 12.4 ms with two copies per GPT-L launch).
+constexpr float kRankMaxSpread = 256.0f;
+
+// Whether the ranked launch works (wave-uniform): the clamp-free loop, thresholds spread over at
+// most kRankMaxSpread records, and a coordinate window that fits the launch's table halves.
+__device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP) {
+    if (!coords_in_padded_range(partials, NP)) return false;
+    const CoordRange c = read_coord_range(partials);
+    if (!(c.whi - c.wlo <= kRankMaxSpread)) return false;
+    int lo, n;
+    coord_window(c, NP, lo, n);
+    return n <= kRankWindow;
+}
+
+// The branch deal, one thread per (input, output block, residue class): ranks by (coordinate,
+// branch index), so ties keep a fixed order. Block 0 records the mode word.
+__global__ __launch_bounds__(256) void bwd_rank_kernel(RankArgs a) {
+    const bool on = ranked_mode(a.partials, a.NP);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.mode_word = on ? kModeRanked : 0;
+    if (!on) return;
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= (int64_t)a.Kp * a.n_ob * 32) return;
+    const int c = (int)(p & 31);
+    const int64_t q = p >> 5;  // k * n_ob + ob
+    const int ob = (int)(q % a.n_ob);
+    const int64_t k = q / a.n_ob;
+    const float2* src = a.wsT + k * a.Op + (int64_t)ob * 256 + c;
+    float key[16];  // branch i: output c + 32 (i / 2), sign i % 2
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const float2 w = src[32 * t];
+        key[2 * t] = w.x;
+        key[2 * t + 1] = w.y;
+    }
+    float* dst = a.ws_ranked + q * 64 * 8;
+    unsigned pk0 = 0, pk1 = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) rank += (key[j] < key[i] || (key[j] == key[i] && j < i)) ? 1 : 0;
+        const int slot = rank & 7;
+        dst[(c + (rank & 8) * 4) * 8 + slot] = key[i];
+        const unsigned code = (unsigned)((i >> 1) | ((i & 1) << 3)) << (4 * slot);
+        if (rank < 8)
+            pk0 |= code;
+        else
+            pk1 |= code;
+    }
+    a.branch[q * 64 + c] = pk0;
+    a.branch[q * 64 + c + 32] = pk1;
+}
+
+// Block = kRankWaves waves: inputs kg*W .. kg*W+W-1 (one per wave), one output block, one token split.
+// Needs dX (the copies machinery's launches all do); NEED_W adds the dVth partials.
+template <bool NEED_W>
+__global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranked_kernel(BwdArgs a, const float* __restrict__ ws_ranked,
+                                                                     const unsigned* __restrict__ branch) {
+    if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != kModeRanked) return;
+    extern __shared__ float4 s_ranked[];
+    char* smem = reinterpret_cast<char*>(s_ranked);
+    float2* s_tab = reinterpret_cast<float2*>(smem);  // I halves [0, n), D halves [kRankDOffset, kRankDOffset + n)
+    int lo, n;
+    coord_window(read_coord_range(a.partials), a.NP, lo, n);
+    stage_to_lds<8>(a.lut + lo, n, [&](int i, float4 rec) {
+        s_tab[i] = make_float2(rec.x, rec.y);
+        s_tab[kRankDOffset + i] = make_float2(rec.z, rec.w);
+    });
+    const float2* tab = s_tab - lo;  // record i of the table at LDS record i - lo
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n_kg = (a.Kp + kRankWaves - 1) / kRankWaves;
+    int b = blockIdx.x;
+    const int kg = b % n_kg;
+    b /= n_kg;
+    const int ob = b % a.n_ob;
+    const int sp = b / a.n_ob;
+    const int k = kg * kRankWaves + wave;
+    const bool active = k < a.Kp;  // wave-uniform; inactive waves still stage G and meet the barriers
+    const int m_begin = sp * a.m_chunk;
+    const int m_end = min(a.M, m_begin + a.m_chunk);
+    const int c = lane & 31;
+
+    float ws[8];
+    unsigned goff[8];  // byte address of each slot's G quad in ring buffer 0, group 0
+    {
+        unsigned pk = 0;
+        float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+        if (active) {
+            const size_t q = ((size_t)k * a.n_ob + ob) * 64 + lane;
+            w0 = *reinterpret_cast<const float4*>(ws_ranked + q * 8);
+            w1 = *reinterpret_cast<const float4*>(ws_ranked + q * 8 + 4);
+            pk = branch[q];
+        }
+        ws[0] = w0.x; ws[1] = w0.y; ws[2] = w0.z; ws[3] = w0.w;
+        ws[4] = w1.x; ws[5] = w1.y; ws[6] = w1.z; ws[7] = w1.w;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const unsigned t = (pk >> (4 * s)) & 7u, sg = (pk >> (4 * s + 3)) & 1u;
+            goff[s] = kRankRingBase + (sg * 256u + (unsigned)c + 32u * t) * 16u;
+        }
+    }
+    float acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc[s] = 0.0f;
+    const int row_tok = wave_rows_input();  // which token of a group this lane's 16-lane row sums
+    // this lane's dX partial for the first token of the split (written by one lane per row)
+    float* const dxp = a.dx_part + ((size_t)ob * a.M + m_begin + row_tok) * a.K + k;
+
+    // G staging by waves 0-7: each thread holds the quad (4 tokens) of one output and token
+    // group; the wave decides the group, so each load's token row is wave-uniform and its buffer
+    // descriptor (base at the row's output slice, 1 KB long, empty past the split's tokens,
+    // whose loads then return 0) is formed in scalar registers
+    const int so = tid & 255, stg = (wave >> 2) & 1;
+    const bool stager = wave < 8;
+    const unsigned gvoff = (unsigned)so * 4u;
+    auto grow = [&](int m) {
+        const float* base = a.grad + (size_t)m * a.ldg + (size_t)ob * 256;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, m < m_end ? 1024 : 0,
+                                                 0x00027000);
+    };
+    auto gload = [&](int m0) {
+        const int m = m0 + 4 * stg;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)  // (the builtin returns the 32 loaded bits as an integer)
+            v[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(grow(m + j), gvoff, 0, 0));
+        return make_float4(v[0], v[1], v[2], v[3]);
+    };
+    auto gstore = [&](int buf, float4 v) {
+        float4* d = reinterpret_cast<float4*>(smem + kRankRingBase + (size_t)(buf * 2 + stg) * kRankGroupBytes) + so;
+        d[0] = v;
+        d[256] = make_float4(-v.x, -v.y, -v.z, -v.w);  // the - half, 4 KB on
+    };
+    // one group of four tokens from ring buffer BUF, group TG
+    auto group = [&](auto buf_c, auto tg_c, int mg) {
+        constexpr int BUF = decltype(buf_c)::value, TG = decltype(tg_c)::value;
+        float xs[4], rr[4], zz[4];
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const int m = min(mg + mm, m_end - 1);
+            const float4 xv = load_uniform4(a.xrec + (size_t)m * a.Kp + k);
+            xs[mm] = xv.x;
+            rr[mm] = xv.y;
+            zz[mm] = xv.z;
+        }
+        // per token, r*sum(G L_D) - r^2/V_sat*sum(G L_I) as sum(G r (L_D + z L_I)), z = -r/V_sat
+        float tv[4];
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) tv[mm] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            // the slot's reads: I and D records of four tokens, and their G quad
+            float cc[4];
+            float2 ei[4], ed[4];
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+                cc[mm] = xs[mm] - ws[s];
+                const unsigned i = (unsigned)cc[mm];
+                ei[mm] = tab[i];
+                ed[mm] = tab[i + kRankDOffset];
+            }
+            const float4 q = *reinterpret_cast<const float4*>(smem + goff[s] + (BUF * 2 + TG) * kRankGroupBytes);
+            const float qv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+                const float li = fmaf(cc[mm], ei[mm].y, ei[mm].x);
+                const float ld = fmaf(cc[mm], ed[mm].y, ed[mm].x);
+                const float gr = qv[mm] * rr[mm];
+                if (NEED_W) acc[s] = fmaf(gr, ld, acc[s]);
+                tv[mm] = fmaf(gr, fmaf(zz[mm], li, ld), tv[mm]);
+            }
+            // the slot's dVth sum is formed here: left to itself the compiler sinks the chain
+            // to the end of the group and keeps every (G r, L_D) pair live until then
+            if (NEED_W) asm volatile("" : "+v"(acc[s]));
+        }
+        // summed over the wave (row r: token r)
+        const float sum = wave_sum_rows4(tv[0], tv[1], tv[2], tv[3]);
+        if ((lane & 15) == 0 && mg + row_tok < m_end && k < a.K) dxp[(size_t)(mg - m_begin) * a.K] = sum;
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+
+    float4 gv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (stager) gv = gload(m_begin);
+    __syncthreads();  // the table halves are in place
+    if (stager) gstore(0, gv);
+    __syncthreads();
+    // chunks alternate between the ring's two buffers; the next chunk's G loads are in flight
+    // while this one is evaluated, and stored after it (one barrier per chunk)
+    for (int m0 = m_begin; m0 < m_end; m0 += 2 * kRankChunk) {
+        bool more = m0 + kRankChunk < m_end;
+        if (more && stager) gv = gload(m0 + kRankChunk);
+        if (active) {
+            group(I0{}, I0{}, m0);
+            group(I0{}, I1{}, m0 + 4);
+        }
+        if (more && stager) gstore(1, gv);
+        __syncthreads();
+        if (!more) break;
+        const int m1 = m0 + kRankChunk;
+        more = m1 + kRankChunk < m_end;
+        if (more && stager) gv = gload(m1 + kRankChunk);
+        if (active) {
+            group(I1{}, I0{}, m1);
+            group(I1{}, I1{}, m1 + 4);
+        }
+        if (more && stager) gstore(0, gv);
+        __syncthreads();
+        if (!more) break;
+    }
+    if (NEED_W && active) {
+        const size_t q = ((size_t)k * a.n_ob + ob) * 64 + lane;
+        const unsigned pk = branch[q];
+        float* plane = a.dv_part + (size_t)sp * 2 * a.Kp * a.Op + (size_t)k * a.Op + (size_t)ob * 256 + c;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const unsigned t = (pk >> (4 * s)) & 7u, sg = (pk >> (4 * s + 3)) & 1u;
+            plane[(size_t)sg * a.Kp * a.Op + 32u * t] = sg ? -acc[s] : acc[s];
+        }
+    }
 }
 
 // ----------------------------------------------------------------------------------
@@ -2606,9 +2893,12 @@ struct BwdPlan {
     bool dv_group;
     bool grad_padded, split, lane_red, gtab, halves;
     bool copies;  // at least ISA_EKV_OPT_COPY_MIN_CELLS cells: the second table copy may pay
+    bool ranked;  // the copies' launches may include the ranked backward (its branch-deal arrays)
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
-        bytes, lds_bytes;
+        off_rank_ws, off_rank_branch, bytes, lds_bytes;
 };
+
+bool bwd_may_use_copies(const BwdPlan& p, bool exact, bool need_x);
 
 // n_entries = 0 plans the exact-formula backward (no LDS table, general-loop records).
 // glue: the layer backward (G_eff always written [M][Op], plus the glue partial sums).
@@ -2751,6 +3041,12 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
         off += (size_t)round_up((int64_t)kGlueBlocks * 2 * p.Op * 4, 256) +
                (size_t)round_up((int64_t)kGlueBlocks * (p.Op / 256) * 4, 256) +
                (size_t)round_up(kDxReduceBlocks * 8, 256);
+    // the ranked backward rides with the copies' launch pair (decided on the device)
+    p.ranked = bwd_may_use_copies(p, exact, need_x) && kBwdORR == 4 && g_ranked.load(std::memory_order_relaxed) != 0;
+    p.off_rank_ws = off;
+    if (p.ranked) off += (size_t)round_up(p.Kp * p.n_ob * 64 * 8 * 4, 256);
+    p.off_rank_branch = off;
+    if (p.ranked) off += (size_t)round_up(p.Kp * p.n_ob * 64 * 4, 256);
     p.bytes = round_up((int64_t)off, 256);
     return p;
 }
@@ -3233,7 +3529,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
                                dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials,
                                fa.NP, fa.copy_window > 0 ? fa.copy_window : fa.NP, mode, p.Kp, p.Op,
-                               tc.copy_offset);
+                               tc.copy_offset, 0);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward copy assignment launch");
         }
@@ -3387,17 +3683,25 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     const bool copies = bwd_may_use_copies(p, cs.exact, need_x);
     if (copies) {
         int* mode = reinterpret_cast<int*>(ws + p.off_mode);
+        if (p.ranked) {  // the branch deal first: it records the ranked mode when that launch works
+            const RankArgs ra{reinterpret_cast<const float2*>(ws + p.off_wsT),
+                              reinterpret_cast<float*>(ws + p.off_rank_ws),
+                              reinterpret_cast<unsigned*>(ws + p.off_rank_branch), ba.partials, mode,
+                              (int)p.Kp, (int)p.Op, p.n_ob, ba.NP};
+            const int64_t threads = p.Kp * p.n_ob * 32;
+            hipLaunchKernelGGL(bwd_rank_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, ra);
+        }
         // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
         const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * (p.split ? 4 : 8);
         const dim3 agrid((unsigned)((problems + kAssignThreads - 1) / kAssignThreads));
         if (p.split)
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, agrid, dim3(kAssignThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
-                               p.Kp, p.Op, kBwdCopyOffset);
+                               p.Kp, p.Op, kBwdCopyOffset, p.ranked ? 1 : 0);
         else
             hipLaunchKernelGGL(fwd_copy_assign_kernel<16>, agrid, dim3(kAssignThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
-                               p.Kp, p.Op, kBwdCopyOffsetI);
+                               p.Kp, p.Op, kBwdCopyOffsetI, p.ranked ? 1 : 0);
         ba.copy_mode = mode;
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "backward copy assignment launch");
@@ -3406,8 +3710,18 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     prof_start(s, 1, &prof);
     if (p.halves)
         launch_backward_halves(need_x, need_w, grid, block, p.lds_bytes, s, ba);
-    else if (copies)
+    else if (copies) {
         launch_backward_copies(p.split, need_w, grid, block, p.lds_bytes, s, ba);
+        if (p.ranked) {
+            const dim3 rgrid((unsigned)(((p.Kp + kRankWaves - 1) / kRankWaves) * p.n_ob * p.n_split));
+            const float* rws = reinterpret_cast<const float*>(ws + p.off_rank_ws);
+            const unsigned* rbr = reinterpret_cast<const unsigned*>(ws + p.off_rank_branch);
+            if (need_w)
+                hipLaunchKernelGGL(bwd_ranked_kernel<true>, rgrid, dim3(kRankWaves * 64), kRankLds, s, ba, rws, rbr);
+            else
+                hipLaunchKernelGGL(bwd_ranked_kernel<false>, rgrid, dim3(kRankWaves * 64), kRankLds, s, ba, rws, rbr);
+        }
+    }
     else
         launch_backward(cs.exact, p.gtab, need_x, need_w, p.split, p.lane_red, grid, block, p.lds_bytes, s, ba);
     err = hipGetLastError();
@@ -4027,8 +4341,11 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
 }
 
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous) {
-    if (option != ISA_EKV_OPT_COPY_MIN_CELLS) return fail(ISA_EKV_EINVAL, "unknown option %d", option);
-    const int64_t old = value >= 0 ? g_copy_min_cells.exchange(value) : g_copy_min_cells.load();
+    std::atomic<int64_t>* opt = option == ISA_EKV_OPT_COPY_MIN_CELLS ? &g_copy_min_cells
+                                : option == ISA_EKV_OPT_RANKED      ? &g_ranked
+                                                                    : nullptr;
+    if (!opt) return fail(ISA_EKV_EINVAL, "unknown option %d", option);
+    const int64_t old = value >= 0 ? opt->exchange(value) : opt->load();
     if (previous) *previous = old;
     return 0;
 }

@@ -28,6 +28,7 @@ PLAN_LAYER_BACKWARD = 2
 PLAN_INFO_LEN = 8
 NOALLOC_MAX_BYTES = 64 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
 OPT_COPY_MIN_CELLS = 1
+OPT_RANKED = 2
 
 EXPORTS = (
     "isa_ekv_abi_version",

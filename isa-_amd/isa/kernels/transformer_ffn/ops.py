@@ -84,9 +84,20 @@ def copy_min_cells(value: Optional[int] = None) -> int:
     return int(prev.value)
 
 
+def ranked_backward(value: Optional[bool] = None) -> bool:
+    """The library's ISA_EKV_OPT_RANKED (whether table backwards that consider the second copy
+    may run the ranked kernel); sets it when value is given. Returns the value before the call."""
+    lib = _hip.load()
+    prev = ctypes.c_int64()
+    rc = lib.isa_ekv_set_option(_hip.OPT_RANKED, -1 if value is None else int(bool(value)), ctypes.byref(prev))
+    _hip.check(rc, "isa_ekv_set_option")
+    return bool(prev.value)
+
+
 def copy_mode(workspace: torch.Tensor, plan: dict) -> Optional[int]:
-    """After a call that used `workspace` (and synchronised), whether its main kernel ran with
-    the second table copy (1) or one copy (0); None when the plan has no second copy."""
+    """After a call that used `workspace` (and synchronised), which table mode its main kernel
+    ran in: 1 the second table copy, 0 one copy, 2 the ranked backward; None when the plan has
+    no second copy."""
     off = plan["mode_offset"]
     if off < 0:
         return None

@@ -19,8 +19,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(x, vp, vn, g, cfg, dev, modes=None):
-    """Forward and backward through the C ABI; modes (a dict) receives the table-copy mode each
-    main kernel ran in (1 two copies, 0 one copy, None no second copy in the plan)."""
+    """Forward and backward through the C ABI; modes (a dict) receives the table mode each main
+    kernel ran in (1 two copies, 0 one copy, 2 the ranked backward, None no second copy in the
+    plan)."""
     from isa.approximations.delta_lut import get_packed_tables, lut_range
     from isa.kernels.transformer_ffn import ops
 
@@ -63,7 +64,8 @@ def test_headline_ffn_layers(cuda_device):
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=0))
     modes = {}
     res1 = _run(x, vp, vn, g, cfg, cuda_device, modes)
-    assert modes == {"fwd": 0, "bwd": 0}, modes  # the initial thresholds span ~69 records: one copy
+    # the initial thresholds span ~69 records: one forward copy; the backward runs ranked
+    assert modes == {"fwd": 0, "bwd": 2}, modes
     _check_samples(x, vp, vn, g, res1, cfg, rng)
     # fc2 is driven by the TIA output of fc1: clamp(R_TIA * Idiff, -4, 4) (cim.py:192-193)
     x2 = (res1[0] * 1e5).clamp(-4.0, 4.0).contiguous()
@@ -81,11 +83,19 @@ def test_headline_ffn_layers(cuda_device):
 
 
 def test_headline_equal_threshold_invariant(cuda_device):
+    """vth_pos == vth_neg: exactly zero Idiff, dVth+ == -dVth- bitwise, and dX zero to rounding
+    (the ranked backward, which runs here, sums an output's + and - branches in separate slots:
+    bounded by 1e-6 of the dX magnitude of the same inputs with distinct thresholds)."""
     cfg = flash_cfg(4096)
-    x, vp, _, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=5))
-    out, gx, gp, gn = _run(x, vp, vp, g, cfg, cuda_device)
-    assert torch.count_nonzero(out) == 0 and torch.count_nonzero(gx) == 0
+    x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=5))
+    modes = {}
+    out, gx, gp, gn = _run(x, vp, vp, g, cfg, cuda_device, modes)
+    assert modes["bwd"] == 2, modes
+    assert torch.count_nonzero(out) == 0
     assert torch.equal(gp, -gn)
+    scale = float(_run(x, vp, vn, g, cfg, cuda_device)[1].abs().max())
+    print(f"max |dX| {float(gx.abs().max()):.3e} of dX scale {scale:.3e}")
+    assert float(gx.abs().max()) <= 1e-6 * scale
 
 
 @pytest.mark.parametrize("size,vth_mode", [(8192, "init"), (4096, "full"), (16384, "init")])
@@ -102,8 +112,12 @@ def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=7, vth_mode=vth_mode))
     modes = {}
     res = _run(x, vp, vn, g, cfg, cuda_device, modes)
-    expect = None if size > 8192 else 1  # 16384 entries: no LDS room for a second copy
-    assert modes == {"fwd": expect, "bwd": expect}, modes
+    # 16384 entries: no LDS room for a second copy; otherwise the forward holds two copies, and
+    # the backward runs ranked at the initial thresholds (135 records) and with two copies at the
+    # wide spread (1576 records, past the ranked kernel's 256)
+    expect = ({"fwd": None, "bwd": None} if size > 8192 else
+              {"fwd": 1, "bwd": 2} if vth_mode == "init" else {"fwd": 1, "bwd": 1})
+    assert modes == expect, modes
     _check_samples(x, vp, vn, g, res, cfg, rng)
     again = _run(x, vp, vn, g, cfg, cuda_device)
     for a, b in zip(res, again):

@@ -34,8 +34,9 @@ def _small_calls_consider_table_copies():
 
 
 def _dev_run(x, vp, vn, grad, cfg, dev, need_x=True, need_w=True, out_min=-4.0, out_max=4.0, modes=None):
-    """Forward and backward through the C ABI. modes: a dict that receives the table-copy mode
-    each main kernel ran in ("fwd", "bwd": 1 two copies, 0 one copy, None no second copy)."""
+    """Forward and backward through the C ABI. modes: a dict that receives the table mode each
+    main kernel ran in ("fwd", "bwd": 1 two copies, 0 one copy, 2 the ranked backward, None no
+    second copy)."""
     from isa.approximations.delta_lut import get_packed_tables, lut_range
     from isa.kernels.transformer_ffn import ops
 
@@ -162,9 +163,11 @@ def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
     too wide a window as well."""
     print(f"[case] 8192 entries {x_mode}/{vth_mode}", flush=True)
     cfg = flash_cfg(8192)
-    # the windowed copies are taken exactly when the coordinates reach a window that fits
-    # (mapped inputs, initial thresholds); the other cases must run one copy
-    expect = 1 if (x_mode, vth_mode) == ("mapped", "init") else 0
+    # the windowed forward copies and the ranked backward are taken exactly when the
+    # coordinates reach a window that fits (mapped inputs, initial thresholds); the other cases
+    # must run one copy
+    fit = (x_mode, vth_mode) == ("mapped", "init")
+    expect = {"fwd": 1, "bwd": 2} if fit else {"fwd": 0, "bwd": 0}
     # (64, 203, 300): K % 8 != 0, so padded inputs k >= K run inside the windowed copies
     for M, K, O in ((64, 200, 300), (40, 768, 256), (64, 203, 300)):
         print(f"[case] 8192 entries {x_mode}/{vth_mode} M={M} K={K} O={O}", flush=True)
@@ -175,7 +178,7 @@ def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
                                    modes=modes)
         e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
         print(modes, [f"{v:.2e}" for v in e])
-        assert modes == {"fwd": expect, "bwd": expect}, modes
+        assert modes == expect, modes
         assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (M, K, O, e)
         _, gx2, gp2, gn2 = _dev_run(x, vp, vn, g, cfg, cuda_device, need_x=True, need_w=False)
         assert torch.equal(gx2, gx)
@@ -216,14 +219,32 @@ def test_bitwise_determinism(cuda_device):
         assert torch.equal(u, v)
 
 
-def test_invariants_on_device(cuda_device):
-    """vth_pos == vth_neg gives exactly zero Idiff and dX, and dVth+ == -dVth-."""
+@pytest.mark.parametrize("ranked", [False, True])
+def test_invariants_on_device(cuda_device, ranked):
+    """vth_pos == vth_neg gives exactly zero Idiff, and dVth+ == -dVth- bitwise. dX is exactly
+    zero where each cell forms L_D(+) - L_D(-) (the one-copy kernel); the ranked backward sums
+    the + and - branches of an output in separate lanes and slots, so there dX vanishes to
+    rounding: bounded by 1e-6 of the dX magnitude of the same inputs with distinct thresholds."""
+    from isa.kernels.transformer_ffn import ops
+
     cfg = flash_cfg(4096)
-    x, vp, _, g = make_inputs(33, 50, 70, seed=2)
-    out, gx, gp, gn = _dev_run(x, vp, vp.clone(), g, cfg, cuda_device)
+    x, vp, vn, g = make_inputs(33, 50, 70, seed=2)
+    prev = ops.ranked_backward(ranked)
+    try:
+        modes = {}
+        out, gx, gp, gn = _dev_run(x, vp, vp.clone(), g, cfg, cuda_device, modes=modes)
+        _, gx_ref, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device)
+    finally:
+        ops.ranked_backward(prev)
+    assert modes["bwd"] == (2 if ranked else 0), modes
     assert torch.count_nonzero(out) == 0
-    assert torch.count_nonzero(gx) == 0
     assert torch.equal(gp, -gn)
+    if ranked:
+        scale = float(gx_ref.abs().max())
+        print(f"max |dX| {float(gx.abs().max()):.3e} of dX scale {scale:.3e}")
+        assert float(gx.abs().max()) <= 1e-6 * scale
+    else:
+        assert torch.count_nonzero(gx) == 0
 
 
 def test_nan_semantics(cuda_device):
