@@ -1588,10 +1588,9 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
     static_assert(kSplitRecords % 16 == 0 && kBwdCopyOffsetI % 16 == 8, "copy 1 eight bank quads away");
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
-    // which launch of a pair works: the copy assignment pass wrote the mode word. (Where the
-    // checks sit matters: reading anything before the table loop costs the one-copy split
-    // kernel ~10 VGPRs and with them its second block per CU, so it checks after the loop;
-    // the interleaved one runs one block per CU in any case and checks first.)
+    // which launch of the set works: the branch-deal and copy assignment passes wrote the mode
+    // word; the others exit before loading their table (the scalar load of the word costs no
+    // VGPRs: the one-copy kernels keep their 64-VGPR budget)
     int lo = 0, n_rec = a.NP;  // table records held: [lo, lo + n_rec)
     if constexpr (MODE == kBwdTwoCopies) {
         if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 1) return;
@@ -1602,7 +1601,7 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
             n_rec = min(n_rec, kSplitRecords);  // as the mode word's test: the window fits
         }
     }
-    if constexpr (MODE == kBwdOneCopy && !SPLIT)
+    if constexpr (MODE == kBwdOneCopy)
         if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
     stage_to_lds<8>(a.lut + lo, n_rec, [&](int i, float4 rec) {
         if constexpr (SPLIT) {
@@ -1624,8 +1623,6 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
     });
     __builtin_amdgcn_sched_barrier(0);  // the range loads after the table loads (VGPRs: one set live)
     const bool fast = coords_in_padded_range(a.partials, a.NP);
-    if constexpr (MODE == kBwdOneCopy && SPLIT)
-        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
     __syncthreads();
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
