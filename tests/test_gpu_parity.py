@@ -247,6 +247,36 @@ def test_invariants_on_device(cuda_device, ranked):
         assert torch.count_nonzero(gx) == 0
 
 
+@pytest.mark.parametrize("M,K,O", [(70, 129, 300), (40, 203, 520), (1, 3000, 5), (96, 40, 768), (333, 768, 256)])
+def test_ranked_matches_one_copy(cuda_device, M, K, O):
+    """The ranked backward re-deals each input's branches to lanes in threshold rank but sums
+    dVth+- from the same products in the same token order as the one-copy kernel: on the same
+    plan (token splits) its dVth are bitwise those of the one-copy kernel (a dropped,
+    repeated or mis-signed branch would show here), and its dX, summed in rank order, agrees
+    to rounding. Both are checked against the oracle as well."""
+    from isa.kernels.transformer_ffn import ops
+
+    print(f"[case] ranked vs one copy M={M} K={K} O={O}", flush=True)
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = make_inputs(M, K, O, seed=M + 3 * K)
+    res = {}
+    for ranked in (True, False):
+        prev = ops.ranked_backward(ranked)
+        try:
+            modes = {}
+            res[ranked] = _dev_run(x, vp, vn, g, cfg, cuda_device, modes=modes)
+        finally:
+            ops.ranked_backward(prev)
+        assert modes["bwd"] == (2 if ranked else 0), (ranked, modes)
+    (_, dx_r, gp_r, gn_r), (_, dx_1, gp_1, gn_1) = res[True], res[False]
+    assert torch.equal(gp_r, gp_1) and torch.equal(gn_r, gn_1)
+    e = errs(dx_r, dx_1.cpu().numpy())[0]
+    print(f"dX ranked vs one copy {e:.2e}")
+    assert e <= 1e-6
+    _, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg)
+    assert max(errs(dx_r, ref_dx)[0], errs(gp_r, ref_gp)[0], errs(gn_r, ref_gn)[0]) <= BWD_TOL
+
+
 def test_nan_semantics(cuda_device):
     """NaN x: r is NaN so its cells are NaN and the NaN row sum clamps to out_min (fminf/fmaxf);
     NaN vth reads table entry 0 like ekv_cuda.cu:19-21. Same rules as the oracle."""
