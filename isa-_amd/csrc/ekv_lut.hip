@@ -1723,7 +1723,10 @@ struct RankArgs {
 // Thresholds spread over more table records than this leave a rank's window across 32 classes
 // hundreds of records wide; there the second table copy does better (measured at U[0, 5] V,
 // 1576 records: 13.5 ms ranked against 12.4 ms with two copies per GPT-L launch).
-constexpr float kRankMaxSpread = 256.0f;
+#ifndef ISA_EKV_RANK_MAX_SPREAD
+#define ISA_EKV_RANK_MAX_SPREAD 256
+#endif
+constexpr float kRankMaxSpread = (float)ISA_EKV_RANK_MAX_SPREAD;
 
 // Whether the ranked launch works (wave-uniform): the clamp-free loop, thresholds spread over at
 // most kRankMaxSpread records, and a coordinate window that fits the launch's table halves.
