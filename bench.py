@@ -375,7 +375,10 @@ def lds_roofline(model, cfg: dict, cells_launch: float, fwd_ms: float, bwd_ms: f
     their indices spread over the window the thresholds of the wave's outputs span,
     (max - min of vth) / LUT step records. isa_ekv_probe_lds_gather measures the time per
     random b64 gather at that window on this GPU (bank conflicts included), which gives
-    the kernels' LDS-bound launch times."""
+    the LDS-bound launch times of a kernel that reads one table copy with the lanes in
+    output order. The kernels beat that rate where they spread a gather over the banks (the
+    forward's windowed table copies, the ranked backward), so those fractions can pass 1;
+    the conflict-free rate (one record per bank pair) bounds both."""
     import math
 
     import torch
@@ -411,6 +414,8 @@ def lds_roofline(model, cfg: dict, cells_launch: float, fwd_ms: float, bwd_ms: f
         "conflict_free_frac": {"forward": round(fwd_free / fwd_ms, 4) if fwd_ms else None,
                                "backward": round(bwd_free / bwd_ms, 4) if bwd_ms else None},
         "work": "forward 2, backward 4 random ds_read_b64 gathers per cell-eval (wave-level: per 64 cells); "
+                "forward/backward_frac price them at the one-copy random rate of the window (the windowed "
+                "forward copies and the ranked backward conflict less, so these can pass 1); "
                 "conflict_free_frac prices them at the probe's W = 32 rate (one record per bank pair)",
         "_clock": clock,
     }
@@ -442,6 +447,9 @@ def main() -> int:
     ap.add_argument("--no-ranked", action="store_true",
                     help="plan the table backwards without the ranked kernel (isa_ekv_set_option "
                          "ISA_EKV_OPT_RANKED = 0): the one- or two-copy kernel runs instead")
+    ap.add_argument("--fwd-copies", type=int, default=None,
+                    help="the most windowed table copies a LUT forward may hold (isa_ekv_set_option "
+                         "ISA_EKV_OPT_FWD_COPIES: 4, 8, 16 or 32, default 16; 0 none)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -464,6 +472,10 @@ def main() -> int:
         from isa.kernels.transformer_ffn import ops
 
         ops.ranked_backward(False)
+    if args.fwd_copies is not None:
+        from isa.kernels.transformer_ffn import ops
+
+        ops.forward_copies(args.fwd_copies)
     if args.config == "gptl_train":
         return gpt_train_step(args)
     if args.config == "measured_fc1":
@@ -613,12 +625,13 @@ def main() -> int:
         "frac": round(achieved / peak, 4),
         "traffic": None if exact else measured_traffic(args.config)[0],
         "traffic_source": None if exact else measured_traffic(args.config)[1],
-        "kernel": ("bwd_exact_kernel<true,true>" if exact else "bwd_kernel<true,true,true,true>")
-                  + " (backward main kernel, dominant)",
+        "kernel": ("bwd_exact_kernel<true,true> (backward main kernel, dominant)" if exact else
+                   "table backward main kernel, dominant: bwd_ranked_kernel<true> where the ranked mode applies "
+                   "(the initial thresholds), else bwd_kernel / bwd_two_copies_kernel"),
         "work": f"{bwd_instr} VALU lane-instr per cell-eval x {cells_launch:.4e} cells per launch",
         "avg_launch_ms": round(bwd_avg, 4),
         "forward_kernel": {
-            "kernel": ("fwd_exact_kernel" if exact else "fwd_kernel")
+            "kernel": ("fwd_exact_kernel" if exact else "fwd_kernel (windowed table copies where they fit)")
                       + " (with split_reduce_kernel where the plan splits K)",
             "avg_launch_ms": round(fwd_avg, 4),
             "achieved": round(fwd_cells_s * fwd_instr / 1e12, 3),

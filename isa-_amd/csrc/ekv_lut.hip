@@ -130,6 +130,12 @@ std::atomic<int64_t> g_copy_min_cells{(int64_t)1 << 28};
 // Planning option ISA_EKV_OPT_RANKED: whether table backwards may run the ranked kernel.
 std::atomic<int64_t> g_ranked{1};
 
+// Planning option ISA_EKV_OPT_FWD_COPIES: the most bank-rotated copies of the coordinate
+// window a LUT forward may hold (4, 8, 16 or 32; below 4 the forward never holds them). At the
+// headline's narrow fc2 window 8, 16 and 32 copies run the forward in the same time within
+// 1%, and the assignment pass costs ~10 us more per doubling: 16.
+std::atomic<int64_t> g_fwd_copies{16};
+
 bool copies_pay(int64_t M, int64_t K, int64_t O) {
     return (double)M * (double)K * (double)O >= (double)g_copy_min_cells.load(std::memory_order_relaxed);
 }
@@ -859,6 +865,7 @@ struct FwdArgs {
     float* split_part;
     int copy_offset;        // LUT: T1 > 0 when the launch may use the second table copy
     int copy_window;        // LUT: > 0: the copies hold only the coordinate window, of at most this many records
+    int mc_budget, mc_max;  // LUT: mc_budget > 0: the launch may hold up to mc_max windowed copies in this many LDS records
 };
 
 // The work of one forward wave.
@@ -1090,8 +1097,11 @@ __device__ inline bool launch_copy_mode(const float2* __restrict__ partials, int
 }
 
 // Mode word values: 0 one table copy, 1 the second copy, kModeRanked the ranked backward (whose
-// branch-deal pass runs before the copy assignment and records its decision first).
+// branch-deal pass runs before the copy assignment and records its decision first), and in a
+// forward, C >= 4: C bank-rotated copies of the coordinate window (fwd_multi_assign_kernel,
+// which also runs before the two-copy assignment).
 constexpr int kModeRanked = 2;
+constexpr int kModeMultiMin = 4;
 
 // LANES = 32: 8-byte records, gathered by half-waves over 32 bank pairs; LANES = 16: 16-byte
 // records, gathered by quarter-waves over 16 bank quads. Copy 1 sits LANES / 2 bins away.
@@ -1102,12 +1112,13 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
                                                               const float2* __restrict__ partials, int NP,
                                                               int max_window, int* __restrict__ mode_word,
                                                               int64_t Kp, int64_t Op, int copy_offset,
-                                                              int after_rank) {
+                                                              int skip_from) {
     static_assert(LANES == 32 || LANES == 16, "half-wave or quarter-wave gathers");
     constexpr int kGroups = 64 / LANES, kMask = LANES - 1;
-    // a backward whose branch-deal pass chose the ranked launch keeps that mode (this pass
-    // never writes kModeRanked, so every block reads the same decision)
-    if (after_rank && __builtin_amdgcn_readfirstlane(*mode_word) == kModeRanked) return;
+    // skip_from > 0: a pass earlier in the call recorded a mode of its own (the ranked backward,
+    // skip_from = kModeRanked; the forward's windowed copies, skip_from = kModeMultiMin), which
+    // this call keeps (this pass writes only 0 or 1, so every block reads the same decision)
+    if (skip_from > 0 && __builtin_amdgcn_readfirstlane(*mode_word) >= skip_from) return;
     const bool on = launch_copy_mode(partials, NP, max_window);
     if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = on ? 1 : 0;
     if (!on) return;
@@ -1155,6 +1166,221 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
     }
 }
 
+// LUT forward with C bank-rotated copies of the coordinate window (C = 4, 8, 16 or 32), the
+// generalisation of the second copy that also pays at narrow spreads. Copy c holds the
+// window's records at LDS record c * stride (stride = the window rounded up to 32 records,
+// plus 32 / C), so its bank pairs sit c * 32 / C from copy 0's; a threshold that takes copy c
+// is stored as ws - c * stride and copy c's records as {A - c stride dT, dT}, as for the
+// second copy. A launch takes the most copies (up to the host's maximum) whose layout fits
+// its LDS allocation, when the clamp-free loop runs: the assignment pass and the forward
+// kernel decide it from the same range partials.
+struct MultiLayout {
+    int copies, stride, lo, n;  // copies == 0: not in this mode
+};
+
+// The clamp-free loop's condition (coords_in_padded_range) on a range already read.
+__device__ inline bool clamp_free(const CoordRange& c, int NP) {
+    return __builtin_amdgcn_readfirstlane((int)((c.xlo - c.whi >= 1.0f) && (c.xhi - c.wlo <= (float)(NP - 2)))) != 0;
+}
+
+__device__ inline MultiLayout fwd_multi_layout(const CoordRange& cr, int NP, int budget, int max_copies) {
+    MultiLayout m{0, 0, 0, NP};
+    if (max_copies < kModeMultiMin || !clamp_free(cr, NP)) return m;
+    coord_window(cr, NP, m.lo, m.n);
+    const int r = (m.n + 31) & ~31;
+    for (int c = 32; c >= kModeMultiMin; c >>= 1) {
+        const int stride = r + 32 / c;
+        if (c <= max_copies && (c - 1) * stride + m.n <= budget) {
+            m.copies = c;
+            m.stride = stride;
+            break;
+        }
+    }
+    return m;
+}
+
+// Copy choice for the windowed copies. A problem is the 32 thresholds one half-wave gather
+// reads (as in fwd_copy_assign_kernel<32>: input k, sign, output slot j, half of an output
+// block); kMcGroup threads share it, each pricing C / kMcGroup of the copies. The thresholds
+// are taken in increasing order, so that lanes reading one record for a token follow each
+// other. At kMultiSamples token-coordinate fractions f_q = (q + 1/2) / kMultiSamples, a
+// threshold w = W + g reads record floor(u) - W - [f_q < g] for a token at u: bank pair
+// -W - [f_q < g] plus the copy's rotation, up to the common floor(u). Each threshold takes the
+// copy that least raises the sum over the samples of the squared number of distinct records
+// per bank pair (nothing at a sample where the copy already holds the threshold's record), a
+// surrogate of the half-wave's conflict degree, with the number of records per bank pair and
+// sample kept as two bit planes (one record or more, two or more: the increase 2 n + 1 is
+// priced with n capped at 2). On uniform thresholds over a 68-record window it lowers the
+// expected conflict degree from 2.21 (one copy) to 1.97 (4 copies), 1.84 (8) and 1.51 (32).
+constexpr int kMultiSamples = 8;  // one bit per sample in the bit planes
+constexpr int kMcProblems = 64;   // problems per assignment block
+constexpr int kMcGroup = 4;       // threads per problem
+constexpr int kMcThreads = kMcProblems * kMcGroup;
+
+// s_pe[i][problem], i in [0, 64): bank pair b = i % 32's planes (bits 0-7 one record or more
+// per sample, bits 8-15 two or more) in the low half and bank pair b - 1's in the high half,
+// stored twice so that copy c's pair for base bank b0 is entry b0 + c * 32 / C, unwrapped.
+// s_info[rank][problem]: the sorted threshold's base bank pair b0 = -W mod 32 (bits 0-4), its
+// samples reading the record below (bits 5-12), the samples whose record differs from the
+// previous threshold's (bits 13-20) and its lane (bits 21-25).
+template <int C>
+__device__ inline void multi_greedy(const float* s_sw, const unsigned* s_info, unsigned* s_pe, int prob, int sub,
+                                    bool active, float* w0, int64_t lane_stride, int stride) {
+    constexpr int kPer = C / kMcGroup;  // copies priced by this thread: c = sub + kMcGroup * i
+    constexpr int kRot = 32 / C;
+    static_assert(kPer >= 1 && kMcGroup == 4 && kMultiSamples == 8, "copies per thread; quads; a byte of samples");
+    unsigned held[kPer];  // bit q: copy c holds the current run's record at sample q
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) held[i] = 0u;
+    for (int it = 0; it < 32; ++it) {
+        const unsigned info = s_info[it * kMcProblems + prob];
+        const int b0 = (int)(info & 31u);
+        const unsigned lo = (info >> 5) & 0xffu, chg = (info >> 13) & 0xffu, hi = lo ^ 0xffu;
+        const unsigned m_all = (hi | lo << 16) * 0x101u;  // the samples' planes at b (hi) and b - 1 (lo)
+        const unsigned* pe = s_pe + b0 * kMcProblems + prob;
+        unsigned v[kPer];
+        unsigned best = 0xffffffffu;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            held[i] &= ~chg;
+            v[i] = pe[((sub + kMcGroup * i) * kRot) * kMcProblems];
+            const unsigned x = v[i] & m_all & ~__builtin_amdgcn_perm(0u, held[i], 0u);  // unheld samples only
+            const unsigned cost = (unsigned)__builtin_popcount(held[i] ^ 0xffu) + 2u * (unsigned)__builtin_popcount(x);
+            best = min(best, cost << 5 | (unsigned)(sub + kMcGroup * i));
+        }
+        // the quad's minimum (ties: the lowest copy)
+        best = min(best, (unsigned)__builtin_amdgcn_update_dpp(0, (int)best, 0xb1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+        best = min(best, (unsigned)__builtin_amdgcn_update_dpp(0, (int)best, 0x4e, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+        const int bc = (int)(best & 31u), ib = bc / kMcGroup;
+        const bool own = bc % kMcGroup == sub;
+        unsigned vb = v[0], hb = held[0];
+#pragma unroll
+        for (int i = 1; i < kPer; ++i)
+            if (i == ib) vb = v[i], hb = held[i];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            if (own && i == ib) held[i] = 0xffu;  // copy bc now holds the threshold's records
+        if (own) {
+            const unsigned mh = hi & ~hb, ml = lo & ~hb;
+            const unsigned add_b = mh | (mh & vb) << 8;          // bank pair b*
+            const unsigned add_m = ml | (ml & (vb >> 16)) << 8;  // bank pair b* - 1
+            const int bs = (b0 + bc * kRot) & 31;
+            const int bp = (bs + 1) & 31, bm = (bs + 31) & 31;
+            atomicOr(&s_pe[bs * kMcProblems + prob], add_b | add_m << 16);
+            atomicOr(&s_pe[(bs + 32) * kMcProblems + prob], add_b | add_m << 16);
+            atomicOr(&s_pe[bp * kMcProblems + prob], add_b << 16);
+            atomicOr(&s_pe[(bp + 32) * kMcProblems + prob], add_b << 16);
+            atomicOr(&s_pe[bm * kMcProblems + prob], add_m);
+            atomicOr(&s_pe[(bm + 32) * kMcProblems + prob], add_m);
+            if (active && bc != 0)
+                w0[(int64_t)(info >> 21) * lane_stride] = s_sw[it * kMcProblems + prob] - (float)(bc * stride);
+        }
+        // the next threshold's reads of s_pe come after these updates (one wave: in order)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+// Samples f_q < g of a threshold w = W + g (they read the record below -W).
+__device__ inline unsigned multi_lo_mask(float w, float fl) {
+    const int nlo = min(kMultiSamples, max(0, (int)ceilf((w - fl) * (float)kMultiSamples - 0.5f)));
+    return (1u << nlo) - 1u;
+}
+
+// Block 0 records the launch's mode in the mode word: the number of copies, or 0 (the two-copy
+// pass that follows then decides between one and two copies).
+__global__ __launch_bounds__(kMcThreads) void fwd_multi_assign_kernel(float2* __restrict__ wsT,
+                                                          const float2* __restrict__ partials, int NP, int budget,
+                                                          int max_copies, int* __restrict__ mode_word, int64_t Kp,
+                                                          int64_t Op) {
+    const MultiLayout ml = fwd_multi_layout(read_coord_range(partials), NP, budget, max_copies);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = ml.copies;
+    if (ml.copies == 0) return;
+    __shared__ float s_sw[32 * kMcProblems];       // [rank][problem]: the thresholds in order
+    __shared__ unsigned s_info[32 * kMcProblems];  // [rank][problem] (multi_greedy)
+    __shared__ unsigned s_pe[64 * kMcProblems];    // bit planes (multi_greedy)
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 64 * kMcProblems; i += kMcThreads) s_pe[i] = 0u;
+    const int prob = tid / kMcGroup, sub = tid % kMcGroup;
+    constexpr int kGroups = 2;
+    const int64_t n_ot = Op / (64 * kFwdORR);
+    const int64_t p = (int64_t)blockIdx.x * kMcProblems + prob;
+    const bool active = p < Kp * n_ot * kFwdORR * 2 * kGroups;
+    const int sign = (int)(p & 1), group = (int)((p >> 1) % kGroups);
+    const int64_t rest0 = (p >> 1) / kGroups;
+    const int j = (int)(rest0 % kFwdORR);
+    const int64_t rest = rest0 / kFwdORR;
+    const int64_t tile = rest % n_ot, k = rest / n_ot;
+    const int64_t lane_stride = 2 * kFwdORR;  // floats between consecutive lanes' records
+    float* w0 = reinterpret_cast<float*>(wsT + k * Op + tile * 64 * kFwdORR + j) + sign + 32 * group * lane_stride;
+    // sort keys: order-preserving integer images of the thresholds (NaN included) with the lane
+    // in the low 5 bits, so that they are distinct (the order is then exact to 32 ulps)
+    auto sort_key = [](float w, int l) {
+        const int b = __float_as_int(w);
+        return ((b ^ ((b >> 31) & 0x7fffffff)) & ~31) | l;
+    };
+    int key[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) key[l] = sort_key(active ? w0[l * lane_stride] : 0.0f, l);
+#pragma unroll
+    for (int i = 0; i < 32 / kMcGroup; ++i) {  // this thread's lanes l = sub + kMcGroup * i
+        const int l = sub + kMcGroup * i;
+        const float wl = active ? w0[l * lane_stride] : 0.0f;
+        const int kl = sort_key(wl, l);
+        int rank = 0;
+#pragma unroll
+        for (int q = 0; q < 32; ++q) rank += key[q] < kl ? 1 : 0;
+        s_sw[rank * kMcProblems + prob] = wl;
+        s_info[rank * kMcProblems + prob] = (unsigned)l;
+    }
+    __syncthreads();
+    // per rank: base bank pair, low samples and the samples whose record changes from the
+    // previous rank's (a new run of equal records starts there)
+#pragma unroll
+    for (int i = 0; i < 32 / kMcGroup; ++i) {
+        const int r = sub + kMcGroup * i;
+        const float w = s_sw[r * kMcProblems + prob];
+        const float fl = floorf(w);
+        const int wi = (int)fl;
+        const unsigned lo = multi_lo_mask(w, fl);
+        unsigned chg = 0xffu;
+        if (r > 0) {
+            const float wp = s_sw[(r - 1) * kMcProblems + prob];
+            const float flp = floorf(wp);
+            const int wpi = (int)flp;
+            const unsigned lop = multi_lo_mask(wp, flp);
+            // record -W - [f_q < g] equals the previous one's where W + lo_q = W' + lo'_q
+            if (wi == wpi) chg = lo ^ lop;
+            else if (wi == wpi + 1) chg = 0xffu & ~(lop & ~lo);
+        }
+        const unsigned lane = s_info[r * kMcProblems + prob];
+        s_info[r * kMcProblems + prob] = (unsigned)((-wi) & 31) | lo << 5 | chg << 13 | lane << 21;
+    }
+    __syncthreads();
+    if (ml.copies == 32)
+        multi_greedy<32>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
+    else if (ml.copies == 16)
+        multi_greedy<16>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
+    else if (ml.copies == 8)
+        multi_greedy<8>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
+    else
+        multi_greedy<4>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
+}
+
+// The window's records [lo, lo + n) into LDS as the layout's copies (record i of copy c at
+// LDS record c * stride + i, holding {A - c stride dT, dT}).
+__device__ inline void stage_window_copies(float2* dst, const float2* __restrict__ src, int n, int copies,
+                                           int stride) {
+    const int total = n * copies;
+    for (int q = threadIdx.x; q < total; q += blockDim.x) {
+        const int c = q / n, i = q - c * n;
+        const float2 r = src[i];
+        const float t = (float)(c * stride);
+        dst[c * stride + i] = make_float2(fmaf(-t, r.y, r.x), r.y);
+    }
+}
+
 // The whole table (float2 records) into LDS, two records per 16-byte load when n is even.
 __device__ inline void stage_table2(float2* dst, const float2* __restrict__ src, int n) {
     if ((n & 1) == 0) {
@@ -1165,29 +1391,37 @@ __device__ inline void stage_table2(float2* dst, const float2* __restrict__ src,
     }
 }
 
-// WIN: the launch may hold two copies of only the coordinate window (tables whose two full
-// copies do not fit); the range is then read before the table load. Without WIN the load
-// comes first (reading the range first costs the 4096-entry kernels ~1%).
+// WIN: the launch may hold copies of only the coordinate window (the windowed copies, or two
+// copies of tables whose two full copies do not fit); the range is then read before the table
+// load. Without WIN the load comes first (reading the range first costs the 4096-entry kernels
+// ~1%).
 template <int MR, bool SPLITS, bool WIN = false>
 __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
     if constexpr (!WIN) stage_table2(s_lut_fwd, a.lut, a.NP);
     // fast loop and copy mode from one read of the range partials (as coords_in_padded_range,
-    // fwd_copies_mode and launch_copy_mode decide them; a second read costs the main loop
-    // ~50 VGPRs)
+    // fwd_copies_mode, launch_copy_mode and fwd_multi_layout decide them; a second read costs
+    // the main loop ~50 VGPRs)
     const CoordRange cr = read_coord_range(a.partials);
-    const bool fast = __builtin_amdgcn_readfirstlane(
-                          (int)((cr.xlo - cr.whi >= 1.0f) && (cr.xhi - cr.wlo <= (float)(a.NP - 2)))) != 0;
+    const bool fast = clamp_free(cr, a.NP);
     bool copies = fast && a.copy_offset > 0 &&
                   __builtin_amdgcn_readfirstlane((int)(cr.whi - cr.wlo >= kFwdCopyMinWindow)) != 0;
     int lo = 0, n_rec = a.NP;  // records held per copy: [lo, lo + n_rec)
     if constexpr (WIN) {
-        if (copies) {
-            coord_window(cr, a.NP, lo, n_rec);
-            copies = n_rec <= a.copy_window;
-            if (!copies) lo = 0, n_rec = a.NP;
+        const MultiLayout ml = fwd_multi_layout(cr, a.NP, a.mc_budget, a.mc_max);
+        if (ml.copies > 0) {
+            copies = false;
+            lo = ml.lo;
+            n_rec = ml.n;
+            stage_window_copies(s_lut_fwd, a.lut + lo, n_rec, ml.copies, ml.stride);
+        } else {
+            if (copies && a.copy_window > 0) {
+                coord_window(cr, a.NP, lo, n_rec);
+                copies = n_rec <= a.copy_window;
+                if (!copies) lo = 0, n_rec = a.NP;
+            }
+            if (!copies) stage_table2(s_lut_fwd, a.lut, a.NP);
         }
-        if (!copies) stage_table2(s_lut_fwd, a.lut, a.NP);
     }
     if (copies) {  // record i of copy 1 holds {A - T1 dT, dT}: fma(c + T1, dT, A') = fma(c, dT, A)
         const float t1 = (float)a.copy_offset;
@@ -3089,7 +3323,7 @@ void launch_forward_split(bool exact, bool gtab, int mr, int wpb, dim3 grid, siz
             hipLaunchKernelGGL((fwd_exact_kernel<2, SPLITS>), grid, block, 0, s, fa);
         return;
     }
-    if (fa.copy_window > 0) {
+    if (fa.copy_window > 0 || fa.mc_budget > 0) {
         if (mr == 8)
             hipLaunchKernelGGL((fwd_kernel<8, SPLITS, true>), grid, block, lds, s, fa);
         else if (mr == 4)
@@ -3432,6 +3666,7 @@ struct FwdTableCfg {
     bool gtab;  // table read from global memory
     size_t lds;
     int copy_offset, copy_window;
+    int mc_budget, mc_max;  // windowed copies (mc_budget > 0): LDS records of the allocation, most copies
 };
 
 FwdTableCfg fwd_table_cfg(int n_entries, int wpb, bool copies) {
@@ -3455,6 +3690,14 @@ FwdTableCfg fwd_table_cfg(int n_entries, int wpb, bool copies) {
     if (lds2 <= lds_cap) {
         t.copy_offset = t1;
         t.lds = lds2;
+    }
+    // the windowed copies, in an allocation of at least the block shape's share of the CU's
+    // LDS (the device takes as many copies as fit the launch's window)
+    const int64_t mc_max = std::min<int64_t>(g_fwd_copies.load(std::memory_order_relaxed), 32);
+    if (mc_max >= kModeMultiMin) {
+        t.lds = std::max(t.lds, lds_cap);
+        t.mc_budget = (int)(t.lds / 8);
+        t.mc_max = (int)mc_max;
     }
     return t;
 }
@@ -3523,13 +3766,24 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         lds = tc.lds;
         fa.copy_offset = tc.copy_offset;
         fa.copy_window = tc.copy_window;
+        fa.mc_budget = tc.mc_budget;
+        fa.mc_max = tc.mc_max;
+        int* mode = reinterpret_cast<int*>(ws + p.off_mode);
+        const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
+        const dim3 agrid((unsigned)((problems + kAssignThreads - 1) / kAssignThreads));
+        if (tc.mc_budget > 0) {
+            hipLaunchKernelGGL(fwd_multi_assign_kernel, dim3((unsigned)((problems + kMcProblems - 1) / kMcProblems)),
+                               dim3(kMcThreads), 0, s,
+                               reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials, fa.NP, tc.mc_budget,
+                               tc.mc_max, mode, p.Kp, p.Op);
+            err = hipGetLastError();
+            if (err != hipSuccess) return hip_fail(err, "forward windowed-copy assignment launch");
+        }
         if (tc.copy_offset > 0) {
-            int* mode = reinterpret_cast<int*>(ws + p.off_mode);
-            const int64_t problems = p.Kp * (p.Op / (64 * kFwdORR)) * kFwdORR * 4;
-            hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, dim3((unsigned)((problems + kAssignThreads - 1) / kAssignThreads)),
-                               dim3(kAssignThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials,
-                               fa.NP, fa.copy_window > 0 ? fa.copy_window : fa.NP, mode, p.Kp, p.Op,
-                               tc.copy_offset, 0);
+            hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, agrid, dim3(kAssignThreads), 0, s,
+                               reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials, fa.NP,
+                               fa.copy_window > 0 ? fa.copy_window : fa.NP, mode, p.Kp, p.Op, tc.copy_offset,
+                               tc.mc_budget > 0 ? kModeMultiMin : 0);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward copy assignment launch");
         }
@@ -3697,11 +3951,11 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         if (p.split)
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, agrid, dim3(kAssignThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
-                               p.Kp, p.Op, kBwdCopyOffset, p.ranked ? 1 : 0);
+                               p.Kp, p.Op, kBwdCopyOffset, p.ranked ? kModeRanked : 0);
         else
             hipLaunchKernelGGL(fwd_copy_assign_kernel<16>, agrid, dim3(kAssignThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
-                               p.Kp, p.Op, kBwdCopyOffsetI, p.ranked ? 1 : 0);
+                               p.Kp, p.Op, kBwdCopyOffsetI, p.ranked ? kModeRanked : 0);
         ba.copy_mode = mode;
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "backward copy assignment launch");
@@ -4315,7 +4569,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
         const FwdPlan p = plan_forward_call(false, n_entries, M, K, O);
         const FwdTableCfg tc = fwd_table_cfg(n_entries, p.wpb, copies_pay(M, K, O));
         v[0] = (int64_t)p.bytes;
-        v[1] = tc.copy_offset > 0 ? (int64_t)p.off_mode : -1;
+        v[1] = tc.copy_offset > 0 || tc.mc_budget > 0 ? (int64_t)p.off_mode : -1;
         v[2] = p.n_split;
         v[3] = p.mr;
         v[4] = p.blocks;
@@ -4343,6 +4597,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous) {
     std::atomic<int64_t>* opt = option == ISA_EKV_OPT_COPY_MIN_CELLS ? &g_copy_min_cells
                                 : option == ISA_EKV_OPT_RANKED      ? &g_ranked
+                                : option == ISA_EKV_OPT_FWD_COPIES  ? &g_fwd_copies
                                                                     : nullptr;
     if (!opt) return fail(ISA_EKV_EINVAL, "unknown option %d", option);
     const int64_t old = value >= 0 ? opt->exchange(value) : opt->load();

@@ -254,10 +254,20 @@ def test_plan_info_reports_the_call_plans():
     # 8192 entries, 768 inputs per wave: both copies in one 16-wave block per CU
     f8 = ops.plan_info("forward", 8192, 768, 3072, 8192)
     assert f8["waves_per_block"] == 16 and f8["mode_offset"] >= 0
-    # 16384 entries: one LDS copy in the forward, two half-table passes in the backward, no
-    # mode word
-    assert ops.plan_info("forward", 8192, 768, 3072, 16384)["mode_offset"] == -1
+    # 16384 entries: one LDS copy in the forward (whose allocation may hold windowed copies
+    # of a narrow enough coordinate window: a mode word), two half-table passes in the
+    # backward (no mode word)
+    f16 = ops.plan_info("forward", 8192, 768, 3072, 16384)
+    assert f16["mode_offset"] >= 0 and f16["lds_bytes"] == (16384 + 2 * 16) * 8
     assert ops.plan_info("backward", 8192, 768, 3072, 16384)["mode_offset"] == -1
+    # without windowed copies (ISA_EKV_OPT_FWD_COPIES < 4) the 16384-entry forward has no mode word
+    prev = ops.forward_copies(0)
+    try:
+        assert ops.plan_info("forward", 8192, 768, 3072, 16384)["mode_offset"] == -1
+        assert ops.forward_copies() == 0
+    finally:
+        ops.forward_copies(prev)
+    assert prev == 16
     # a dVth-only backward runs no copy pair
     assert ops.plan_info("backward", 512, 64, 256, 4096, need_grad_x=False)["mode_offset"] == -1
     info = (ctypes.c_int64 * 7)()

@@ -235,22 +235,24 @@ def run_physical_ffn(monkeypatch, dev, D, F, B, T, size, expect_modes, n_rows=48
 
 
 def test_config1_vitm_physical_ffn_4096(cuda_device, monkeypatch):
-    """configs[1] with the 4096-entry table: the initial thresholds span ~67 records, one
-    forward copy; the backward runs ranked."""
-    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 4096, ([0, 0], [2, 2]))
+    """configs[1] with the 4096-entry table: the initial thresholds span ~67 records; fc1's
+    mapped inputs reach a coordinate window of ~1400 records (four windowed forward copies fit
+    its LDS), fc2's TIA outputs a narrow one (sixteen); the backward runs ranked."""
+    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 4096, ([4, 16], [2, 2]))
 
 
 def test_config1_vitm_physical_ffn_8192(cuda_device, monkeypatch):
     """configs[1] with the vision default of 8192 entries: the initial thresholds span ~135
     records and both layers' inputs reach a coordinate window that fits (fc1's mapped inputs in
-    [0, 4] V, fc2's TIA outputs within a fraction of a volt of zero), so every forward holds
-    two bank-rotated copies of that window and every backward runs ranked on it."""
-    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 8192, ([1, 1], [2, 2]))
+    [0, 4] V, fc2's TIA outputs within a fraction of a volt of zero): fc1's forward holds two
+    bank-rotated copies of its ~2800-record window (four do not fit), fc2's sixteen of its
+    narrow one, and every backward runs ranked."""
+    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 8192, ([1, 16], [2, 2]))
 
 
 def test_config3_headline_physical_ffn(cuda_device, monkeypatch):
     """configs[3], the headline Physical GPT-L FFN at full size, exactly as bench.py runs it."""
-    run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([0, 0], [2, 2]))
+    run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([4, 16], [2, 2]))
 
 
 def test_config2_gptm_hybrid_ffn(cuda_device, monkeypatch):
@@ -271,7 +273,7 @@ def test_config2_gptm_hybrid_ffn(cuda_device, monkeypatch):
     out, xx = _step(ffn, x, g)
     fmodes, bmodes = spy.modes()
     print(f"[case] HybridFFN {D}->{F} + Linear x[{B},{T},{D}]: copy modes fwd {fmodes} bwd {bmodes}")
-    assert len(spy.fwd) == 1 and len(spy.bwd) == 1 and (fmodes, bmodes) == ([0], [2])
+    assert len(spy.fwd) == 1 and len(spy.bwd) == 1 and (fmodes, bmodes) == ([4], [2])
 
     M = B * T
     rng = np.random.default_rng(6)

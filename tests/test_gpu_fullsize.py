@@ -64,8 +64,9 @@ def test_headline_ffn_layers(cuda_device):
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=0))
     modes = {}
     res1 = _run(x, vp, vn, g, cfg, cuda_device, modes)
-    # the initial thresholds span ~69 records: one forward copy; the backward runs ranked
-    assert modes == {"fwd": 0, "bwd": 2}, modes
+    # the initial thresholds span ~69 records and the mapped inputs ~1350: the forward holds
+    # four windowed table copies (what fits its 80 KB of LDS); the backward runs ranked
+    assert modes == {"fwd": 4, "bwd": 2}, modes
     _check_samples(x, vp, vn, g, res1, cfg, rng)
     # fc2 is driven by the TIA output of fc1: clamp(R_TIA * Idiff, -4, 4) (cim.py:192-193)
     x2 = (res1[0] * 1e5).clamp(-4.0, 4.0).contiguous()
@@ -102,7 +103,7 @@ def test_headline_equal_threshold_invariant(cuda_device):
 def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     """The regimes where the kernels hold a second, bank-rotated table copy, at the headline
     fc1 shape: the 8192-entry table (its initial thresholds span ~135 records; the forward
-    runs both copies in one 16-wave block per CU, each wave summing all 768 inputs) and
+    runs its table copies in one 16-wave block per CU, each wave summing all 768 inputs) and
     thresholds spread over U[V_TH_MIN, V_TH_MAX] (forward copies, and the persistent
     two-copy backward); and the 16384-entry table (one 131 KB copy per CU in the forward, the
     backward from global memory), checked on sampled exact sub-problems."""
@@ -112,11 +113,13 @@ def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=7, vth_mode=vth_mode))
     modes = {}
     res = _run(x, vp, vn, g, cfg, cuda_device, modes)
-    # 16384 entries: no LDS room for a second copy; otherwise the forward holds two copies, and
-    # the backward runs ranked at the initial thresholds (135 records) and with two copies at the
-    # wide spread (1576 records, past the ranked kernel's 256)
-    expect = ({"fwd": None, "bwd": None} if size > 8192 else
-              {"fwd": 1, "bwd": 2} if vth_mode == "init" else {"fwd": 1, "bwd": 1})
+    # 16384 entries: no LDS room for a second copy (the forward's windowed-copy pass finds its
+    # window too wide and records one copy); 8192 entries at the initial thresholds: the forward
+    # holds four windowed copies in its 16-wave blocks, the backward runs ranked (135 records);
+    # the wide spread: two full forward copies and the two-copy backward (1576 records, past the
+    # ranked kernel's 256)
+    expect = ({"fwd": 0, "bwd": None} if size > 8192 else
+              {"fwd": 4, "bwd": 2} if vth_mode == "init" else {"fwd": 1, "bwd": 1})
     assert modes == expect, modes
     _check_samples(x, vp, vn, g, res, cfg, rng)
     again = _run(x, vp, vn, g, cfg, cuda_device)

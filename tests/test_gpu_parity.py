@@ -165,9 +165,9 @@ def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
     cfg = flash_cfg(8192)
     # the windowed forward copies and the ranked backward are taken exactly when the
     # coordinates reach a window that fits (mapped inputs, initial thresholds); the other cases
-    # must run one copy
+    # must run one copy. The forward holds two copies of the window, or four when its window
+    # (which these random inputs set) is short enough for four in its LDS
     fit = (x_mode, vth_mode) == ("mapped", "init")
-    expect = {"fwd": 1, "bwd": 2} if fit else {"fwd": 0, "bwd": 0}
     # (64, 203, 300): K % 8 != 0, so padded inputs k >= K run inside the windowed copies
     for M, K, O in ((64, 200, 300), (40, 768, 256), (64, 203, 300)):
         print(f"[case] 8192 entries {x_mode}/{vth_mode} M={M} K={K} O={O}", flush=True)
@@ -178,7 +178,10 @@ def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
                                    modes=modes)
         e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
         print(modes, [f"{v:.2e}" for v in e])
-        assert modes == expect, modes
+        if fit:
+            assert modes["bwd"] == 2 and modes["fwd"] in (1, 4), modes
+        else:
+            assert modes == {"fwd": 0, "bwd": 0}, modes
         assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (M, K, O, e)
         _, gx2, gp2, gn2 = _dev_run(x, vp, vn, g, cfg, cuda_device, need_x=True, need_w=False)
         assert torch.equal(gx2, gx)
