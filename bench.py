@@ -449,7 +449,7 @@ def main() -> int:
                          "ISA_EKV_OPT_RANKED = 0): the one- or two-copy kernel runs instead")
     ap.add_argument("--fwd-copies", type=int, default=None,
                     help="the most windowed table copies a LUT forward may hold (isa_ekv_set_option "
-                         "ISA_EKV_OPT_FWD_COPIES: 4, 8, 16 or 32, default 16; 0 none)")
+                         "ISA_EKV_OPT_FWD_COPIES: 3 to 32, default 16; 0 none)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")

@@ -281,7 +281,7 @@ int isa_ekv_profile_end(double* ms, int* launches);
  *   [0] workspace bytes
  *   [1] byte offset in the workspace of the table-copy mode word (int32: after the call, 1 when
  *       the main kernel ran with the second, bank-rotated table copy, 0 when with one copy,
- *       2 when the backward ran ranked: see ISA_EKV_OPT_RANKED, 4 to 32 when the forward held
+ *       2 when the backward ran ranked: see ISA_EKV_OPT_RANKED, 3 to 32 when the forward held
  *       that many windowed copies: see ISA_EKV_OPT_FWD_COPIES), or -1 when the call cannot
  *       use a second copy (the word is then not written)
  *   [2] forward: K ranges summed separately (1: no split); backward: token splits
@@ -306,11 +306,11 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *     the ranked backward instead, when their coordinates need no clamp and reach a window of
  *     at most 3008 table records (decided on the device; mode word 2): each wave's gathers
  *     then read thresholds dealt to lanes in rank order. 0 never runs it.
- *   ISA_EKV_OPT_FWD_COPIES: the most bank-rotated copies of the coordinate window (4, 8, 16 or
- *     32; default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
+ *   ISA_EKV_OPT_FWD_COPIES: the most bank-rotated copies of the coordinate window (3 to 32;
+ *     default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
  *     LDS when its coordinates need no clamp (decided on the device, which takes the most
  *     copies that fit; mode word = the number of copies): each threshold then reads the copy
- *     its assignment pass chose to spread a gather's records over the LDS banks. Below 4 the
+ *     its assignment pass chose to spread a gather's records over the LDS banks. Below 3 the
  *     forward never holds them.
  * Plans (and so workspace sizes) depend on the options: query workspace sizes after setting
  * them, and do not change them while calls are in flight. */

@@ -131,7 +131,7 @@ std::atomic<int64_t> g_copy_min_cells{(int64_t)1 << 28};
 std::atomic<int64_t> g_ranked{1};
 
 // Planning option ISA_EKV_OPT_FWD_COPIES: the most bank-rotated copies of the coordinate
-// window a LUT forward may hold (4, 8, 16 or 32; below 4 the forward never holds them). At the
+// window a LUT forward may hold (3 to 32; below 3 the forward never holds them). At the
 // headline's narrow fc2 window 8, 16 and 32 copies run the forward in the same time within
 // 1%, and the assignment pass costs ~10 us more per doubling: 16.
 std::atomic<int64_t> g_fwd_copies{16};
@@ -1098,10 +1098,11 @@ __device__ inline bool launch_copy_mode(const float2* __restrict__ partials, int
 
 // Mode word values: 0 one table copy, 1 the second copy, kModeRanked the ranked backward (whose
 // branch-deal pass runs before the copy assignment and records its decision first), and in a
-// forward, C >= 4: C bank-rotated copies of the coordinate window (fwd_multi_assign_kernel,
-// which also runs before the two-copy assignment).
+// forward, C >= kModeMultiMin: C bank-rotated copies of the coordinate window
+// (fwd_multi_assign_kernel, which also runs before the two-copy assignment).
 constexpr int kModeRanked = 2;
-constexpr int kModeMultiMin = 4;
+constexpr int kModeMultiMin = 3;
+constexpr int kMultiMax = 32;
 
 // LANES = 32: 8-byte records, gathered by half-waves over 32 bank pairs; LANES = 16: 16-byte
 // records, gathered by quarter-waves over 16 bank quads. Copy 1 sits LANES / 2 bins away.
@@ -1166,17 +1167,23 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
     }
 }
 
-// LUT forward with C bank-rotated copies of the coordinate window (C = 4, 8, 16 or 32), the
+// LUT forward with C bank-rotated copies of the coordinate window (3 <= C <= 32), the
 // generalisation of the second copy that also pays at narrow spreads. Copy c holds the
-// window's records at LDS record c * stride (stride = the window rounded up to 32 records,
-// plus 32 / C), so its bank pairs sit c * 32 / C from copy 0's; a threshold that takes copy c
-// is stored as ws - c * stride and copy c's records as {A - c stride dT, dT}, as for the
+// window's records from LDS record T_c = c * stride + floor(32 c / C) (stride = the window
+// rounded up to 32 records), so its bank pairs sit floor(32 c / C) from copy 0's; a threshold
+// that takes copy c is stored as ws - T_c and copy c's records as {A - T_c dT, dT}, as for the
 // second copy. A launch takes the most copies (up to the host's maximum) whose layout fits
 // its LDS allocation, when the clamp-free loop runs: the assignment pass and the forward
 // kernel decide it from the same range partials.
 struct MultiLayout {
     int copies, stride, lo, n;  // copies == 0: not in this mode
 };
+
+// Bank-pair rotation and first LDS record of copy c.
+__host__ __device__ inline int multi_rot(int c, int copies) { return c * 32 / copies; }
+__host__ __device__ inline int multi_offset(int c, int copies, int stride) {
+    return c * stride + multi_rot(c, copies);
+}
 
 // The clamp-free loop's condition (coords_in_padded_range) on a range already read.
 __device__ inline bool clamp_free(const CoordRange& c, int NP) {
@@ -1187,10 +1194,9 @@ __device__ inline MultiLayout fwd_multi_layout(const CoordRange& cr, int NP, int
     MultiLayout m{0, 0, 0, NP};
     if (max_copies < kModeMultiMin || !clamp_free(cr, NP)) return m;
     coord_window(cr, NP, m.lo, m.n);
-    const int r = (m.n + 31) & ~31;
-    for (int c = 32; c >= kModeMultiMin; c >>= 1) {
-        const int stride = r + 32 / c;
-        if (c <= max_copies && (c - 1) * stride + m.n <= budget) {
+    const int stride = (m.n + 31) & ~31;
+    for (int c = min(max_copies, kMultiMax); c >= kModeMultiMin; --c) {
+        if (multi_offset(c - 1, c, stride) + m.n <= budget) {
             m.copies = c;
             m.stride = stride;
             break;
@@ -1219,19 +1225,25 @@ constexpr int kMcThreads = kMcProblems * kMcGroup;
 
 // s_pe[i][problem], i in [0, 64): bank pair b = i % 32's planes (bits 0-7 one record or more
 // per sample, bits 8-15 two or more) in the low half and bank pair b - 1's in the high half,
-// stored twice so that copy c's pair for base bank b0 is entry b0 + c * 32 / C, unwrapped.
+// stored twice so that copy c's pair for base bank b0 is entry b0 + floor(32 c / C), unwrapped.
 // s_info[rank][problem]: the sorted threshold's base bank pair b0 = -W mod 32 (bits 0-4), its
 // samples reading the record below (bits 5-12), the samples whose record differs from the
 // previous threshold's (bits 13-20) and its lane (bits 21-25).
-template <int C>
+template <int kPer>  // copies priced by this thread: c = sub + kMcGroup * i < copies, i < kPer
 __device__ inline void multi_greedy(const float* s_sw, const unsigned* s_info, unsigned* s_pe, int prob, int sub,
-                                    bool active, float* w0, int64_t lane_stride, int stride) {
-    constexpr int kPer = C / kMcGroup;  // copies priced by this thread: c = sub + kMcGroup * i
-    constexpr int kRot = 32 / C;
-    static_assert(kPer >= 1 && kMcGroup == 4 && kMultiSamples == 8, "copies per thread; quads; a byte of samples");
+                                    bool active, float* w0, int64_t lane_stride, int copies, int stride) {
+    static_assert(kPer >= 1 && kPer * kMcGroup <= kMultiMax && kMcGroup == 4 && kMultiSamples == 8,
+                  "copies per thread; quads; a byte of samples");
     unsigned held[kPer];  // bit q: copy c holds the current run's record at sample q
+    int rot[kPer];        // copy c's bank-pair rotation
+    bool valid[kPer];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) held[i] = 0u;
+    for (int i = 0; i < kPer; ++i) {
+        const int c = sub + kMcGroup * i;
+        valid[i] = c < copies;
+        rot[i] = valid[i] ? multi_rot(c, copies) : 0;
+        held[i] = 0u;
+    }
     for (int it = 0; it < 32; ++it) {
         const unsigned info = s_info[it * kMcProblems + prob];
         const int b0 = (int)(info & 31u);
@@ -1243,10 +1255,10 @@ __device__ inline void multi_greedy(const float* s_sw, const unsigned* s_info, u
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             held[i] &= ~chg;
-            v[i] = pe[((sub + kMcGroup * i) * kRot) * kMcProblems];
+            v[i] = pe[rot[i] * kMcProblems];
             const unsigned x = v[i] & m_all & ~__builtin_amdgcn_perm(0u, held[i], 0u);  // unheld samples only
             const unsigned cost = (unsigned)__builtin_popcount(held[i] ^ 0xffu) + 2u * (unsigned)__builtin_popcount(x);
-            best = min(best, cost << 5 | (unsigned)(sub + kMcGroup * i));
+            if (valid[i]) best = min(best, cost << 5 | (unsigned)(sub + kMcGroup * i));
         }
         // the quad's minimum (ties: the lowest copy)
         best = min(best, (unsigned)__builtin_amdgcn_update_dpp(0, (int)best, 0xb1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
@@ -1254,9 +1266,10 @@ __device__ inline void multi_greedy(const float* s_sw, const unsigned* s_info, u
         const int bc = (int)(best & 31u), ib = bc / kMcGroup;
         const bool own = bc % kMcGroup == sub;
         unsigned vb = v[0], hb = held[0];
+        int rb = rot[0];
 #pragma unroll
         for (int i = 1; i < kPer; ++i)
-            if (i == ib) vb = v[i], hb = held[i];
+            if (i == ib) vb = v[i], hb = held[i], rb = rot[i];
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
             if (own && i == ib) held[i] = 0xffu;  // copy bc now holds the threshold's records
@@ -1264,7 +1277,7 @@ __device__ inline void multi_greedy(const float* s_sw, const unsigned* s_info, u
             const unsigned mh = hi & ~hb, ml = lo & ~hb;
             const unsigned add_b = mh | (mh & vb) << 8;          // bank pair b*
             const unsigned add_m = ml | (ml & (vb >> 16)) << 8;  // bank pair b* - 1
-            const int bs = (b0 + bc * kRot) & 31;
+            const int bs = (b0 + rb) & 31;
             const int bp = (bs + 1) & 31, bm = (bs + 31) & 31;
             atomicOr(&s_pe[bs * kMcProblems + prob], add_b | add_m << 16);
             atomicOr(&s_pe[(bs + 32) * kMcProblems + prob], add_b | add_m << 16);
@@ -1273,7 +1286,7 @@ __device__ inline void multi_greedy(const float* s_sw, const unsigned* s_info, u
             atomicOr(&s_pe[bm * kMcProblems + prob], add_m);
             atomicOr(&s_pe[(bm + 32) * kMcProblems + prob], add_m);
             if (active && bc != 0)
-                w0[(int64_t)(info >> 21) * lane_stride] = s_sw[it * kMcProblems + prob] - (float)(bc * stride);
+                w0[(int64_t)(info >> 21) * lane_stride] = s_sw[it * kMcProblems + prob] - (float)(bc * stride + rb);
         }
         // the next threshold's reads of s_pe come after these updates (one wave: in order)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1358,26 +1371,26 @@ __global__ __launch_bounds__(kMcThreads) void fwd_multi_assign_kernel(float2* __
         s_info[r * kMcProblems + prob] = (unsigned)((-wi) & 31) | lo << 5 | chg << 13 | lane << 21;
     }
     __syncthreads();
-    if (ml.copies == 32)
-        multi_greedy<32>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
-    else if (ml.copies == 16)
-        multi_greedy<16>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
-    else if (ml.copies == 8)
-        multi_greedy<8>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
+    if (ml.copies > 16)
+        multi_greedy<8>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.copies, ml.stride);
+    else if (ml.copies > 8)
+        multi_greedy<4>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.copies, ml.stride);
+    else if (ml.copies > 4)
+        multi_greedy<2>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.copies, ml.stride);
     else
-        multi_greedy<4>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.stride);
+        multi_greedy<1>(s_sw, s_info, s_pe, prob, sub, active, w0, lane_stride, ml.copies, ml.stride);
 }
 
 // The window's records [lo, lo + n) into LDS as the layout's copies (record i of copy c at
-// LDS record c * stride + i, holding {A - c stride dT, dT}).
+// LDS record T_c + i, holding {A - T_c dT, dT}).
 __device__ inline void stage_window_copies(float2* dst, const float2* __restrict__ src, int n, int copies,
                                            int stride) {
     const int total = n * copies;
     for (int q = threadIdx.x; q < total; q += blockDim.x) {
         const int c = q / n, i = q - c * n;
         const float2 r = src[i];
-        const float t = (float)(c * stride);
-        dst[c * stride + i] = make_float2(fmaf(-t, r.y, r.x), r.y);
+        const int t = multi_offset(c, copies, stride);
+        dst[t + i] = make_float2(fmaf(-(float)t, r.y, r.x), r.y);
     }
 }
 

@@ -96,7 +96,7 @@ def ranked_backward(value: Optional[bool] = None) -> bool:
 
 def forward_copies(value: Optional[int] = None) -> int:
     """The library's ISA_EKV_OPT_FWD_COPIES (the most windowed table copies a LUT forward may
-    hold: 4, 8, 16 or 32, default 16; below 4 none); sets it when value is given. Returns the value before
+    hold: 3 to 32, default 16; below 3 none); sets it when value is given. Returns the value before
     the call."""
     lib = _hip.load()
     prev = ctypes.c_int64()
@@ -107,7 +107,7 @@ def forward_copies(value: Optional[int] = None) -> int:
 
 def copy_mode(workspace: torch.Tensor, plan: dict) -> Optional[int]:
     """After a call that used `workspace` (and synchronised), which table mode its main kernel
-    ran in: 1 the second table copy, 0 one copy, 2 the ranked backward, 4 to 32 the forward's
+    ran in: 1 the second table copy, 0 one copy, 2 the ranked backward, 3 to 32 the forward's
     windowed copies (their number); None when the plan has no second copy."""
     off = plan["mode_offset"]
     if off < 0:

@@ -64,9 +64,9 @@ def test_headline_ffn_layers(cuda_device):
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=0))
     modes = {}
     res1 = _run(x, vp, vn, g, cfg, cuda_device, modes)
-    # the initial thresholds span ~69 records and the mapped inputs ~1350: the forward holds
-    # four windowed table copies (what fits its 80 KB of LDS); the backward runs ranked
-    assert modes == {"fwd": 4, "bwd": 2}, modes
+    # the initial thresholds span ~69 records and the mapped inputs ~1350: the forward holds as
+    # many windowed table copies as fit its 80 KB of LDS (about seven); the backward runs ranked
+    assert 3 <= modes["fwd"] <= 16 and modes["bwd"] == 2, modes
     _check_samples(x, vp, vn, g, res1, cfg, rng)
     # fc2 is driven by the TIA output of fc1: clamp(R_TIA * Idiff, -4, 4) (cim.py:192-193)
     x2 = (res1[0] * 1e5).clamp(-4.0, 4.0).contiguous()
@@ -113,14 +113,16 @@ def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     x, vp, vn, g = (t.to(cuda_device) for t in make_inputs(8192, 768, 3072, seed=7, vth_mode=vth_mode))
     modes = {}
     res = _run(x, vp, vn, g, cfg, cuda_device, modes)
-    # 16384 entries: no LDS room for a second copy (the forward's windowed-copy pass finds its
-    # window too wide and records one copy); 8192 entries at the initial thresholds: the forward
-    # holds four windowed copies in its 16-wave blocks, the backward runs ranked (135 records);
-    # the wide spread: two full forward copies and the two-copy backward (1576 records, past the
-    # ranked kernel's 256)
-    expect = ({"fwd": 0, "bwd": None} if size > 8192 else
-              {"fwd": 4, "bwd": 2} if vth_mode == "init" else {"fwd": 1, "bwd": 1})
-    assert modes == expect, modes
+    # 16384 entries: no LDS room for a second full copy; the forward holds three windowed copies
+    # in its one-copy allocation when its window is short enough, the backward reads the table
+    # from global memory (no mode). 8192 entries at the initial thresholds: the forward holds
+    # windowed copies in its 16-wave blocks, the backward runs ranked (135 records). The wide
+    # spread: windowed forward copies of a ~2900-record window (three fit), the two-copy
+    # backward (1576 records, past the ranked kernel's 256)
+    if size > 8192:
+        assert modes["bwd"] is None and (modes["fwd"] == 0 or 3 <= modes["fwd"] <= 16), modes
+    else:
+        assert 3 <= modes["fwd"] <= 16 and modes["bwd"] == (2 if vth_mode == "init" else 1), modes
     _check_samples(x, vp, vn, g, res, cfg, rng)
     again = _run(x, vp, vn, g, cfg, cuda_device)
     for a, b in zip(res, again):

@@ -165,8 +165,8 @@ def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
     cfg = flash_cfg(8192)
     # the windowed forward copies and the ranked backward are taken exactly when the
     # coordinates reach a window that fits (mapped inputs, initial thresholds); the other cases
-    # must run one copy. The forward holds two copies of the window, or four when its window
-    # (which these random inputs set) is short enough for four in its LDS
+    # must run one copy. The forward holds windowed copies (three or more, as many as fit its
+    # LDS at the window these random inputs reach) or, when three do not fit, two
     fit = (x_mode, vth_mode) == ("mapped", "init")
     # (64, 203, 300): K % 8 != 0, so padded inputs k >= K run inside the windowed copies
     for M, K, O in ((64, 200, 300), (40, 768, 256), (64, 203, 300)):
@@ -179,7 +179,7 @@ def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
         e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
         print(modes, [f"{v:.2e}" for v in e])
         if fit:
-            assert modes["bwd"] == 2 and modes["fwd"] in (1, 4), modes
+            assert modes["bwd"] == 2 and (modes["fwd"] == 1 or 3 <= modes["fwd"] <= 16), modes
         else:
             assert modes == {"fwd": 0, "bwd": 0}, modes
         assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (M, K, O, e)
