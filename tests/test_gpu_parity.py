@@ -280,6 +280,58 @@ def test_ranked_matches_one_copy(cuda_device, M, K, O):
     assert max(errs(dx_r, ref_dx)[0], errs(gp_r, ref_gp)[0], errs(gn_r, ref_gn)[0]) <= BWD_TOL
 
 
+@pytest.mark.parametrize("max_copies", [3, 5, 8, 16, 32])
+def test_windowed_forward_copies(cuda_device, max_copies):
+    """The forward's windowed table copies under each cap ISA_EKV_OPT_FWD_COPIES allows (the
+    device takes as many as fit, up to the cap, and records their number): on ragged shapes
+    whose coordinates reach a narrow window (mapped inputs, initial thresholds) the count is
+    the cap; every case matches the oracle and the one-copy forward of the same inputs to
+    rounding, and equal + and - thresholds still give exactly zero (the two signs' identical
+    threshold sets get identical copy choices)."""
+    from isa.approximations.delta_lut import get_packed_tables, lut_range
+    from isa.kernels.transformer_ffn import ops
+
+    cfg = flash_cfg(4096)
+    dmin, dmax, n = lut_range(cfg)
+    fwd, _ = get_packed_tables(cfg, cuda_device)
+    # "narrow": inputs within a few hundredths of a volt of zero, as fc2's TIA outputs are
+    cases = (((70, 129, 300), "narrow", "init"), ((5, 40, 1000), "narrow", "init"),
+             ((64, 203, 520), "mapped", "init"), ((48, 200, 300), "mapped", "full"),
+             ((33, 768, 256), "signed", "init"))
+    prev = ops.forward_copies()
+    try:
+        for (M, K, O), x_mode, vth_mode in cases:
+            print(f"[case] windowed copies <= {max_copies}: M={M} K={K} O={O} {x_mode}/{vth_mode}", flush=True)
+            x, vp, vn, g = make_inputs(M, K, O, seed=M + K + O, x_mode="signed" if x_mode == "narrow" else x_mode,
+                                       vth_mode=vth_mode)
+            if x_mode == "narrow":
+                x = x * 0.01
+            ref_out = oracle.forward(x.numpy(), vp.numpy(), vn.numpy(), oracle.lut_tables(cfg)[0], dmin, dmax,
+                                     cfg["V_sat"], -4.0, 4.0)
+            ops.forward_copies(max_copies)
+            modes = {}
+            out, _, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device, modes=modes)
+            xd, pd = x.to(cuda_device), vp.to(cuda_device)
+            pf = ops.plan_info("forward", M, K, O, n)
+            wsf = torch.empty(pf["workspace_bytes"], dtype=torch.uint8, device=cuda_device)
+            zero = ops.lut_forward(xd, pd, pd.clone(), fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0, workspace=wsf)
+            torch.cuda.synchronize()
+            zmode = ops.copy_mode(wsf, pf)
+            ops.forward_copies(0)
+            one, _, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device)
+            e = errs(out, ref_out)[0]
+            d = float((out - one).abs().max()) / max(float(one.abs().max()), 1e-30)
+            print(modes, zmode, f"oracle {e:.2e}, vs one copy {d:.2e}")
+            if x_mode == "narrow":  # a window of ~80 records: the cap
+                assert modes["fwd"] == max_copies and zmode == max_copies, (modes, zmode)
+            elif (x_mode, vth_mode) == ("mapped", "init"):  # ~1000-1400 records: fewer fit
+                assert 3 <= modes["fwd"] <= max_copies, modes
+            assert e <= FWD_TOL and d <= FWD_TOL
+            assert torch.count_nonzero(zero) == 0
+    finally:
+        ops.forward_copies(prev)
+
+
 def test_nan_semantics(cuda_device):
     """NaN x: r is NaN so its cells are NaN and the NaN row sum clamps to out_min (fminf/fmaxf);
     NaN vth reads table entry 0 like ekv_cuda.cu:19-21. Same rules as the oracle."""
