@@ -1970,6 +1970,9 @@ struct RankArgs {
 // Thresholds spread over more table records than this leave a rank's window across 32 classes
 // hundreds of records wide; there the second table copy does better (measured at U[0, 5] V,
 // 1576 records: 13.5 ms ranked against 12.4 ms with two copies per GPT-L launch).
+#ifndef ISA_EKV_RANK_MERGE_MAX
+#define ISA_EKV_RANK_MERGE_MAX 2  // most token splits the ranked launch merges per block
+#endif
 #ifndef ISA_EKV_RANK_MAX_SPREAD
 #define ISA_EKV_RANK_MAX_SPREAD 256
 #endif
@@ -2652,6 +2655,10 @@ struct DvReduceArgs {
     float scale;
     float* dvp;
     float* dvn;
+    // a table backward that may run ranked: its mode word, and the planes the ranked launch
+    // writes (it merges token splits) when the word says it ran
+    const int* mode_word;
+    int ranked_planes;
 };
 
 constexpr int kDvTileK = 8;
@@ -2666,6 +2673,8 @@ __device__ inline void dv_reduce_block(const DvReduceArgs& a, int b, int nb) {
     const int kl = t & (kDvTileK - 1), orow = t >> 3;                          // stores: 8 x 32
     const size_t plane_floats = (size_t)a.Kp * a.Op;
     const float sg = plane == 0 ? -a.scale : a.scale;
+    const int n_split =
+        a.mode_word && __builtin_amdgcn_readfirstlane(*a.mode_word) == kModeRanked ? a.ranked_planes : a.n_split;
     for (int tile_id = b; tile_id < n_ot * n_kt; tile_id += nb) {
         const int ot = tile_id % n_ot, kt = tile_id / n_ot;
         const int k = kt * kDvTileK + row;
@@ -2675,7 +2684,7 @@ __device__ inline void dv_reduce_block(const DvReduceArgs& a, int b, int nb) {
                 reinterpret_cast<const float4*>(a.part + plane * plane_floats + (size_t)k * a.Op + ot * 64 + c4 * 4);
             const size_t split4 = 2 * plane_floats / 4;
 #pragma unroll 8
-            for (int sidx = 0; sidx < a.n_split; ++sidx) {
+            for (int sidx = 0; sidx < n_split; ++sidx) {
                 const float4 v = src[(size_t)sidx * split4];
                 acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
             }
@@ -3143,6 +3152,7 @@ struct BwdPlan {
     bool ranked;  // the copies' launches may include the ranked backward (its branch-deal arrays)
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
         off_rank_ws, off_rank_branch, bytes, lds_bytes;
+    int rank_merge;  // ranked launch: token splits summed per block
 };
 
 bool bwd_may_use_copies(const BwdPlan& p, bool exact, bool need_x);
@@ -3290,6 +3300,25 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
                (size_t)round_up(kDxReduceBlocks * 8, 256);
     // the ranked backward rides with the copies' launch pair (decided on the device)
     p.ranked = bwd_may_use_copies(p, exact, need_x) && kBwdORR == 4 && g_ranked.load(std::memory_order_relaxed) != 0;
+    // The ranked launch (16 inputs per block, two blocks per CU) has twice the one-copy
+    // launch's blocks at the same token splits; it merges r consecutive splits per block (r
+    // dividing the split count) when its rounds stay as well filled and number at least 4:
+    // fewer dVth partial planes to write and reduce, and fewer table loads.
+    p.rank_merge = 1;
+    if (p.ranked) {
+        const int64_t n_kg = (p.Kp + kRankWaves - 1) / kRankWaves, slots = kCUs * 2;
+        auto fill = [&](int64_t r, int64_t& rounds) {
+            const int64_t blocks = n_kg * p.n_ob * (p.n_split / r);
+            rounds = (blocks + slots - 1) / slots;
+            return (double)blocks / (double)(rounds * slots);
+        };
+        int64_t rounds1 = 0;
+        const double f1 = fill(1, rounds1);
+        for (int r = 2; r <= ISA_EKV_RANK_MERGE_MAX; r *= 2) {
+            int64_t rounds = 0;
+            if (p.n_split % r == 0 && fill(r, rounds) >= f1 - 0.005 && rounds >= 4) p.rank_merge = r;
+        }
+    }
     p.off_rank_ws = off;
     if (p.ranked) off += (size_t)round_up(p.Kp * p.n_ob * 64 * 8 * 4, 256);
     p.off_rank_branch = off;
@@ -3980,13 +4009,17 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     else if (copies) {
         launch_backward_copies(p.split, need_w, grid, block, p.lds_bytes, s, ba);
         if (p.ranked) {
-            const dim3 rgrid((unsigned)(((p.Kp + kRankWaves - 1) / kRankWaves) * p.n_ob * p.n_split));
+            // the ranked launch sums p.rank_merge consecutive token splits per block
+            BwdArgs br = ba;
+            br.n_split = p.n_split / p.rank_merge;
+            br.m_chunk = p.m_chunk * p.rank_merge;
+            const dim3 rgrid((unsigned)(((p.Kp + kRankWaves - 1) / kRankWaves) * p.n_ob * br.n_split));
             const float* rws = reinterpret_cast<const float*>(ws + p.off_rank_ws);
             const unsigned* rbr = reinterpret_cast<const unsigned*>(ws + p.off_rank_branch);
             if (need_w)
-                hipLaunchKernelGGL(bwd_ranked_kernel<true>, rgrid, dim3(kRankWaves * 64), kRankLds, s, ba, rws, rbr);
+                hipLaunchKernelGGL(bwd_ranked_kernel<true>, rgrid, dim3(kRankWaves * 64), kRankLds, s, br, rws, rbr);
             else
-                hipLaunchKernelGGL(bwd_ranked_kernel<false>, rgrid, dim3(kRankWaves * 64), kRankLds, s, ba, rws, rbr);
+                hipLaunchKernelGGL(bwd_ranked_kernel<false>, rgrid, dim3(kRankWaves * 64), kRankLds, s, br, rws, rbr);
         }
     }
     else
@@ -4008,7 +4041,9 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     int dv_blocks = 0;
     if (need_w) {
         dva = DvReduceArgs{reinterpret_cast<const float*>(ws + p.off_dv), p.dv_planes, (int)K, (int)O, (int)p.Kp,
-                           (int)p.Op, scale, grad_vth_pos, grad_vth_neg};
+                           (int)p.Op, scale, grad_vth_pos, grad_vth_neg,
+                           p.ranked && copies ? reinterpret_cast<const int*>(ws + p.off_mode) : nullptr,
+                           p.n_split / p.rank_merge};
         dv_blocks = std::min(dv_reduce_tiles(K, O), 4096);
     }
     GlueReduceArgs gra{};
