@@ -1922,17 +1922,20 @@ __global__ __launch_bounds__(1024) void bwd_two_copies_kernel(BwdArgs a) {
 // whole threshold window (69 records at the initial thresholds). The backward's sums do not
 // care which lane evaluates which (output, sign) branch of an input: dVth± accumulates per
 // branch over tokens, and dX sums every branch of an input per token. So per (input, block of
-// 256 outputs) the branches are re-dealt: residue class c (outputs c + 32 t, t < 8, each with
-// its + and - threshold: 16 branches) goes to lanes c and c + 32, ranked by threshold
-// coordinate, lane c taking ranks 0-7 and lane c + 32 ranks 8-15 as slots 0-7. A gather
-// instruction (one slot) then reads, across a half-wave, one rank of 32 classes: a window of
-// ~30 records instead of ~69 (measured: 1.13 instead of 1.95 ns per gather per CU).
-// The cost is G: a branch's G[m][o] is no longer in its lane's registers. Each block (12
-// waves, 12 consecutive inputs sharing the output block and token range) stages G for 8
+// 256 outputs) the branches are re-dealt by residue class. With kRankClasses = 16, class c
+// (outputs c + 16 t, t < 16, each with its + and - threshold: 32 branches) goes to lanes c,
+// c + 16, c + 32 and c + 48, ranked by threshold coordinate: ranks 0-15 to the first half-wave
+// (even ranks to lane c, odd ranks to lane c + 16, rank 2 s + 1 in slot s), ranks 16-31 to
+// the second. A gather instruction (one slot) then reads, across a half-wave, two adjacent
+// ranks of 16 classes: at the initial thresholds' 69-record window, records inside a window of
+// ~20 (the 32-class deal, one rank of 32 classes of 16 branches, spans ~30: measured 1.13
+// instead of 1.95 ns per random gather per CU, 0.28 conflict cycles per LDS instruction).
+// The cost is G: a branch's G[m][o] is no longer in its lane's registers. Each block (16
+// waves, 16 consecutive inputs sharing the output block and token range) stages G for 8
 // tokens at a time in LDS, as {G, -G} quads of 4 tokens per output (the sign of a - branch
 // folds into its G), and a lane reads one 16-byte quad per slot and token group: lane c's
-// quads sit in bank quad c mod 16, so the reads are conflict-free. The staged G is read once
-// per block, not once per wave.
+// quads sit in bank quad c mod 16, and a quarter-wave holds 16 different classes, so the reads
+// are conflict-free. The staged G is read once per block, not once per wave.
 // Each branch accumulates sign * sum_m G r L_D: dVth+ partials as the one-copy kernel (the same
 // products in the same token order, so bitwise the same sums), dVth- partials negated back.
 // ----------------------------------------------------------------------------------
@@ -1958,10 +1961,20 @@ constexpr size_t kRankLds = (size_t)kRankRingBase + 4 * kRankGroupBytes;  // [bu
 static_assert(2 * kRankLds <= (size_t)kLdsBytes, "two ranked blocks per CU");
 static_assert((size_t)kRankDOffset * 8 < 65536 && 3 * kRankGroupBytes < 65536, "ds immediate offsets");
 
+#ifndef ISA_EKV_RANK_CLASSES
+#define ISA_EKV_RANK_CLASSES 16
+#endif
+// residue classes of a ranked deal (lane c's outputs are c + kRankClasses t): 16 or 32
+constexpr int kRankClasses = ISA_EKV_RANK_CLASSES;
+static_assert(kRankClasses == 16 || kRankClasses == 32, "a quarter-wave of distinct classes");
+constexpr int kRankOut = 256 / kRankClasses;   // outputs per class in a block
+constexpr int kRankBranches = 2 * kRankOut;    // branches per class
+constexpr int kRankLanesHalf = 32 / kRankClasses;  // lanes of a class in each half-wave
+
 struct RankArgs {
     const float2* wsT;    // [Kp][Op] threshold records {+, -}
     float* ws_ranked;     // [Kp][n_ob][64 lanes][8 slots] threshold coordinate of each slot's branch
-    unsigned* branch;     // [Kp][n_ob][64 lanes]: slot s in bits 4s..4s+3, t (output c + 32 t) | sign << 3
+    uint2* branch;        // [Kp][n_ob][64 lanes]: slot s in byte s: t (output c + kRankClasses t) | sign << 4
     const float2* partials;
     int* mode_word;
     int Kp, Op, n_ob, NP;
@@ -1990,49 +2003,61 @@ __device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP) 
 }
 
 // The branch deal, one thread per (input, output block, residue class): ranks by (coordinate,
-// branch index), so ties keep a fixed order. Block 0 records the mode word.
+// branch index), so ties keep a fixed order, and rank r goes to half-wave h = r / (B / 2)
+// (B branches per class), lane c + kRankClasses (r' mod L) + 32 h and slot r' / L, where
+// r' = r mod (B / 2) and L = the class's lanes per half-wave. Block 0 records the mode word.
 __global__ __launch_bounds__(256) void bwd_rank_kernel(RankArgs a) {
     const bool on = ranked_mode(a.partials, a.NP);
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.mode_word = on ? kModeRanked : 0;
     if (!on) return;
     const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= (int64_t)a.Kp * a.n_ob * 32) return;
-    const int c = (int)(p & 31);
-    const int64_t q = p >> 5;  // k * n_ob + ob
+    if (p >= (int64_t)a.Kp * a.n_ob * kRankClasses) return;
+    const int c = (int)(p % kRankClasses);
+    const int64_t q = p / kRankClasses;  // k * n_ob + ob
     const int ob = (int)(q % a.n_ob);
     const int64_t k = q / a.n_ob;
     const float2* src = a.wsT + k * a.Op + (int64_t)ob * 256 + c;
-    float key[16];  // branch i: output c + 32 (i / 2), sign i % 2
+    float key[kRankBranches];  // branch i: output c + kRankClasses (i / 2), sign i % 2
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const float2 w = src[32 * t];
+    for (int t = 0; t < kRankOut; ++t) {
+        const float2 w = src[kRankClasses * t];
         key[2 * t] = w.x;
         key[2 * t + 1] = w.y;
     }
     float* dst = a.ws_ranked + q * 64 * 8;
-    unsigned pk0 = 0, pk1 = 0;
+    unsigned codes[2 * kRankLanesHalf][2] = {};  // per lane of the class: slots 0-3, 4-7
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kRankBranches; ++i) {
         int rank = 0;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) rank += (key[j] < key[i] || (key[j] == key[i] && j < i)) ? 1 : 0;
-        const int slot = rank & 7;
-        dst[(c + (rank & 8) * 4) * 8 + slot] = key[i];
-        const unsigned code = (unsigned)((i >> 1) | ((i & 1) << 3)) << (4 * slot);
-        if (rank < 8)
-            pk0 |= code;
-        else
-            pk1 |= code;
+        for (int j = 0; j < kRankBranches; ++j) rank += (key[j] < key[i] || (key[j] == key[i] && j < i)) ? 1 : 0;
+        const int h = rank / (kRankBranches / 2), r1 = rank % (kRankBranches / 2);
+        const int li = r1 % kRankLanesHalf, slot = r1 / kRankLanesHalf;
+        dst[(c + kRankClasses * li + 32 * h) * 8 + slot] = key[i];
+        const unsigned code = (unsigned)((i >> 1) | ((i & 1) << 4)) << (8 * (slot & 3));
+#pragma unroll
+        for (int l = 0; l < 2 * kRankLanesHalf; ++l)
+            if (l == h * kRankLanesHalf + li) {
+                if (slot < 4)
+                    codes[l][0] |= code;
+                else
+                    codes[l][1] |= code;
+            }
     }
-    a.branch[q * 64 + c] = pk0;
-    a.branch[q * 64 + c + 32] = pk1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int li = 0; li < kRankLanesHalf; ++li) {
+            const int l = h * kRankLanesHalf + li;
+            a.branch[q * 64 + c + kRankClasses * li + 32 * h] = make_uint2(codes[l][0], codes[l][1]);
+        }
 }
 
 // Block = kRankWaves waves: inputs kg*W .. kg*W+W-1 (one per wave), one output block, one token split.
 // Needs dX (the copies machinery's launches all do); NEED_W adds the dVth partials.
 template <bool NEED_W>
 __global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranked_kernel(BwdArgs a, const float* __restrict__ ws_ranked,
-                                                                     const unsigned* __restrict__ branch) {
+                                                                     const uint2* __restrict__ branch) {
     if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != kModeRanked) return;
     extern __shared__ float4 s_ranked[];
     char* smem = reinterpret_cast<char*>(s_ranked);
@@ -2056,12 +2081,12 @@ __global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranke
     const bool active = k < a.Kp;  // wave-uniform; inactive waves still stage G and meet the barriers
     const int m_begin = sp * a.m_chunk;
     const int m_end = min(a.M, m_begin + a.m_chunk);
-    const int c = lane & 31;
+    const int c = lane % kRankClasses;  // the lane's residue class
 
     float ws[8];
     unsigned goff[8];  // byte address of each slot's G quad in ring buffer 0, group 0
     {
-        unsigned pk = 0;
+        uint2 pk = make_uint2(0u, 0u);
         float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
         if (active) {
             const size_t q = ((size_t)k * a.n_ob + ob) * 64 + lane;
@@ -2073,8 +2098,9 @@ __global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranke
         ws[4] = w1.x; ws[5] = w1.y; ws[6] = w1.z; ws[7] = w1.w;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const unsigned t = (pk >> (4 * s)) & 7u, sg = (pk >> (4 * s + 3)) & 1u;
-            goff[s] = kRankRingBase + (sg * 256u + (unsigned)c + 32u * t) * 16u;
+            const unsigned code = ((s < 4 ? pk.x : pk.y) >> (8 * (s & 3))) & 0xffu;
+            const unsigned t = code & 15u, sg = (code >> 4) & 1u;
+            goff[s] = kRankRingBase + (sg * 256u + (unsigned)c + (unsigned)kRankClasses * t) * 16u;
         }
     }
     float acc[8];
@@ -2188,12 +2214,13 @@ __global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranke
     }
     if (NEED_W && active) {
         const size_t q = ((size_t)k * a.n_ob + ob) * 64 + lane;
-        const unsigned pk = branch[q];
+        const uint2 pk = branch[q];
         float* plane = a.dv_part + (size_t)sp * 2 * a.Kp * a.Op + (size_t)k * a.Op + (size_t)ob * 256 + c;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const unsigned t = (pk >> (4 * s)) & 7u, sg = (pk >> (4 * s + 3)) & 1u;
-            plane[(size_t)sg * a.Kp * a.Op + 32u * t] = sg ? -acc[s] : acc[s];
+            const unsigned code = ((s < 4 ? pk.x : pk.y) >> (8 * (s & 3))) & 0xffu;
+            const unsigned t = code & 15u, sg = (code >> 4) & 1u;
+            plane[(size_t)sg * a.Kp * a.Op + (unsigned)kRankClasses * t] = sg ? -acc[s] : acc[s];
         }
     }
 }
@@ -3322,7 +3349,7 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
     p.off_rank_ws = off;
     if (p.ranked) off += (size_t)round_up(p.Kp * p.n_ob * 64 * 8 * 4, 256);
     p.off_rank_branch = off;
-    if (p.ranked) off += (size_t)round_up(p.Kp * p.n_ob * 64 * 4, 256);
+    if (p.ranked) off += (size_t)round_up(p.Kp * p.n_ob * 64 * 8, 256);
     p.bytes = round_up((int64_t)off, 256);
     return p;
 }
@@ -3982,9 +4009,9 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         if (p.ranked) {  // the branch deal first: it records the ranked mode when that launch works
             const RankArgs ra{reinterpret_cast<const float2*>(ws + p.off_wsT),
                               reinterpret_cast<float*>(ws + p.off_rank_ws),
-                              reinterpret_cast<unsigned*>(ws + p.off_rank_branch), ba.partials, mode,
+                              reinterpret_cast<uint2*>(ws + p.off_rank_branch), ba.partials, mode,
                               (int)p.Kp, (int)p.Op, p.n_ob, ba.NP};
-            const int64_t threads = p.Kp * p.n_ob * 32;
+            const int64_t threads = p.Kp * p.n_ob * kRankClasses;
             hipLaunchKernelGGL(bwd_rank_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, ra);
         }
         // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
@@ -4015,7 +4042,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
             br.m_chunk = p.m_chunk * p.rank_merge;
             const dim3 rgrid((unsigned)(((p.Kp + kRankWaves - 1) / kRankWaves) * p.n_ob * br.n_split));
             const float* rws = reinterpret_cast<const float*>(ws + p.off_rank_ws);
-            const unsigned* rbr = reinterpret_cast<const unsigned*>(ws + p.off_rank_branch);
+            const uint2* rbr = reinterpret_cast<const uint2*>(ws + p.off_rank_branch);
             if (need_w)
                 hipLaunchKernelGGL(bwd_ranked_kernel<true>, rgrid, dim3(kRankWaves * 64), kRankLds, s, br, rws, rbr);
             else
