@@ -304,8 +304,9 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *     more than the copy saves). 0 lets every call consider it.
  *   ISA_EKV_OPT_RANKED: 1 (default) lets table backwards that consider the second copy run
  *     the ranked backward instead, when their coordinates need no clamp and reach a window of
- *     at most 3008 table records (decided on the device; mode word 2): each wave's gathers
- *     then read thresholds dealt to lanes in rank order. 0 never runs it.
+ *     at most 3008 table records and their thresholds span at most 420 (decided on the
+ *     device; mode word 2): each wave's gathers then read thresholds dealt to lanes in rank
+ *     order. 0 never runs it.
  *   ISA_EKV_OPT_FWD_COPIES: the most bank-rotated copies of the coordinate window (3 to 32;
  *     default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
  *     LDS when its coordinates need no clamp (decided on the device, which takes the most

@@ -1980,14 +1980,14 @@ struct RankArgs {
     int Kp, Op, n_ob, NP;
 };
 
-// Thresholds spread over more table records than this leave a rank's window across 32 classes
-// hundreds of records wide; there the second table copy does better (measured at U[0, 5] V,
-// 1576 records: 13.5 ms ranked against 12.4 ms with two copies per GPT-L launch).
+// Thresholds spread over more table records than this leave a half-wave's ranks hundreds of
+// records apart; there the second table copy does better (GPT-L fc1 backward, 16-class deal:
+// 11.93 ms ranked against 12.12 ms with two copies at 400 records, 12.27 against 12.18 at 450).
 #ifndef ISA_EKV_RANK_MERGE_MAX
 #define ISA_EKV_RANK_MERGE_MAX 2  // most token splits the ranked launch merges per block
 #endif
 #ifndef ISA_EKV_RANK_MAX_SPREAD
-#define ISA_EKV_RANK_MAX_SPREAD 256
+#define ISA_EKV_RANK_MAX_SPREAD 420
 #endif
 constexpr float kRankMaxSpread = (float)ISA_EKV_RANK_MAX_SPREAD;
 

@@ -118,7 +118,7 @@ def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     # from global memory (no mode). 8192 entries at the initial thresholds: the forward holds
     # windowed copies in its 16-wave blocks, the backward runs ranked (135 records). The wide
     # spread: windowed forward copies of a ~2900-record window (three fit), the two-copy
-    # backward (1576 records, past the ranked kernel's 256)
+    # backward (1576 records, past the ranked kernel's 420)
     if size > 8192:
         assert modes["bwd"] is None and (modes["fwd"] == 0 or 3 <= modes["fwd"] <= 16), modes
     else:
