@@ -447,6 +447,9 @@ def main() -> int:
     ap.add_argument("--no-ranked", action="store_true",
                     help="plan the table backwards without the ranked kernel (isa_ekv_set_option "
                          "ISA_EKV_OPT_RANKED = 0): the one- or two-copy kernel runs instead")
+    ap.add_argument("--copy-min-cells", type=int, default=None,
+                    help="calls of fewer cells M*K*O plan one table copy and no ranked backward "
+                         "(isa_ekv_set_option ISA_EKV_OPT_COPY_MIN_CELLS, default 2^28)")
     ap.add_argument("--fwd-copies", type=int, default=None,
                     help="the most windowed table copies a LUT forward may hold (isa_ekv_set_option "
                          "ISA_EKV_OPT_FWD_COPIES: 3 to 32, default 16; 0 none)")
@@ -476,6 +479,10 @@ def main() -> int:
         from isa.kernels.transformer_ffn import ops
 
         ops.forward_copies(args.fwd_copies)
+    if args.copy_min_cells is not None:
+        from isa.kernels.transformer_ffn import ops
+
+        ops.copy_min_cells(args.copy_min_cells)
     if args.config == "gptl_train":
         return gpt_train_step(args)
     if args.config == "measured_fc1":
