@@ -450,9 +450,10 @@ def main() -> int:
     ap.add_argument("--copy-min-cells", type=int, default=None,
                     help="calls of fewer cells M*K*O plan one table copy and no ranked backward "
                          "(isa_ekv_set_option ISA_EKV_OPT_COPY_MIN_CELLS, default 2^28)")
-    ap.add_argument("--fwd-copies", type=int, default=None,
-                    help="the most windowed table copies a LUT forward may hold (isa_ekv_set_option "
-                         "ISA_EKV_OPT_FWD_COPIES: 3 to 32, default 16; 0 none)")
+    ap.add_argument("--window-copies", type=int, default=None,
+                    help="the most windowed table copies a LUT forward or the two-copy backward may hold "
+                         "(isa_ekv_set_option "
+                         "ISA_EKV_OPT_WINDOW_COPIES: 3 to 32, default 16; 0 none)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -475,10 +476,10 @@ def main() -> int:
         from isa.kernels.transformer_ffn import ops
 
         ops.ranked_backward(False)
-    if args.fwd_copies is not None:
+    if args.window_copies is not None:
         from isa.kernels.transformer_ffn import ops
 
-        ops.forward_copies(args.fwd_copies)
+        ops.window_copies(args.window_copies)
     if args.copy_min_cells is not None:
         from isa.kernels.transformer_ffn import ops
 

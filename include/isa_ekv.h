@@ -282,7 +282,7 @@ int isa_ekv_profile_end(double* ms, int* launches);
  *   [1] byte offset in the workspace of the table-copy mode word (int32: after the call, 1 when
  *       the main kernel ran with the second, bank-rotated table copy, 0 when with one copy,
  *       2 when the backward ran ranked: see ISA_EKV_OPT_RANKED, 3 to 32 when the forward held
- *       that many windowed copies: see ISA_EKV_OPT_FWD_COPIES), or -1 when the call cannot
+ *       that many windowed copies: see ISA_EKV_OPT_WINDOW_COPIES), or -1 when the call cannot
  *       use a second copy (the word is then not written)
  *   [2] forward: K ranges summed separately (1: no split); backward: token splits
  *   [3] forward: tokens per wave; backward: inputs per wave of the one-copy kernel
@@ -307,17 +307,18 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *     at most 3008 table records and their thresholds span at most 420 (decided on the
  *     device; mode word 2): each wave's gathers then read thresholds dealt to lanes in rank
  *     order. 0 never runs it.
- *   ISA_EKV_OPT_FWD_COPIES: the most bank-rotated copies of the coordinate window (3 to 32;
+ *   ISA_EKV_OPT_WINDOW_COPIES: the most bank-rotated copies of the coordinate window (3 to 32;
  *     default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
- *     LDS when its coordinates need no clamp (decided on the device, which takes the most
- *     copies that fit; mode word = the number of copies): each threshold then reads the copy
- *     its assignment pass chose to spread a gather's records over the LDS banks. Below 3 the
- *     forward never holds them.
+ *     LDS when its coordinates need no clamp, and a table backward's two-copy launch when the
+ *     ranked backward does not apply (decided on the device, which takes the most copies
+ *     that fit; mode word = the number of copies): each threshold then reads the copy its
+ *     assignment pass chose to spread a gather's records over the LDS banks. Below 3 neither
+ *     holds them.
  * Plans (and so workspace sizes) depend on the options: query workspace sizes after setting
  * them, and do not change them while calls are in flight. */
 #define ISA_EKV_OPT_COPY_MIN_CELLS 1
 #define ISA_EKV_OPT_RANKED 2
-#define ISA_EKV_OPT_FWD_COPIES 3
+#define ISA_EKV_OPT_WINDOW_COPIES 3
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous);
 
 /* Measurement aid, no reference counterpart: launches two 1024-thread blocks per CU, each

@@ -130,11 +130,12 @@ std::atomic<int64_t> g_copy_min_cells{(int64_t)1 << 28};
 // Planning option ISA_EKV_OPT_RANKED: whether table backwards may run the ranked kernel.
 std::atomic<int64_t> g_ranked{1};
 
-// Planning option ISA_EKV_OPT_FWD_COPIES: the most bank-rotated copies of the coordinate
-// window a LUT forward may hold (3 to 32; below 3 the forward never holds them). At the
+// Planning option ISA_EKV_OPT_WINDOW_COPIES: the most bank-rotated copies of the coordinate
+// window a LUT forward, or a table backward's two-copy launch, may hold (3 to 32; below 3
+// neither holds them). At the
 // headline's narrow fc2 window 8, 16 and 32 copies run the forward in the same time within
 // 1%, and the assignment pass costs ~10 us more per doubling: 16.
-std::atomic<int64_t> g_fwd_copies{16};
+std::atomic<int64_t> g_window_copies{16};
 
 bool copies_pay(int64_t M, int64_t K, int64_t O) {
     return (double)M * (double)K * (double)O >= (double)g_copy_min_cells.load(std::memory_order_relaxed);
@@ -1190,13 +1191,21 @@ __device__ inline bool clamp_free(const CoordRange& c, int NP) {
     return __builtin_amdgcn_readfirstlane((int)((c.xlo - c.whi >= 1.0f) && (c.xhi - c.wlo <= (float)(NP - 2)))) != 0;
 }
 
-__device__ inline MultiLayout fwd_multi_layout(const CoordRange& cr, int NP, int budget, int max_copies) {
+// dhalf > 0 (the backward's split tables): each copy also holds the D halves of its records,
+// dhalf records after its I halves, for windows of at most max_window records, and only when
+// the thresholds spread over at least kFwdCopyMinWindow records (below that the backward's
+// one-copy launch, two blocks per CU, beats the copies' one block: 9.37 against 9.54 ms at the
+// headline's 69 records).
+__device__ inline MultiLayout multi_layout(const CoordRange& cr, int NP, int budget, int max_copies, int dhalf,
+                                           int max_window) {
     MultiLayout m{0, 0, 0, NP};
     if (max_copies < kModeMultiMin || !clamp_free(cr, NP)) return m;
+    if (dhalf > 0 && __builtin_amdgcn_readfirstlane((int)(cr.whi - cr.wlo >= kFwdCopyMinWindow)) == 0) return m;
     coord_window(cr, NP, m.lo, m.n);
-    const int stride = (m.n + 31) & ~31;
+    if (m.n > max_window) return MultiLayout{0, 0, 0, NP};
+    const int stride = (dhalf + m.n + 31) & ~31;
     for (int c = min(max_copies, kMultiMax); c >= kModeMultiMin; --c) {
-        if (multi_offset(c - 1, c, stride) + m.n <= budget) {
+        if (multi_offset(c - 1, c, stride) + dhalf + m.n <= budget) {
             m.copies = c;
             m.stride = stride;
             break;
@@ -1204,6 +1213,12 @@ __device__ inline MultiLayout fwd_multi_layout(const CoordRange& cr, int NP, int
     }
     return m;
 }
+
+__device__ inline MultiLayout fwd_multi_layout(const CoordRange& cr, int NP, int budget, int max_copies) {
+    return multi_layout(cr, NP, budget, max_copies, 0, NP);
+}
+
+__device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP);
 
 // Copy choice for the windowed copies. A problem is the 32 thresholds one half-wave gather
 // reads (as in fwd_copy_assign_kernel<32>: input k, sign, output slot j, half of an output
@@ -1303,11 +1318,14 @@ __device__ inline unsigned multi_lo_mask(float w, float fl) {
 
 // Block 0 records the launch's mode in the mode word: the number of copies, or 0 (the two-copy
 // pass that follows then decides between one and two copies).
+// (The backward's two-copy launch takes the same pass with dhalf > 0; after_rank: the ranked
+// backward, when its mode applies, keeps the word its pass wrote.)
 __global__ __launch_bounds__(kMcThreads) void fwd_multi_assign_kernel(float2* __restrict__ wsT,
                                                           const float2* __restrict__ partials, int NP, int budget,
                                                           int max_copies, int* __restrict__ mode_word, int64_t Kp,
-                                                          int64_t Op) {
-    const MultiLayout ml = fwd_multi_layout(read_coord_range(partials), NP, budget, max_copies);
+                                                          int64_t Op, int dhalf, int max_window, int after_rank) {
+    if (after_rank && ranked_mode(partials, NP)) return;
+    const MultiLayout ml = multi_layout(read_coord_range(partials), NP, budget, max_copies, dhalf, max_window);
     if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = ml.copies;
     if (ml.copies == 0) return;
     __shared__ float s_sw[32 * kMcProblems];       // [rank][problem]: the thresholds in order
@@ -1506,6 +1524,7 @@ struct BwdArgs {
                             // in its block, one dVth partial plane per group (see bwd_item)
     float cmin, cmax;
     float k2, c2;           // exact: 2^(-V_D a), V_D a
+    int mc_budget, mc_max;  // split tables: the two-copy launch may hold up to mc_max windowed copies
 };
 
 // LDS table views for the backward. Interleaved: one 16-byte record {A_I, dI, A_D, dD} per
@@ -1517,14 +1536,16 @@ struct BwdTableInterleaved {
     const float4* t;
     __device__ float4 operator[](unsigned i) const { return t[i]; }
 };
-struct BwdTableSplit {
+template <int DOFF>
+struct BwdTableSplitAt {  // D halves DOFF records after the I halves
     const float2* t;
     __device__ float4 operator[](unsigned i) const {
         const float2 ri = t[i];
-        const float2 rd = t[i + kSplitRecords];
+        const float2 rd = t[i + DOFF];
         return make_float4(ri.x, ri.y, rd.x, rd.y);
     }
 };
+using BwdTableSplit = BwdTableSplitAt<kSplitRecords>;
 
 // Cross-lane dX reduction without LDS (gfx950 lane exchanges): the wave's four per-lane
 // partials v0..v3 (one per input of the wave) are summed over all 64 lanes so that every
@@ -1829,6 +1850,42 @@ constexpr int kBwdCopyOffset = 2 * kSplitRecords + 16;
 constexpr int kBwdCopyOffsetI = kSplitRecords + 8;
 constexpr size_t kBwdTwoCopiesLds = (size_t)(kBwdCopyOffset + 2 * kSplitRecords) * 8;
 constexpr size_t kBwdTwoCopiesLdsI = (size_t)(kBwdCopyOffsetI + kSplitRecords) * 16;
+// Windowed copies in the two-copy launch (split tables; mode word C >= kModeMultiMin, chosen
+// by fwd_multi_assign_kernel with dhalf = kBwdWinDOffset): copy c holds the coordinate
+// window's I records from LDS record T_c and their D records kBwdWinDOffset further (a
+// multiple of 32 that is not one of 64, so the two reads stay two ds_read_b64 through the
+// immediate offset), for windows of at most kBwdWinWindow records, in the whole LDS of the
+// launch's one block per CU.
+constexpr int kBwdWinWindow = 3008;
+constexpr int kBwdWinDOffset = kBwdWinWindow + 32;
+constexpr int kBwdWinBudget = kLdsBytes / 8;  // records
+using BwdTableWin = BwdTableSplitAt<kBwdWinDOffset>;
+
+template <bool NEED_X, bool NEED_W, bool LANE_RED, int MODE, class Table, bool FAST_ONLY>
+__device__ inline void bwd_table_items(const BwdArgs& a, const Table t, bool fast, float* red);
+
+// The windowed copies of the two-copy launch (mode word C >= kModeMultiMin): the layout from
+// the range partials as the assignment pass computed it, copy c's records {A - T_c dT, dT}.
+template <bool NEED_X, bool NEED_W>
+__device__ inline void bwd_windowed_copies(const BwdArgs& a) {
+    extern __shared__ float4 s_lut_bwd[];
+    float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
+    const MultiLayout ml =
+        multi_layout(read_coord_range(a.partials), a.NP, a.mc_budget, a.mc_max, kBwdWinDOffset, kBwdWinWindow);
+    if (ml.copies == 0) return;  // (not reached: the pass records a count only when it fits)
+    const int n = ml.n, total = n * ml.copies;
+    for (int q = threadIdx.x; q < total; q += blockDim.x) {
+        const int c = q / n, i = q - c * n;
+        const float4 r = a.lut[ml.lo + i];
+        const int tc = multi_offset(c, ml.copies, ml.stride);
+        const float ft = (float)tc;
+        s_split[tc + i] = make_float2(fmaf(-ft, r.y, r.x), r.y);
+        s_split[tc + kBwdWinDOffset + i] = make_float2(fmaf(-ft, r.w, r.z), r.w);
+    }
+    __syncthreads();
+    bwd_table_items<NEED_X, NEED_W, true, kBwdTwoCopies, BwdTableWin, true>(a, BwdTableWin{s_split - ml.lo}, true,
+                                                                             nullptr);
+}
 
 template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED, int MODE>
 __device__ inline void bwd_table_body(const BwdArgs& a) {
@@ -1840,7 +1897,13 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
     // VGPRs: the one-copy kernels keep their 64-VGPR budget)
     int lo = 0, n_rec = a.NP;  // table records held: [lo, lo + n_rec)
     if constexpr (MODE == kBwdTwoCopies) {
-        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 1) return;
+        const int mode = __builtin_amdgcn_readfirstlane(*a.copy_mode);
+        if constexpr (SPLIT && LANE_RED)
+            if (mode >= kModeMultiMin) {
+                bwd_windowed_copies<NEED_X, NEED_W>(a);
+                return;
+            }
+        if (mode != 1) return;
         // tables past kSplitRecords hold the window the launch's coordinates reach (the mode
         // word is set only when it fits)
         if (a.NP > kSplitRecords) {
@@ -1871,7 +1934,6 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
     __builtin_amdgcn_sched_barrier(0);  // the range loads after the table loads (VGPRs: one set live)
     const bool fast = coords_in_padded_range(a.partials, a.NP);
     __syncthreads();
-    const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int table_records = SPLIT ? kSplitRecords : a.NP;
     float* red = LANE_RED ? nullptr
@@ -1882,21 +1944,29 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
         t = BwdTableSplit{s_split - lo};  // record i of the table at LDS record i - lo
     else
         t = BwdTableInterleaved{s_lut_bwd - lo};
-    // The two-copy launch runs one block per CU (its 132 KB of LDS) over as many blocks as CUs,
-    // each wave taking the plan's blocks in turn, so the launch costs little when it is not
-    // the working one and loads its tables once per CU when it is.
+    bwd_table_items<NEED_X, NEED_W, LANE_RED, MODE, Table, false>(a, t, fast, red);
+}
+
+// The work items of a table-backward launch (the two-copy launch: persistent, one block per CU,
+// each wave taking the plan's items in turn, so the launch costs little when it is not the
+// working one and loads its tables once per CU when it is). FAST_ONLY: the clamp-free loop only.
+template <bool NEED_X, bool NEED_W, bool LANE_RED, int MODE, class Table, bool FAST_ONLY>
+__device__ inline void bwd_table_items(const BwdArgs& a, const Table t, bool fast, float* red) {
+    const int waves = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int stride = MODE == kBwdTwoCopies ? (int)gridDim.x : 0;
     constexpr int KRM = MODE == kBwdTwoCopies ? kBwdKRTwoCopies : kBwdKR;  // inputs per wave
+    extern __shared__ float4 s_lut_bwd[];
     for (int vb = blockIdx.x;; vb += stride) {
         const int item = vb * waves + wave;
         if (item >= a.n_items) return;
         // the one-shot launch may sum its blocks' dVth partials in the table's LDS (dv_group)
         constexpr bool DVG = MODE == kBwdAlone;
         float* dv_lds = reinterpret_cast<float*>(s_lut_bwd);
-        if (fast)
+        if (FAST_ONLY || fast)
             bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<false, Table>, LANE_RED, DVG>(
                 a, LutBwdCell<false, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item, dv_lds);
-        else
+        else if constexpr (!FAST_ONLY)
             bwd_body<KRM, NEED_X, NEED_W, LutBwdCell<true, Table>, LANE_RED, DVG>(
                 a, LutBwdCell<true, Table>{t, a.cmin, a.cmax}, a.xrec, a.wsT, red, item, dv_lds);
         if (MODE != kBwdTwoCopies) return;
@@ -3177,6 +3247,7 @@ struct BwdPlan {
     bool grad_padded, split, lane_red, gtab, halves;
     bool copies;  // at least ISA_EKV_OPT_COPY_MIN_CELLS cells: the second table copy may pay
     bool ranked;  // the copies' launches may include the ranked backward (its branch-deal arrays)
+    int mc_max;   // split tables with the copies' launches: most windowed copies of the two-copy launch (0: none)
     size_t off_xrec, off_wsT, off_xrec_alt, off_wsT_alt, off_part, off_mode, off_gpad, off_dx, off_dv, off_glue,
         off_rank_ws, off_rank_branch, bytes, lds_bytes;
     int rank_merge;  // ranked launch: token splits summed per block
@@ -3327,6 +3398,10 @@ BwdPlan plan_backward(int64_t M, int64_t K, int64_t O, int n_entries, bool need_
                (size_t)round_up(kDxReduceBlocks * 8, 256);
     // the ranked backward rides with the copies' launch pair (decided on the device)
     p.ranked = bwd_may_use_copies(p, exact, need_x) && kBwdORR == 4 && g_ranked.load(std::memory_order_relaxed) != 0;
+    {
+        const int64_t mc = std::min<int64_t>(g_window_copies.load(std::memory_order_relaxed), kMultiMax);
+        p.mc_max = bwd_may_use_copies(p, exact, need_x) && p.split && mc >= kModeMultiMin ? (int)mc : 0;
+    }
     // The ranked launch (16 inputs per block, two blocks per CU) has twice the one-copy
     // launch's blocks at the same token splits; it merges r consecutive splits per block (r
     // dividing the split count) when its rounds stay as well filled and number at least 4:
@@ -3431,7 +3506,7 @@ void launch_backward_layout(bool need_x, bool need_w, dim3 grid, dim3 block, siz
 // The split-layout lane-exchange backward as a pair of launches (kBwdOneCopy, kBwdTwoCopies)
 // of which the device runs one; the same plan (grid, token splits, partial planes) serves both.
 void launch_backward_copies(bool split, bool need_w, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                            const BwdArgs& ba0) {
+                            const BwdArgs& ba0, size_t lds2) {
     const dim3 grid2(std::min<unsigned>(grid.x, kCUs));  // persistent: one block per CU
     BwdArgs ba2 = ba0;  // the two-copy kernel's inputs per wave
     ba2.n_kb = ba0.Kp / kBwdKRTwoCopies;
@@ -3443,8 +3518,7 @@ void launch_backward_copies(bool split, bool need_w, dim3 grid, dim3 block, size
         else
             hipLaunchKernelGGL((bwd_kernel<true, true, false, true, kBwdOneCopy>), grid, block, lds, s, ba);
         if (split)
-            hipLaunchKernelGGL((bwd_two_copies_kernel<true, true, true>), grid2, block, kBwdTwoCopiesLds, s,
-                               ba2);
+            hipLaunchKernelGGL((bwd_two_copies_kernel<true, true, true>), grid2, block, lds2, s, ba2);
         else
             hipLaunchKernelGGL((bwd_two_copies_kernel<true, true, false>), grid2, block, kBwdTwoCopiesLdsI,
                                s, ba2);
@@ -3454,8 +3528,7 @@ void launch_backward_copies(bool split, bool need_w, dim3 grid, dim3 block, size
         else
             hipLaunchKernelGGL((bwd_kernel<true, false, false, true, kBwdOneCopy>), grid, block, lds, s, ba);
         if (split)
-            hipLaunchKernelGGL((bwd_two_copies_kernel<true, false, true>), grid2, block, kBwdTwoCopiesLds, s,
-                               ba2);
+            hipLaunchKernelGGL((bwd_two_copies_kernel<true, false, true>), grid2, block, lds2, s, ba2);
         else
             hipLaunchKernelGGL((bwd_two_copies_kernel<true, false, false>), grid2, block, kBwdTwoCopiesLdsI,
                                s, ba2);
@@ -3762,7 +3835,7 @@ FwdTableCfg fwd_table_cfg(int n_entries, int wpb, bool copies) {
     }
     // the windowed copies, in an allocation of at least the block shape's share of the CU's
     // LDS (the device takes as many copies as fit the launch's window)
-    const int64_t mc_max = std::min<int64_t>(g_fwd_copies.load(std::memory_order_relaxed), 32);
+    const int64_t mc_max = std::min<int64_t>(g_window_copies.load(std::memory_order_relaxed), 32);
     if (mc_max >= kModeMultiMin) {
         t.lds = std::max(t.lds, lds_cap);
         t.mc_budget = (int)(t.lds / 8);
@@ -3844,7 +3917,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
             hipLaunchKernelGGL(fwd_multi_assign_kernel, dim3((unsigned)((problems + kMcProblems - 1) / kMcProblems)),
                                dim3(kMcThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials, fa.NP, tc.mc_budget,
-                               tc.mc_max, mode, p.Kp, p.Op);
+                               tc.mc_max, mode, p.Kp, p.Op, 0, fa.NP, 0);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward windowed-copy assignment launch");
         }
@@ -4017,14 +4090,24 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
         const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * (p.split ? 4 : 8);
         const dim3 agrid((unsigned)((problems + kAssignThreads - 1) / kAssignThreads));
+        if (p.mc_max > 0) {  // then the windowed copies of the two-copy launch, unless ranked
+            ba.mc_budget = kBwdWinBudget;
+            ba.mc_max = p.mc_max;
+            hipLaunchKernelGGL(fwd_multi_assign_kernel, dim3((unsigned)((problems + kMcProblems - 1) / kMcProblems)),
+                               dim3(kMcThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials,
+                               ba.NP, kBwdWinBudget, p.mc_max, mode, p.Kp, p.Op, kBwdWinDOffset, kBwdWinWindow,
+                               p.ranked ? 1 : 0);
+        }
+        // (a pass before it recorded the ranked mode or the windowed copies: skip_from)
+        const int skip_from = p.ranked ? kModeRanked : p.mc_max > 0 ? kModeMultiMin : 0;
         if (p.split)
             hipLaunchKernelGGL(fwd_copy_assign_kernel<32>, agrid, dim3(kAssignThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
-                               p.Kp, p.Op, kBwdCopyOffset, p.ranked ? kModeRanked : 0);
+                               p.Kp, p.Op, kBwdCopyOffset, skip_from);
         else
             hipLaunchKernelGGL(fwd_copy_assign_kernel<16>, agrid, dim3(kAssignThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials, ba.NP, kSplitRecords, mode,
-                               p.Kp, p.Op, kBwdCopyOffsetI, p.ranked ? kModeRanked : 0);
+                               p.Kp, p.Op, kBwdCopyOffsetI, skip_from);
         ba.copy_mode = mode;
         err = hipGetLastError();
         if (err != hipSuccess) return hip_fail(err, "backward copy assignment launch");
@@ -4034,7 +4117,8 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     if (p.halves)
         launch_backward_halves(need_x, need_w, grid, block, p.lds_bytes, s, ba);
     else if (copies) {
-        launch_backward_copies(p.split, need_w, grid, block, p.lds_bytes, s, ba);
+        launch_backward_copies(p.split, need_w, grid, block, p.lds_bytes, s, ba,
+                               p.mc_max > 0 ? (size_t)kLdsBytes : kBwdTwoCopiesLds);
         if (p.ranked) {
             // the ranked launch sums p.rank_merge consecutive token splits per block
             BwdArgs br = ba;
@@ -4672,7 +4756,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous) {
     std::atomic<int64_t>* opt = option == ISA_EKV_OPT_COPY_MIN_CELLS ? &g_copy_min_cells
                                 : option == ISA_EKV_OPT_RANKED      ? &g_ranked
-                                : option == ISA_EKV_OPT_FWD_COPIES  ? &g_fwd_copies
+                                : option == ISA_EKV_OPT_WINDOW_COPIES  ? &g_window_copies
                                                                     : nullptr;
     if (!opt) return fail(ISA_EKV_EINVAL, "unknown option %d", option);
     const int64_t old = value >= 0 ? opt->exchange(value) : opt->load();

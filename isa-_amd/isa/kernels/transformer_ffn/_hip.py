@@ -29,7 +29,7 @@ PLAN_INFO_LEN = 8
 NOALLOC_MAX_BYTES = 64 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
 OPT_COPY_MIN_CELLS = 1
 OPT_RANKED = 2
-OPT_FWD_COPIES = 3
+OPT_WINDOW_COPIES = 3
 
 EXPORTS = (
     "isa_ekv_abi_version",

@@ -94,13 +94,14 @@ def ranked_backward(value: Optional[bool] = None) -> bool:
     return bool(prev.value)
 
 
-def forward_copies(value: Optional[int] = None) -> int:
-    """The library's ISA_EKV_OPT_FWD_COPIES (the most windowed table copies a LUT forward may
-    hold: 3 to 32, default 16; below 3 none); sets it when value is given. Returns the value before
+def window_copies(value: Optional[int] = None) -> int:
+    """The library's ISA_EKV_OPT_WINDOW_COPIES (the most windowed table copies a LUT forward, or
+    a table backward's two-copy launch, may hold: 3 to 32, default 16; below 3 none); sets it
+    when value is given. Returns the value before
     the call."""
     lib = _hip.load()
     prev = ctypes.c_int64()
-    rc = lib.isa_ekv_set_option(_hip.OPT_FWD_COPIES, -1 if value is None else int(value), ctypes.byref(prev))
+    rc = lib.isa_ekv_set_option(_hip.OPT_WINDOW_COPIES, -1 if value is None else int(value), ctypes.byref(prev))
     _hip.check(rc, "isa_ekv_set_option")
     return int(prev.value)
 

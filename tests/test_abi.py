@@ -260,13 +260,13 @@ def test_plan_info_reports_the_call_plans():
     f16 = ops.plan_info("forward", 8192, 768, 3072, 16384)
     assert f16["mode_offset"] >= 0 and f16["lds_bytes"] == (16384 + 2 * 16) * 8
     assert ops.plan_info("backward", 8192, 768, 3072, 16384)["mode_offset"] == -1
-    # without windowed copies (ISA_EKV_OPT_FWD_COPIES < 4) the 16384-entry forward has no mode word
-    prev = ops.forward_copies(0)
+    # without windowed copies (ISA_EKV_OPT_WINDOW_COPIES < 4) the 16384-entry forward has no mode word
+    prev = ops.window_copies(0)
     try:
         assert ops.plan_info("forward", 8192, 768, 3072, 16384)["mode_offset"] == -1
-        assert ops.forward_copies() == 0
+        assert ops.window_copies() == 0
     finally:
-        ops.forward_copies(prev)
+        ops.window_copies(prev)
     assert prev == 16
     # a dVth-only backward runs no copy pair
     assert ops.plan_info("backward", 512, 64, 256, 4096, need_grad_x=False)["mode_offset"] == -1

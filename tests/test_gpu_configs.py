@@ -154,7 +154,7 @@ def _inputs(B, T, D, seed):
 
 
 # the forward's windowed table copies: their number depends on the coordinate window the
-# inputs reach (3 up to ISA_EKV_OPT_FWD_COPIES, default 16)
+# inputs reach (3 up to ISA_EKV_OPT_WINDOW_COPIES, default 16)
 WINDOWED = range(3, 17)
 
 

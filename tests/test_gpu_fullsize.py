@@ -118,11 +118,14 @@ def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     # from global memory (no mode). 8192 entries at the initial thresholds: the forward holds
     # windowed copies in its 16-wave blocks, the backward runs ranked (135 records). The wide
     # spread: windowed forward copies of a ~2900-record window (three fit), the two-copy
-    # backward (1576 records, past the ranked kernel's 420)
+    # backward (1576 records, past the ranked kernel's 420), with windowed copies where they fit
     if size > 8192:
         assert modes["bwd"] is None and (modes["fwd"] == 0 or 3 <= modes["fwd"] <= 16), modes
     else:
-        assert 3 <= modes["fwd"] <= 16 and modes["bwd"] == (2 if vth_mode == "init" else 1), modes
+        if vth_mode == "init":
+            assert 3 <= modes["fwd"] <= 16 and modes["bwd"] == 2, modes
+        else:  # the two-copy launch, with windowed copies when three fit its LDS
+            assert 3 <= modes["fwd"] <= 16 and (modes["bwd"] == 1 or 3 <= modes["bwd"] <= 16), modes
     _check_samples(x, vp, vn, g, res, cfg, rng)
     again = _run(x, vp, vn, g, cfg, cuda_device)
     for a, b in zip(res, again):

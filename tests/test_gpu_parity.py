@@ -239,6 +239,7 @@ def test_invariants_on_device(cuda_device, ranked):
         _, gx_ref, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device)
     finally:
         ops.ranked_backward(prev)
+    # without the ranked backward at the initial thresholds' spread: the one-copy kernel
     assert modes["bwd"] == (2 if ranked else 0), modes
     assert torch.count_nonzero(out) == 0
     assert torch.equal(gp, -gn)
@@ -264,12 +265,15 @@ def test_ranked_matches_one_copy(cuda_device, M, K, O):
     x, vp, vn, g = make_inputs(M, K, O, seed=M + 3 * K)
     res = {}
     for ranked in (True, False):
+        # without the ranked backward and without windowed copies: the one-copy kernel
         prev = ops.ranked_backward(ranked)
+        prev_w = ops.window_copies(16 if ranked else 0)
         try:
             modes = {}
             res[ranked] = _dev_run(x, vp, vn, g, cfg, cuda_device, modes=modes)
         finally:
             ops.ranked_backward(prev)
+            ops.window_copies(prev_w)
         assert modes["bwd"] == (2 if ranked else 0), (ranked, modes)
     (_, dx_r, gp_r, gn_r), (_, dx_1, gp_1, gn_1) = res[True], res[False]
     assert torch.equal(gp_r, gp_1) and torch.equal(gn_r, gn_1)
@@ -281,8 +285,8 @@ def test_ranked_matches_one_copy(cuda_device, M, K, O):
 
 
 @pytest.mark.parametrize("max_copies", [3, 5, 8, 16, 32])
-def test_windowed_forward_copies(cuda_device, max_copies):
-    """The forward's windowed table copies under each cap ISA_EKV_OPT_FWD_COPIES allows (the
+def test_windowed_window_copies(cuda_device, max_copies):
+    """The forward's windowed table copies under each cap ISA_EKV_OPT_WINDOW_COPIES allows (the
     device takes as many as fit, up to the cap, and records their number): on ragged shapes
     whose coordinates reach a narrow window (mapped inputs, initial thresholds) the count is
     the cap; every case matches the oracle and the one-copy forward of the same inputs to
@@ -298,7 +302,7 @@ def test_windowed_forward_copies(cuda_device, max_copies):
     cases = (((70, 129, 300), "narrow", "init"), ((5, 40, 1000), "narrow", "init"),
              ((64, 203, 520), "mapped", "init"), ((48, 200, 300), "mapped", "full"),
              ((33, 768, 256), "signed", "init"))
-    prev = ops.forward_copies()
+    prev = ops.window_copies()
     try:
         for (M, K, O), x_mode, vth_mode in cases:
             print(f"[case] windowed copies <= {max_copies}: M={M} K={K} O={O} {x_mode}/{vth_mode}", flush=True)
@@ -308,7 +312,7 @@ def test_windowed_forward_copies(cuda_device, max_copies):
                 x = x * 0.01
             ref_out = oracle.forward(x.numpy(), vp.numpy(), vn.numpy(), oracle.lut_tables(cfg)[0], dmin, dmax,
                                      cfg["V_sat"], -4.0, 4.0)
-            ops.forward_copies(max_copies)
+            ops.window_copies(max_copies)
             modes = {}
             out, _, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device, modes=modes)
             xd, pd = x.to(cuda_device), vp.to(cuda_device)
@@ -317,7 +321,7 @@ def test_windowed_forward_copies(cuda_device, max_copies):
             zero = ops.lut_forward(xd, pd, pd.clone(), fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0, workspace=wsf)
             torch.cuda.synchronize()
             zmode = ops.copy_mode(wsf, pf)
-            ops.forward_copies(0)
+            ops.window_copies(0)
             one, _, _, _ = _dev_run(x, vp, vn, g, cfg, cuda_device)
             e = errs(out, ref_out)[0]
             d = float((out - one).abs().max()) / max(float(one.abs().max()), 1e-30)
@@ -329,7 +333,7 @@ def test_windowed_forward_copies(cuda_device, max_copies):
             assert e <= FWD_TOL and d <= FWD_TOL
             assert torch.count_nonzero(zero) == 0
     finally:
-        ops.forward_copies(prev)
+        ops.window_copies(prev)
 
 
 def test_nan_semantics(cuda_device):
