@@ -281,8 +281,9 @@ int isa_ekv_profile_end(double* ms, int* launches);
  *   [0] workspace bytes
  *   [1] byte offset in the workspace of the table-copy mode word (int32: after the call, 1 when
  *       the main kernel ran with the second, bank-rotated table copy, 0 when with one copy,
- *       2 when the backward ran ranked: see ISA_EKV_OPT_RANKED, 3 to 32 when the forward held
- *       that many windowed copies: see ISA_EKV_OPT_WINDOW_COPIES), or -1 when the call cannot
+ *       2 when the backward ran ranked: see ISA_EKV_OPT_RANKED, 3 to 32 when the main kernel
+ *       held that many windowed copies and 33 when it held two: see ISA_EKV_OPT_WINDOW_COPIES),
+ *       or -1 when the call cannot
  *       use a second copy (the word is then not written)
  *   [2] forward: K ranges summed separately (1: no split); backward: token splits
  *   [3] forward: tokens per wave; backward: inputs per wave of the one-copy kernel
@@ -311,9 +312,9 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *     default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
  *     LDS when its coordinates need no clamp, and a table backward's two-copy launch when the
  *     ranked backward does not apply (decided on the device, which takes the most copies
- *     that fit; mode word = the number of copies): each threshold then reads the copy its
- *     assignment pass chose to spread a gather's records over the LDS banks. Below 3 neither
- *     holds them.
+ *     that fit, two where three do not; mode word = the number of copies, 33 for two): each
+ *     threshold then reads the copy its assignment pass chose to spread a gather's records
+ *     over the LDS banks. Below 3 neither holds them.
  * Plans (and so workspace sizes) depend on the options: query workspace sizes after setting
  * them, and do not change them while calls are in flight. */
 #define ISA_EKV_OPT_COPY_MIN_CELLS 1

@@ -1098,12 +1098,13 @@ __device__ inline bool launch_copy_mode(const float2* __restrict__ partials, int
 }
 
 // Mode word values: 0 one table copy, 1 the second copy, kModeRanked the ranked backward (whose
-// branch-deal pass runs before the copy assignment and records its decision first), and in a
-// forward, C >= kModeMultiMin: C bank-rotated copies of the coordinate window
-// (fwd_multi_assign_kernel, which also runs before the two-copy assignment).
+// branch-deal pass runs before the copy assignment and records its decision first), and
+// C >= kModeMultiMin: C bank-rotated copies of the coordinate window (fwd_multi_assign_kernel,
+// which also runs before the two-copy assignment), recorded as kModeWindowed2 for C = 2.
 constexpr int kModeRanked = 2;
 constexpr int kModeMultiMin = 3;
 constexpr int kMultiMax = 32;
+constexpr int kModeWindowed2 = kMultiMax + 1;
 
 // LANES = 32: 8-byte records, gathered by half-waves over 32 bank pairs; LANES = 16: 16-byte
 // records, gathered by quarter-waves over 16 bank quads. Copy 1 sits LANES / 2 bins away.
@@ -1168,8 +1169,8 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
     }
 }
 
-// LUT forward with C bank-rotated copies of the coordinate window (3 <= C <= 32), the
-// generalisation of the second copy that also pays at narrow spreads. Copy c holds the
+// LUT forward with C bank-rotated copies of the coordinate window (3 <= C <= 32, or 2 where
+// three do not fit), the generalisation of the second copy that also pays at narrow spreads. Copy c holds the
 // window's records from LDS record T_c = c * stride + floor(32 c / C) (stride = the window
 // rounded up to 32 records), so its bank pairs sit floor(32 c / C) from copy 0's; a threshold
 // that takes copy c is stored as ws - T_c and copy c's records as {A - T_c dT, dT}, as for the
@@ -1178,6 +1179,7 @@ __global__ __launch_bounds__(kAssignThreads) void fwd_copy_assign_kernel(float2*
 // kernel decide it from the same range partials.
 struct MultiLayout {
     int copies, stride, lo, n;  // copies == 0: not in this mode
+    int dhalf;                  // split tables: the D halves' distance from the I halves, in records
 };
 
 // Bank-pair rotation and first LDS record of copy c.
@@ -1191,28 +1193,37 @@ __device__ inline bool clamp_free(const CoordRange& c, int NP) {
     return __builtin_amdgcn_readfirstlane((int)((c.xlo - c.whi >= 1.0f) && (c.xhi - c.wlo <= (float)(NP - 2)))) != 0;
 }
 
+// Two copies where three do not fit (wide windows): copy 1 sixteen bank pairs from copy 0.
 // dhalf > 0 (the backward's split tables): each copy also holds the D halves of its records,
-// dhalf records after its I halves, for windows of at most max_window records, and only when
-// the thresholds spread over at least kFwdCopyMinWindow records (below that the backward's
+// dhalf records after its I halves, for windows of at most max_window records (wider ones, up
+// to wide_dhalf records, with the D halves wide_dhalf records on), and only when the
+// thresholds spread over at least kFwdCopyMinWindow records (below that the backward's
 // one-copy launch, two blocks per CU, beats the copies' one block: 9.37 against 9.54 ms at the
 // headline's 69 records).
 __device__ inline MultiLayout multi_layout(const CoordRange& cr, int NP, int budget, int max_copies, int dhalf,
-                                           int max_window) {
-    MultiLayout m{0, 0, 0, NP};
-    if (max_copies < kModeMultiMin || !clamp_free(cr, NP)) return m;
-    if (dhalf > 0 && __builtin_amdgcn_readfirstlane((int)(cr.whi - cr.wlo >= kFwdCopyMinWindow)) == 0) return m;
+                                           int max_window, int wide_dhalf = 0) {
+    const MultiLayout none{0, 0, 0, NP, 0};
+    MultiLayout m = none;
+    if (max_copies < kModeMultiMin || !clamp_free(cr, NP)) return none;
+    if (dhalf > 0 && __builtin_amdgcn_readfirstlane((int)(cr.whi - cr.wlo >= kFwdCopyMinWindow)) == 0) return none;
     coord_window(cr, NP, m.lo, m.n);
-    if (m.n > max_window) return MultiLayout{0, 0, 0, NP};
+    if (m.n > max_window) {
+        if (m.n > wide_dhalf) return none;
+        dhalf = wide_dhalf;
+    }
     const int stride = (dhalf + m.n + 31) & ~31;
-    for (int c = min(max_copies, kMultiMax); c >= kModeMultiMin; --c) {
+    for (int c = min(max_copies, kMultiMax); c >= 2; --c) {
         if (multi_offset(c - 1, c, stride) + dhalf + m.n <= budget) {
             m.copies = c;
             m.stride = stride;
-            break;
+            m.dhalf = dhalf;
+            return m;
         }
     }
-    return m;
+    return none;
 }
+
+__host__ __device__ inline int multi_mode_word(int copies) { return copies == 2 ? kModeWindowed2 : copies; }
 
 __device__ inline MultiLayout fwd_multi_layout(const CoordRange& cr, int NP, int budget, int max_copies) {
     return multi_layout(cr, NP, budget, max_copies, 0, NP);
@@ -1323,10 +1334,12 @@ __device__ inline unsigned multi_lo_mask(float w, float fl) {
 __global__ __launch_bounds__(kMcThreads) void fwd_multi_assign_kernel(float2* __restrict__ wsT,
                                                           const float2* __restrict__ partials, int NP, int budget,
                                                           int max_copies, int* __restrict__ mode_word, int64_t Kp,
-                                                          int64_t Op, int dhalf, int max_window, int after_rank) {
+                                                          int64_t Op, int dhalf, int max_window, int wide_dhalf,
+                                                          int after_rank) {
     if (after_rank && ranked_mode(partials, NP)) return;
-    const MultiLayout ml = multi_layout(read_coord_range(partials), NP, budget, max_copies, dhalf, max_window);
-    if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = ml.copies;
+    const MultiLayout ml =
+        multi_layout(read_coord_range(partials), NP, budget, max_copies, dhalf, max_window, wide_dhalf);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = multi_mode_word(ml.copies);
     if (ml.copies == 0) return;
     __shared__ float s_sw[32 * kMcProblems];       // [rank][problem]: the thresholds in order
     __shared__ unsigned s_info[32 * kMcProblems];  // [rank][problem] (multi_greedy)
@@ -1855,24 +1868,26 @@ constexpr size_t kBwdTwoCopiesLdsI = (size_t)(kBwdCopyOffsetI + kSplitRecords) *
 // window's I records from LDS record T_c and their D records kBwdWinDOffset further (a
 // multiple of 32 that is not one of 64, so the two reads stay two ds_read_b64 through the
 // immediate offset), for windows of at most kBwdWinWindow records, in the whole LDS of the
-// launch's one block per CU.
+// launch's one block per CU; wider windows (any of a split table's) take two copies with the
+// D records kBwdWinWideDOffset on.
 constexpr int kBwdWinWindow = 3008;
 constexpr int kBwdWinDOffset = kBwdWinWindow + 32;
+constexpr int kBwdWinWideDOffset = kSplitRecords;
 constexpr int kBwdWinBudget = kLdsBytes / 8;  // records
+static_assert(kBwdWinDOffset % 64 == 32 && kBwdWinWideDOffset % 64 == 32, "two ds_read_b64, not one read2st64");
+static_assert(kBwdWinWideDOffset * 4 + 32 <= kBwdWinBudget, "two copies of a split table's window fit");
 using BwdTableWin = BwdTableSplitAt<kBwdWinDOffset>;
+using BwdTableWinWide = BwdTableSplitAt<kBwdWinWideDOffset>;
 
 template <bool NEED_X, bool NEED_W, bool LANE_RED, int MODE, class Table, bool FAST_ONLY>
 __device__ inline void bwd_table_items(const BwdArgs& a, const Table t, bool fast, float* red);
 
 // The windowed copies of the two-copy launch (mode word C >= kModeMultiMin): the layout from
 // the range partials as the assignment pass computed it, copy c's records {A - T_c dT, dT}.
-template <bool NEED_X, bool NEED_W>
-__device__ inline void bwd_windowed_copies(const BwdArgs& a) {
+template <bool NEED_X, bool NEED_W, class Table>
+__device__ inline void bwd_windowed_items(const BwdArgs& a, const MultiLayout& ml, int dhalf) {
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
-    const MultiLayout ml =
-        multi_layout(read_coord_range(a.partials), a.NP, a.mc_budget, a.mc_max, kBwdWinDOffset, kBwdWinWindow);
-    if (ml.copies == 0) return;  // (not reached: the pass records a count only when it fits)
     const int n = ml.n, total = n * ml.copies;
     for (int q = threadIdx.x; q < total; q += blockDim.x) {
         const int c = q / n, i = q - c * n;
@@ -1880,11 +1895,21 @@ __device__ inline void bwd_windowed_copies(const BwdArgs& a) {
         const int tc = multi_offset(c, ml.copies, ml.stride);
         const float ft = (float)tc;
         s_split[tc + i] = make_float2(fmaf(-ft, r.y, r.x), r.y);
-        s_split[tc + kBwdWinDOffset + i] = make_float2(fmaf(-ft, r.w, r.z), r.w);
+        s_split[tc + dhalf + i] = make_float2(fmaf(-ft, r.w, r.z), r.w);
     }
     __syncthreads();
-    bwd_table_items<NEED_X, NEED_W, true, kBwdTwoCopies, BwdTableWin, true>(a, BwdTableWin{s_split - ml.lo}, true,
-                                                                             nullptr);
+    bwd_table_items<NEED_X, NEED_W, true, kBwdTwoCopies, Table, true>(a, Table{s_split - ml.lo}, true, nullptr);
+}
+
+template <bool NEED_X, bool NEED_W>
+__device__ inline void bwd_windowed_copies(const BwdArgs& a) {
+    const MultiLayout ml = multi_layout(read_coord_range(a.partials), a.NP, a.mc_budget, a.mc_max, kBwdWinDOffset,
+                                        kBwdWinWindow, kBwdWinWideDOffset);
+    if (ml.copies == 0) return;  // (not reached: the pass records a count only when it fits)
+    if (ml.dhalf == kBwdWinDOffset)
+        bwd_windowed_items<NEED_X, NEED_W, BwdTableWin>(a, ml, kBwdWinDOffset);
+    else
+        bwd_windowed_items<NEED_X, NEED_W, BwdTableWinWide>(a, ml, kBwdWinWideDOffset);
 }
 
 template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED, int MODE>
@@ -3917,7 +3942,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
             hipLaunchKernelGGL(fwd_multi_assign_kernel, dim3((unsigned)((problems + kMcProblems - 1) / kMcProblems)),
                                dim3(kMcThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials, fa.NP, tc.mc_budget,
-                               tc.mc_max, mode, p.Kp, p.Op, 0, fa.NP, 0);
+                               tc.mc_max, mode, p.Kp, p.Op, 0, fa.NP, 0, 0);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward windowed-copy assignment launch");
         }
@@ -4096,7 +4121,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
             hipLaunchKernelGGL(fwd_multi_assign_kernel, dim3((unsigned)((problems + kMcProblems - 1) / kMcProblems)),
                                dim3(kMcThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials,
                                ba.NP, kBwdWinBudget, p.mc_max, mode, p.Kp, p.Op, kBwdWinDOffset, kBwdWinWindow,
-                               p.ranked ? 1 : 0);
+                               kBwdWinWideDOffset, p.ranked ? 1 : 0);
         }
         // (a pass before it recorded the ranked mode or the windowed copies: skip_from)
         const int skip_from = p.ranked ? kModeRanked : p.mc_max > 0 ? kModeMultiMin : 0;

@@ -124,8 +124,9 @@ def test_headline_fc1_table_copies(cuda_device, size, vth_mode):
     else:
         if vth_mode == "init":
             assert 3 <= modes["fwd"] <= 16 and modes["bwd"] == 2, modes
-        else:  # the two-copy launch, with windowed copies when three fit its LDS
-            assert 3 <= modes["fwd"] <= 16 and (modes["bwd"] == 1 or 3 <= modes["bwd"] <= 16), modes
+        else:  # the two-copy launch, with windowed copies (33: two) where the window fits
+            assert (3 <= modes["fwd"] <= 16 or modes["fwd"] == 33) and (modes["bwd"] in (1, 33) or
+                                                                      3 <= modes["bwd"] <= 16), modes
     _check_samples(x, vp, vn, g, res, cfg, rng)
     again = _run(x, vp, vn, g, cfg, cuda_device)
     for a, b in zip(res, again):

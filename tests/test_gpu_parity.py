@@ -179,7 +179,7 @@ def test_parity_8192_entries_table_modes(cuda_device, x_mode, vth_mode):
         e = [errs(out, ref_out)[0], errs(gx, ref_dx)[0], errs(gp, ref_gp)[0], errs(gn, ref_gn)[0]]
         print(modes, [f"{v:.2e}" for v in e])
         if fit:
-            assert modes["bwd"] == 2 and (modes["fwd"] == 1 or 3 <= modes["fwd"] <= 16), modes
+            assert modes["bwd"] == 2 and (modes["fwd"] in (1, 33) or 3 <= modes["fwd"] <= 16), modes
         else:
             assert modes == {"fwd": 0, "bwd": 0}, modes
         assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, (M, K, O, e)
