@@ -2101,51 +2101,61 @@ __device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP) 
 // branch index), so ties keep a fixed order, and rank r goes to half-wave h = r / (B / 2)
 // (B branches per class), lane c + kRankClasses (r' mod L) + 32 h and slot r' / L, where
 // r' = r mod (B / 2) and L = the class's lanes per half-wave. Block 0 records the mode word.
+// A block deals kRankQ (input, output block) pairs and writes their dealt thresholds from LDS
+// as one contiguous run (each thread's own stores would land 32 bytes apart across a wave).
+constexpr int kRankQ = 256 / kRankClasses;
 __global__ __launch_bounds__(256) void bwd_rank_kernel(RankArgs a) {
-    const bool on = ranked_mode(a.partials, a.NP);
+    const bool on = ranked_mode(a.partials, a.NP);  // block-uniform: every wave reads the same partials
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.mode_word = on ? kModeRanked : 0;
     if (!on) return;
-    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= (int64_t)a.Kp * a.n_ob * kRankClasses) return;
-    const int c = (int)(p % kRankClasses);
-    const int64_t q = p / kRankClasses;  // k * n_ob + ob
-    const int ob = (int)(q % a.n_ob);
-    const int64_t k = q / a.n_ob;
-    const float2* src = a.wsT + k * a.Op + (int64_t)ob * 256 + c;
-    float key[kRankBranches];  // branch i: output c + kRankClasses (i / 2), sign i % 2
+    __shared__ float4 s_dealt[kRankQ * 64 * 2];  // per pair: 64 lanes x 8 slots
+    const int64_t n_q = (int64_t)a.Kp * a.n_ob;
+    const int64_t q0 = (int64_t)blockIdx.x * kRankQ;
+    const int tq = threadIdx.x / kRankClasses, c = threadIdx.x % kRankClasses;
+    const int64_t q = q0 + tq;  // k * n_ob + ob
+    if (q < n_q) {
+        const int ob = (int)(q % a.n_ob);
+        const int64_t k = q / a.n_ob;
+        const float2* src = a.wsT + k * a.Op + (int64_t)ob * 256 + c;
+        float key[kRankBranches];  // branch i: output c + kRankClasses (i / 2), sign i % 2
 #pragma unroll
-    for (int t = 0; t < kRankOut; ++t) {
-        const float2 w = src[kRankClasses * t];
-        key[2 * t] = w.x;
-        key[2 * t + 1] = w.y;
-    }
-    float* dst = a.ws_ranked + q * 64 * 8;
-    unsigned codes[2 * kRankLanesHalf][2] = {};  // per lane of the class: slots 0-3, 4-7
+        for (int t = 0; t < kRankOut; ++t) {
+            const float2 w = src[kRankClasses * t];
+            key[2 * t] = w.x;
+            key[2 * t + 1] = w.y;
+        }
+        float* dst = reinterpret_cast<float*>(s_dealt) + tq * 64 * 8;
+        unsigned codes[2 * kRankLanesHalf][2] = {};  // per lane of the class: slots 0-3, 4-7
 #pragma unroll
-    for (int i = 0; i < kRankBranches; ++i) {
-        int rank = 0;
+        for (int i = 0; i < kRankBranches; ++i) {
+            int rank = 0;
 #pragma unroll
-        for (int j = 0; j < kRankBranches; ++j) rank += (key[j] < key[i] || (key[j] == key[i] && j < i)) ? 1 : 0;
-        const int h = rank / (kRankBranches / 2), r1 = rank % (kRankBranches / 2);
-        const int li = r1 % kRankLanesHalf, slot = r1 / kRankLanesHalf;
-        dst[(c + kRankClasses * li + 32 * h) * 8 + slot] = key[i];
-        const unsigned code = (unsigned)((i >> 1) | ((i & 1) << 4)) << (8 * (slot & 3));
+            for (int j = 0; j < kRankBranches; ++j) rank += (key[j] < key[i] || (key[j] == key[i] && j < i)) ? 1 : 0;
+            const int h = rank / (kRankBranches / 2), r1 = rank % (kRankBranches / 2);
+            const int li = r1 % kRankLanesHalf, slot = r1 / kRankLanesHalf;
+            dst[(c + kRankClasses * li + 32 * h) * 8 + slot] = key[i];
+            const unsigned code = (unsigned)((i >> 1) | ((i & 1) << 4)) << (8 * (slot & 3));
 #pragma unroll
-        for (int l = 0; l < 2 * kRankLanesHalf; ++l)
-            if (l == h * kRankLanesHalf + li) {
-                if (slot < 4)
-                    codes[l][0] |= code;
-                else
-                    codes[l][1] |= code;
+            for (int l = 0; l < 2 * kRankLanesHalf; ++l)
+                if (l == h * kRankLanesHalf + li) {
+                    if (slot < 4)
+                        codes[l][0] |= code;
+                    else
+                        codes[l][1] |= code;
+                }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int li = 0; li < kRankLanesHalf; ++li) {
+                const int l = h * kRankLanesHalf + li;
+                a.branch[q * 64 + c + kRankClasses * li + 32 * h] = make_uint2(codes[l][0], codes[l][1]);
             }
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int li = 0; li < kRankLanesHalf; ++li) {
-            const int l = h * kRankLanesHalf + li;
-            a.branch[q * 64 + c + kRankClasses * li + 32 * h] = make_uint2(codes[l][0], codes[l][1]);
-        }
+    __syncthreads();
+    const int n = (int)min<int64_t>(kRankQ, n_q - q0) * 64 * 2;
+    float4* out = reinterpret_cast<float4*>(a.ws_ranked + q0 * 64 * 8);
+    for (int i = threadIdx.x; i < n; i += 256) out[i] = s_dealt[i];
 }
 
 // Block = kRankWaves waves: inputs kg*W .. kg*W+W-1 (one per wave), one output block, one token split.
