@@ -336,6 +336,37 @@ def test_windowed_window_copies(cuda_device, max_copies):
         ops.window_copies(prev)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,O", [(48, 200, 300), (33, 203, 520)])
+def test_two_windowed_copies_wide_window(cuda_device, M, K, O):
+    """Inputs over [-4, 4] V against thresholds over [0, 5] V reach a ~4100-record window of
+    the 4096-entry table: three copies fit neither the forward's 80 KB nor the backward's
+    3008-record halves, so both hold two windowed copies (mode word 33; the backward's D
+    halves a split table's length on). Every output and gradient matches the oracle, and the
+    one-copy kernels (window copies off) to rounding."""
+    from isa.kernels.transformer_ffn import ops
+
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = make_inputs(M, K, O, seed=M * K, x_mode="signed", vth_mode="full")
+    ref = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
+    prev = ops.window_copies()
+    try:
+        modes = {}
+        got = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
+        ops.window_copies(0)
+        one_modes = {}
+        one = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=one_modes)
+    finally:
+        ops.window_copies(prev)
+    e = [errs(got[i], ref[i])[0] for i in range(4)]
+    d = [errs(got[i], one[i].detach().double().cpu().numpy())[0] for i in range(4)]
+    print(modes, one_modes, [f"{v:.2e}" for v in e], [f"{v:.2e}" for v in d])
+    assert modes == {"fwd": 33, "bwd": 33}, modes
+    assert one_modes["fwd"] in (0, 1) and one_modes["bwd"] in (0, 1), one_modes
+    assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, e
+    assert d[0] <= FWD_TOL and max(d[1:]) <= BWD_TOL, d
+
+
 def test_nan_semantics(cuda_device):
     """NaN x: r is NaN so its cells are NaN and the NaN row sum clamps to out_min (fminf/fmaxf);
     NaN vth reads table entry 0 like ekv_cuda.cu:19-21. Same rules as the oracle."""
