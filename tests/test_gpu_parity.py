@@ -337,22 +337,25 @@ def test_windowed_window_copies(cuda_device, max_copies):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,K,O", [(48, 200, 300), (33, 203, 520)])
-def test_two_windowed_copies_wide_window(cuda_device, M, K, O):
-    """Inputs over [-4, 4] V against thresholds over [0, 5] V reach a ~4100-record window of
-    the 4096-entry table: three copies fit neither the forward's 80 KB nor the backward's
-    3008-record halves, so both hold two windowed copies (mode word 33; the backward's D
-    halves a split table's length on). Every output and gradient matches the oracle, and the
-    one-copy kernels (window copies off) to rounding."""
+@pytest.mark.parametrize("M,K,O,x_mode", [(48, 200, 300, "signed"), (33, 203, 520, "signed"), (40, 129, 300, "mapped")])
+def test_windowed_copies_wide_spread(cuda_device, M, K, O, x_mode):
+    """Thresholds over [0, 5] V (1576 records: past the ranked backward's 420) against mapped
+    inputs reach a ~2900-record window of the 4096-entry table: both directions hold three or
+    more windowed copies. Inputs over [-4, 4] V reach ~4100 records: three copies fit neither
+    the forward's 80 KB nor the backward's 3008-record halves, so both hold two (mode word 33;
+    the backward's D halves a split table's length on). Every output and gradient matches the
+    oracle and the one-copy kernels (window copies off) to rounding, with and without dVth."""
     from isa.kernels.transformer_ffn import ops
 
     cfg = flash_cfg(4096)
-    x, vp, vn, g = make_inputs(M, K, O, seed=M * K, x_mode="signed", vth_mode="full")
+    x, vp, vn, g = make_inputs(M, K, O, seed=M * K, x_mode=x_mode, vth_mode="full")
     ref = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
     prev = ops.window_copies()
     try:
-        modes = {}
+        modes, modes_x = {}, {}
         got = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
+        got_x = _dev_run(x, vp, vn, g, cfg, cuda_device, need_w=False, out_min=-math.inf, out_max=math.inf,
+                         modes=modes_x)
         ops.window_copies(0)
         one_modes = {}
         one = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=one_modes)
@@ -360,11 +363,16 @@ def test_two_windowed_copies_wide_window(cuda_device, M, K, O):
         ops.window_copies(prev)
     e = [errs(got[i], ref[i])[0] for i in range(4)]
     d = [errs(got[i], one[i].detach().double().cpu().numpy())[0] for i in range(4)]
-    print(modes, one_modes, [f"{v:.2e}" for v in e], [f"{v:.2e}" for v in d])
-    assert modes == {"fwd": 33, "bwd": 33}, modes
+    ex = errs(got_x[1], ref[1])[0]
+    print(modes, modes_x["bwd"], one_modes, [f"{v:.2e}" for v in e], [f"{v:.2e}" for v in d], f"{ex:.2e}")
+    if x_mode == "signed":
+        assert modes == {"fwd": 33, "bwd": 33} and modes_x["bwd"] == 33, (modes, modes_x)
+    else:
+        assert 3 <= modes["fwd"] <= 16 and 3 <= modes["bwd"] <= 16 and modes_x["bwd"] == modes["bwd"], (modes, modes_x)
     assert one_modes["fwd"] in (0, 1) and one_modes["bwd"] in (0, 1), one_modes
     assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, e
     assert d[0] <= FWD_TOL and max(d[1:]) <= BWD_TOL, d
+    assert ex <= BWD_TOL and got_x[2] is None and got_x[3] is None, ex
 
 
 def test_nan_semantics(cuda_device):
