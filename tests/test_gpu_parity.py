@@ -375,6 +375,32 @@ def test_windowed_copies_wide_spread(cuda_device, M, K, O, x_mode):
     assert ex <= BWD_TOL and got_x[2] is None and got_x[3] is None, ex
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("spread_records", [380, 460])
+def test_ranked_spread_limit(cuda_device, spread_records):
+    """The ranked backward runs while the thresholds span at most 420 table records (decided
+    on the device from the range partials) and the two-copy launch's windowed copies past
+    that: thresholds uniform over 380 and 460 records (4096 entries: 315 records per volt)
+    from 1 V, mapped inputs. Both sides of the limit match the oracle."""
+    cfg = flash_cfg(4096)
+    M, K, O = 64, 96, 300
+    x, _, _, g = make_inputs(M, K, O, seed=spread_records)
+    gen = torch.Generator().manual_seed(spread_records + 1)
+    span = spread_records * 13.0 / 4095.0  # volts
+    vp = 1.0 + torch.rand(O, K, generator=gen) * span
+    vn = 1.0 + torch.rand(O, K, generator=gen) * span
+    ref = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
+    modes = {}
+    got = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
+    e = [errs(got[i], ref[i])[0] for i in range(4)]
+    print(spread_records, modes, [f"{v:.2e}" for v in e])
+    if spread_records <= 420:
+        assert modes["bwd"] == 2, modes
+    else:
+        assert 3 <= modes["bwd"] <= 16, modes
+    assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, e
+
+
 def test_nan_semantics(cuda_device):
     """NaN x: r is NaN so its cells are NaN and the NaN row sum clamps to out_min (fminf/fmaxf);
     NaN vth reads table entry 0 like ekv_cuda.cu:19-21. Same rules as the oracle."""
