@@ -175,6 +175,66 @@ def measured_traffic(config: str):
     return None, None
 
 
+def issued_valu_per_cell() -> dict:
+    """Issued VALU lane-instructions per cell-eval of each LUT main kernel, from the committed
+    rocprofv3 SQ_INSTS_VALU summary (lines "valu_per_cell <kernel>: <value>"): the counters
+    need a rocprofv3 --pmc run of their own, so this run does not measure them."""
+    path = ROOT / "profiles" / "counters_gptl_ffn_bench.md"
+    out = {}
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("valu_per_cell "):
+                name, val = line[len("valu_per_cell "):].split(":", 1)
+                out[name.strip()] = float(val)
+    except OSError:
+        pass
+    return out
+
+
+def measured_ceiling(kt, cells_launch: float, fwd_ms: float, bwd_ms: float, dev) -> dict:
+    """Each LUT main kernel against the VALU issue rate it can reach on this GPU: the issued
+    VALU wave-instructions of one launch (committed SQ_INSTS_VALU per cell x cells / 64) over
+    (the register-only replay's wave-instructions per CU-cycle for the kernel's mix x CUs x the
+    shader clock the kernel's own blocks ran at during the timed steps, clock64 / wall_clock64)
+    gives the launch time if VALU issue were its only limit; frac = that / the measured launch
+    time, at most 1. The replay (isa_ekv_probe_valu_issue) runs after the timed steps."""
+    import torch
+
+    from isa.kernels.transformer_ffn import ops
+
+    per_cell = issued_valu_per_cell()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    probes = {mix: ops.probe_valu_issue(mix, device=dev) for mix in ("fma", "forward", "ranked_backward")}
+    bwd_name = max(("bwd_kernel", "bwd_two_copies_kernel", "bwd_ranked_kernel"),
+                   key=lambda n: kt.clocks[n]["block_seconds"])
+
+    def one(name: str, avg_ms: float, mix: str) -> dict:
+        clk = kt.clocks[name]
+        ghz, n = clk["ghz"], per_cell.get(name)
+        res = {"kernel": name, "kernel_ghz": round(ghz, 4) if ghz else None, "issued_valu_per_cell": n,
+               "replay_mix": mix, "replay_instr_per_cu_cycle": round(probes[mix]["instr_per_cu_cycle"], 4),
+               "avg_launch_ms": round(avg_ms, 4)}
+        if ghz and n and avg_ms:
+            wave_instr = n * cells_launch / 64.0
+            ceiling_ms = wave_instr / (probes[mix]["instr_per_cu_cycle"] * cus * ghz * 1e9) * 1e3
+            res.update(ceiling_ms=round(ceiling_ms, 4), frac=round(ceiling_ms / avg_ms, 4),
+                       issue_rate_instr_per_cu_cycle=round(wave_instr / (cus * ghz * 1e9 * avg_ms * 1e-3), 4))
+        return res
+
+    return {
+        "bound": "valu issue, measured",
+        "backward": one(bwd_name, bwd_ms, "ranked_backward"),
+        "forward": one("fwd_kernel", fwd_ms, "forward"),
+        "fma_issue_instr_per_cu_cycle": round(probes["fma"]["instr_per_cu_cycle"], 4),
+        "replay_ghz": {m: round(p.get("ghz", 0.0), 4) for m, p in probes.items()},
+        "source": "issued_valu_per_cell: profiles/counters_gptl_ffn_bench.md (rocprofv3 SQ_INSTS_VALU, not this "
+                  "run); kernel_ghz: clock64 / wall_clock64 of every block of the kernel during the timed steps "
+                  "(isa_ekv_profile_clock); replay: isa_ekv_probe_valu_issue after the timed steps (the kernel's "
+                  "VALU mix on registers only, at its occupancy; the one- and two-copy backwards are priced "
+                  "with the ranked backward's mix)",
+    }
+
+
 def measured_fc1_step(args) -> int:
     """The measured-codebook deployment of a Physical ViT-S fc1 (192 -> 768, measured
     mode, forward and dX) over X[128, 65, 192] with a synthetic 24-state, 61-point codebook
@@ -441,9 +501,10 @@ def main() -> int:
     ap.add_argument("--graph", action="store_true",
                     help="time the step as replays of one captured HIP graph (torch.cuda.CUDAGraph): "
                          "no host launch cost; the per-kernel figures come from an eager pass after")
-    ap.add_argument("--engine-thread", action="store_true",
-                    help="run the backward on torch's autograd device thread (its default) instead of the "
-                         "calling thread; the handoff between the two threads costs ~85 us per eager step")
+    ap.add_argument("--calling-thread", action="store_true",
+                    help="run the backward on the calling thread (torch.autograd.set_multithreading_enabled"
+                         "(False)) instead of torch's autograd device thread (its default); the handoff "
+                         "between the two threads costs ~40-85 us per eager step")
     ap.add_argument("--no-ranked", action="store_true",
                     help="plan the table backwards without the ranked kernel (isa_ekv_set_option "
                          "ISA_EKV_OPT_RANKED = 0): the one- or two-copy kernel runs instead")
@@ -464,11 +525,12 @@ def main() -> int:
               "over tokens with one all-reduce of dVth per layer). Run with --gpus 1.", file=sys.stderr)
         return 2
 
-    if not args.engine_thread:
+    if args.calling_thread:
         # The steps run their backward on the calling thread (a documented torch setting that
         # changes no result): for small layers the wake-up of torch's per-device autograd thread
-        # and the wait for it cost more host time than the library's launches. The CIM configs'
-        # JSON also reports the eager step with the engine thread (host.eager_ms_engine_thread).
+        # and the wait for it cost more host time than the library's launches. By default the
+        # value is timed under torch's default threading, and the CIM configs' JSON reports
+        # the eager step on the calling thread beside it (host.eager_ms_calling_thread).
         import torch
 
         torch.autograd.set_multithreading_enabled(False)
@@ -589,10 +651,10 @@ def main() -> int:
         log(f"[bench] {args.config}: eager step {eager_ms:.3f} ms (host launches included)")
     value = cells_step / (ms * 1e-3)
     median_ms = statistics.median(step_ms) if step_ms else ms
-    host = {"autograd_thread": "engine" if args.engine_thread else "calling"}
+    host = {"autograd_thread": "calling" if args.calling_thread else "engine (torch default)"}
     if graph is None:
         # the same eager step with the other autograd threading, for comparison (not the value)
-        torch.autograd.set_multithreading_enabled(not args.engine_thread)
+        torch.autograd.set_multithreading_enabled(args.calling_thread)
         for _ in range(2):
             step()
         torch.cuda.synchronize()
@@ -601,9 +663,9 @@ def main() -> int:
             step()
         torch.cuda.synchronize()
         other = 1e3 * (time.perf_counter() - t0) / args.steps
-        torch.autograd.set_multithreading_enabled(args.engine_thread)
-        host["eager_ms_calling_thread" if args.engine_thread else "eager_ms_engine_thread"] = round(other, 4)
-        log(f"[bench] eager step with the {'calling' if args.engine_thread else 'engine'} thread: {other:.3f} ms")
+        torch.autograd.set_multithreading_enabled(not args.calling_thread)
+        host["eager_ms_engine_thread" if args.calling_thread else "eager_ms_calling_thread"] = round(other, 4)
+        log(f"[bench] eager step with the {'engine' if args.calling_thread else 'calling'} thread: {other:.3f} ms")
     log(f"[bench] {args.config}: {ms:.3f} ms/step mean, {median_ms:.3f} median"
         f"{' (graph replay)' if graph is not None else ''} "
         f"(wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
@@ -631,6 +693,9 @@ def main() -> int:
         "peak": round(peak, 3),
         "unit": "TOP/s",
         "frac": round(achieved / peak, 4),
+        "model": f"the contract model: {bwd_instr} (backward) / {fwd_instr} (forward) VALU lane-instr per cell-eval "
+                 "at 256 CU x 64 lanes x 2.4 GHz; the kernels issue other counts and gfx950 issues more than one "
+                 "VALU instruction per CU-cycle, so these fractions are not utilisation (measured_ceiling is)",
         "traffic": None if exact else measured_traffic(args.config)[0],
         "traffic_source": None if exact else measured_traffic(args.config)[1],
         "kernel": ("bwd_exact_kernel<true,true> (backward main kernel, dominant)" if exact else
@@ -656,17 +721,14 @@ def main() -> int:
             f"{roofline['lds']['ns_per_gather_per_cu']:.3f} ns per gather per CU): fwd "
             f"{roofline['lds']['forward_frac']:.3f}, bwd {roofline['lds']['backward_frac']:.3f}; "
             f"conflict-free {roofline['lds']['conflict_free_frac']}")
-        if clock.get("ghz"):
-            # the same kernels priced at the shader clock the CUs sustained under a gather load
-            ghz = clock["ghz"]
-            roofline["sustained_clock"] = {
-                "ghz": round(ghz, 4),
-                "frac": round(roofline["frac"] * 2.4 / ghz, 4),
-                "forward_frac": round(roofline["forward_kernel"]["frac"] * 2.4 / ghz, 4),
-                "source": "clock64 cycles / wall_clock64 time of each CU's first wave in the LDS gather probe "
-                          "launched right after the timed steps (median over blocks)",
-            }
-            log(f"[bench] sustained shader clock {ghz:.3f} GHz: bwd frac {roofline['sustained_clock']['frac']:.3f}")
+        roofline["lds"]["probe_ghz"] = round(clock["ghz"], 4) if clock.get("ghz") else None
+        mc = measured_ceiling(kt, cells_launch, fwd_avg, bwd_avg, dev)
+        roofline["measured_ceiling"] = mc
+        for side in ("backward", "forward"):
+            r = mc[side]
+            log(f"[bench] measured VALU ceiling, {r['kernel']}: {r.get('kernel_ghz')} GHz during the steps, "
+                f"{r['issued_valu_per_cell']} VALU/cell, replay {r['replay_instr_per_cu_cycle']} instr/CU-cycle "
+                f"-> ceiling {r.get('ceiling_ms')} ms vs {r['avg_launch_ms']} ms: frac {r.get('frac')}")
 
     cpu = None
     lut_cpu = None

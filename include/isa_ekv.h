@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ISA_EKV_ABI_VERSION 9
+#define ISA_EKV_ABI_VERSION 10
 #define ISA_EKV_EINVAL (-1)
 
 /* LUT layouts produced by isa_ekv_lut_build */
@@ -274,6 +274,18 @@ int isa_ekv_measured_backward(const float* x, const int16_t* ids_a, const int16_
 int isa_ekv_profile_begin(void);
 int isa_ekv_profile_end(double* ms, int* launches);
 
+/* Profiling aid, no reference counterpart: the shader clock the LUT main kernels ran at.
+ * Between isa_ekv_profile_begin (which clears the current device's sample buffer) and this
+ * call, every block of a LUT forward main kernel (kind 0: fwd_kernel), of the table backward's
+ * one-copy kernel (kind 1: bwd_kernel), two-copy kernel (kind 2: bwd_two_copies_kernel) and
+ * ranked kernel (kind 3: bwd_ranked_kernel) launched on the current device adds the clock64
+ * cycles and the wall_clock64 time of its first wave (the launches of a backward's set that
+ * are not the working one exit within microseconds and add little). Synchronises with the
+ * device and writes out[3 k + 0] = summed shader cycles, out[3 k + 1] = summed seconds,
+ * out[3 k + 2] = blocks, for k = 0..3 (12 values); cycles / seconds is the mean shader clock
+ * under each kernel's own load. All zero when nothing was sampled. */
+int isa_ekv_profile_clock(double* out);
+
 /* Plan of a LUT call at this shape (test and measurement aid, no reference counterpart).
  * which: ISA_EKV_PLAN_FORWARD (isa_ekv_forward, isa_ekv_layer_forward), ISA_EKV_PLAN_BACKWARD
  * (isa_ekv_backward), ISA_EKV_PLAN_LAYER_BACKWARD (isa_ekv_layer_backward). Writes
@@ -335,6 +347,20 @@ int isa_ekv_set_option(int option, int64_t value, int64_t* previous);
  * clock the CUs sustained while gathering. */
 int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iterations, float* out, int64_t out_floats,
                              int* gathers_per_cu, int64_t* clocks, int* wall_clock_khz, void* stream);
+
+/* Measurement aid, no reference counterpart: the VALU issue rate of the table kernels'
+ * instruction mixes, replayed on registers only (no LDS or memory access in the loop), two
+ * blocks per CU. mix 0: 32 independent fma chains (the raw issue rate), 16-wave blocks; mix 1:
+ * the ranked backward's branch-token body (288 VALU per iteration), 16-wave blocks; mix 2: the
+ * LUT forward's cell (320 VALU per iteration), 8-wave blocks. tokens: device, 64 float4 token
+ * records {coordinate, r, -r/V_sat, 0} read with scalar loads, as the kernels read theirs
+ * (coordinates within [4, 4000]). out: device scratch of >= 2 x CU count x (64 x waves per
+ * block) floats. clocks (nullable, device, 2 x blocks int64): per block, the clock64 cycles and
+ * wall_clock64 ticks of its first wave; *wall_clock_khz (nullable) the wall clock's rate.
+ * *instr_per_cu (nullable) receives the VALU wave-instructions each CU issues in the loops, so
+ * instr_per_cu / cycles is the issue rate per CU-cycle. Asynchronous on `stream`. */
+int isa_ekv_probe_valu_issue(int mix, int iterations, const float* tokens, float* out, int64_t out_floats,
+                             int64_t* clocks, double* instr_per_cu, int* wall_clock_khz, void* stream);
 
 #ifdef __cplusplus
 }

@@ -174,6 +174,24 @@ void prof_stop(hipStream_t s, ProfiledLaunch* slot) {
     if (slot) (void)hipEventRecord(slot->stop, s);
 }
 
+// Shader-clock sampling of the main kernels while profiling (isa_ekv_profile_begin/_clock): a
+// per-device buffer of kClockKinds x {shader cycles, wall-clock ticks, blocks} (the backward's
+// three kinds adjacent: a backward launch set gets the first, the two-copy kernel adds 3 and the
+// ranked kernel 6), to which wave 0
+// of every block of an instrumented main kernel adds its own clock64 / wall_clock64 spans
+// (BlockClock). The cycle sum over the tick sum is the mean shader clock the CUs ran that
+// kernel at, under its own load (the board lowers the clock under heavy VALU + LDS work).
+constexpr int kClockKinds = 4;   // 0 LUT forward, 1 one-copy, 2 two-copy and 3 ranked table backward
+constexpr int kClockMaxDevices = 64;
+unsigned long long* g_clock_buf[kClockMaxDevices] = {};
+
+unsigned long long* clock_acc(int kind) {
+    if (!g_profiling) return nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kClockMaxDevices || !g_clock_buf[dev]) return nullptr;
+    return g_clock_buf[dev] + 3 * kind;
+}
+
 // Times a whole library call (every kernel it enqueues), closing on every return path.
 struct CallTimer {
     hipStream_t stream;
@@ -837,6 +855,29 @@ __device__ inline bool exact_operands_in_fast_range(const float2* __restrict__ p
 // 64*ORR outputs; wave w owns tokens [ (tile_m * FWD_WAVES + w) * MR, +MR ).
 // ----------------------------------------------------------------------------------
 
+// A block's shader-clock span (profiling only, acc non-null): every wave reads clock64 (shader
+// cycles, s_memtime) and wall_clock64 (constant-rate ticks, s_memrealtime) into scalar
+// registers at the start; wave 0 adds its spans and a block count to acc with vector atomics at
+// the end. acc is a kernel argument, so the branch is uniform and costs no VGPRs.
+struct BlockClock {
+    unsigned long long* acc;
+    long long c0, w0;
+    __device__ explicit BlockClock(unsigned long long* a) : acc(a), c0(0), w0(0) {
+        if (acc) {
+            c0 = clock64();
+            w0 = wall_clock64();
+        }
+    }
+    __device__ void stop() const {
+        if (acc && threadIdx.x == 0) {
+            const long long c1 = clock64(), w1 = wall_clock64();
+            atomicAdd(acc, (unsigned long long)(c1 - c0));
+            atomicAdd(acc + 1, (unsigned long long)(w1 - w0));
+            atomicAdd(acc + 2, 1ull);
+        }
+    }
+};
+
 struct FwdArgs {
     const float2* xrec;     // [M][Kp] token records {t, r}
     const float2* wsT;      // [Kp][Op] threshold records
@@ -867,6 +908,7 @@ struct FwdArgs {
     int copy_offset;        // LUT: T1 > 0 when the launch may use the second table copy
     int copy_window;        // LUT: > 0: the copies hold only the coordinate window, of at most this many records
     int mc_budget, mc_max;  // LUT: mc_budget > 0: the launch may hold up to mc_max windowed copies in this many LDS records
+    unsigned long long* clock_acc;  // profiling: {cycles, wall ticks, blocks} of this kernel (BlockClock), or null
 };
 
 // The work of one forward wave.
@@ -1442,6 +1484,7 @@ __device__ inline void stage_table2(float2* dst, const float2* __restrict__ src,
 template <int MR, bool SPLITS, bool WIN = false>
 __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
+    const BlockClock clk(a.clock_acc);
     if constexpr (!WIN) stage_table2(s_lut_fwd, a.lut, a.NP);
     // fast loop and copy mode from one read of the range partials (as coords_in_padded_range,
     // fwd_copies_mode, launch_copy_mode and fwd_multi_layout decide them; a second read costs
@@ -1477,12 +1520,14 @@ __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     }
     __syncthreads();
     FwdTile t;
-    if (!fwd_tile<SPLITS>(a, MR, t)) return;
-    const float2* tab = WIN ? s_lut_fwd - lo : s_lut_fwd;  // record i of the table at LDS record i - lo
-    if (fast)
-        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
-    else
-        fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+    if (fwd_tile<SPLITS>(a, MR, t)) {
+        const float2* tab = WIN ? s_lut_fwd - lo : s_lut_fwd;  // record i of the table at LDS record i - lo
+        if (fast)
+            fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+        else
+            fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+    }
+    clk.stop();
 }
 
 // LUT forward with the table in global memory (tables past kMaxEntriesFwd; the reference's
@@ -1538,6 +1583,7 @@ struct BwdArgs {
     float cmin, cmax;
     float k2, c2;           // exact: 2^(-V_D a), V_D a
     int mc_budget, mc_max;  // split tables: the two-copy launch may hold up to mc_max windowed copies
+    unsigned long long* clock_acc;  // profiling: {cycles, wall ticks, blocks} of this kernel (BlockClock), or null
 };
 
 // LDS table views for the backward. Interleaved: one 16-byte record {A_I, dI, A_D, dD} per
@@ -1799,6 +1845,9 @@ __device__ inline void bwd_body(const BwdArgs& a, const Cell cell, const float4*
             if (a.dv_group) {  // block-uniform
                 static_assert(ORR == 4, "one 16-byte slot per lane, input and sign");
                 constexpr int kSlice = 2 * KR * 64;  // float4 slots per wave: [sign][input][lane]
+                // 16 waves' slices reuse the split table's allocation (kSplitRecords 16-byte
+                // records, the smallest a grouped plan launches with)
+                static_assert(16 * kSlice * 16 <= kSplitRecords * 16, "grouped dVth sums exceed the table's LDS");
                 __syncthreads();                     // no wave of the block reads the table any more
                 float4* slots = reinterpret_cast<float4*>(dv_lds);
                 float4* mine = slots + (threadIdx.x >> 6) * kSlice;
@@ -2003,12 +2052,16 @@ __device__ inline void bwd_table_items(const BwdArgs& a, const Table t, bool fas
 template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false, int MODE = kBwdAlone>
 __global__ __launch_bounds__(1024, kBwdWavesPerEU) void bwd_kernel(BwdArgs a) {
     static_assert(MODE != kBwdTwoCopies, "bwd_two_copies_kernel");
+    const BlockClock clk(a.clock_acc);
     bwd_table_body<NEED_X, NEED_W, SPLIT, LANE_RED, MODE>(a);
+    clk.stop();  // (blocks of a launch that is not the working one exit in ~5 us and add little)
 }
 
 template <bool NEED_X, bool NEED_W, bool SPLIT>
 __global__ __launch_bounds__(1024) void bwd_two_copies_kernel(BwdArgs a) {
+    const BlockClock clk(a.clock_acc ? a.clock_acc + 3 : nullptr);  // the two-copy kind
     bwd_table_body<NEED_X, NEED_W, SPLIT, true, kBwdTwoCopies>(a);
+    clk.stop();
 }
 
 // ----------------------------------------------------------------------------------
@@ -2164,6 +2217,7 @@ template <bool NEED_W>
 __global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranked_kernel(BwdArgs a, const float* __restrict__ ws_ranked,
                                                                      const uint2* __restrict__ branch) {
     if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != kModeRanked) return;
+    const BlockClock clk(a.clock_acc ? a.clock_acc + 6 : nullptr);  // the ranked kind
     extern __shared__ float4 s_ranked[];
     char* smem = reinterpret_cast<char*>(s_ranked);
     float2* s_tab = reinterpret_cast<float2*>(smem);  // I halves [0, n), D halves [kRankDOffset, kRankDOffset + n)
@@ -2328,6 +2382,7 @@ __global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranke
             plane[(size_t)sg * a.Kp * a.Op + (unsigned)kRankClasses * t] = sg ? -acc[s] : acc[s];
         }
     }
+    clk.stop();
 }
 
 // ----------------------------------------------------------------------------------
@@ -3132,6 +3187,138 @@ __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int 
         }
     }
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+    if (clocks && threadIdx.x == 0) {
+        const long long c1 = clock64(), w1 = wall_clock64();
+        clocks[2 * blockIdx.x] = c1 - c0;
+        clocks[2 * blockIdx.x + 1] = w1 - w0;
+    }
+}
+
+// ----------------------------------------------------------------------------------
+// VALU issue probe (isa_ekv_probe_valu_issue), a measurement aid: the table kernels' VALU
+// instruction mixes replayed on registers only, no LDS or memory in the loop, at the
+// kernels' occupancy, timed per block with clock64 (shader cycles) and wall_clock64. The
+// wave-instructions a CU issues per cycle in this replay bound what the kernel itself can
+// issue: its measured ceiling, which on gfx950 exceeds one instruction per CU-cycle (the
+// second VALU pipe). Mixes, with the VALU wave-instructions of one loop iteration:
+//   0  32 independent fma chains: the raw issue rate (32);
+//   1  the ranked backward's branch-token body (bwd_ranked_kernel's group: per slot and token
+//      coordinate, cvt, address, L_I and L_D, G r, the dVth and the two dX fmas), 8 slots x 4
+//      tokens, token records by scalar loads, 16-wave blocks, two per CU (288);
+//   2  the forward's cell (LutFwdCell: per branch coordinate, cvt, address, interpolation; the
+//      difference and the accumulate), 8 tokens x 4 outputs, 8-wave blocks, two per CU (320).
+// The counts are the instructions the compiler emits for these loops (the replay's own
+// SQ_INSTS_VALU agrees); the addresses are kept live by empty asm statements, not consumed.
+// ----------------------------------------------------------------------------------
+
+constexpr int kValuProbeTokens = 64;  // token records the replay cycles through (uniform loads)
+constexpr int kValuMixInstr[3] = {32, 288, 320};
+constexpr int kValuMixWaves[3] = {16, 16, 8};  // waves per block; two blocks per CU
+
+__device__ inline void keep_live(unsigned v) { asm volatile("" ::"v"(v)); }
+
+template <int MIX>
+__global__ __launch_bounds__(1024, 8) void valu_probe_kernel(int iters, const float4* __restrict__ tok, float* out,
+                                                            long long* clocks) {
+    const int lane = threadIdx.x & 63;
+    const float lf = (float)lane;
+    const long long c0 = clock64(), w0 = wall_clock64();
+    float res = 0.0f;
+    if constexpr (MIX == 0) {
+        float acc[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) acc[j] = lf + j;
+        const float m = 0.999f + 1e-6f * lf, b = 1e-3f * lf;  // VGPR operands, as the kernels' fmas
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) acc[j] = fmaf(acc[j], m, b);
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) res += acc[j];
+    } else if constexpr (MIX == 1) {
+        float ws[8], acc[8], q[8];
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) {
+            ws[s2] = 8.0f + 0.37f * s2 + 0.01f * lf;
+            acc[s2] = 0.0f;
+            q[s2] = 1.0f + 0.01f * (lf + s2);
+        }
+        // the records' intercepts and slopes (LDS reads in the kernel): VGPR operands
+        const float t0 = 0.5f + 1e-3f * lf, t1 = 0.25f + 1e-7f * lf, t2 = 0.125f + 1e-3f * lf,
+                    t3 = 0.0625f + 1e-7f * lf;
+        const unsigned base = (unsigned)lane * 4u;
+        float tvs = 0.0f;
+        for (int it = 0; it < iters; ++it) {
+            const int m0 = (it * 4) & (kValuProbeTokens - 1);
+            float xs[4], rr[4], zz[4], tv[4];
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+                const float4 xv = load_uniform4(tok + m0 + mm);
+                xs[mm] = xv.x;
+                rr[mm] = xv.y;
+                zz[mm] = xv.z;
+                tv[mm] = 0.0f;
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 8; ++s2) {
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm) {
+                    const float cc = xs[mm] - ws[s2];
+                    const unsigned i = (unsigned)cc;
+                    keep_live((i << 3) + base);
+                    const float li = fmaf(cc, t1, t0);
+                    const float ld = fmaf(cc, t3, t2);
+                    const float gr = q[s2] * rr[mm];
+                    acc[s2] = fmaf(gr, ld, acc[s2]);
+                    tv[mm] = fmaf(gr, fmaf(zz[mm], li, ld), tv[mm]);
+                }
+                asm volatile("" : "+v"(acc[s2]));
+            }
+            // (the kernel sums tv across the wave here; the replay keeps one lane's sums live)
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) asm volatile("" : "+v"(tv[mm]));
+            tvs = tv[0];
+        }
+        res = tvs;
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) res += acc[s2];
+    } else {
+        float wp[4], wn[4], acc[8][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wp[j] = 0.3f * j + 0.01f * lf;
+            wn[j] = 0.2f * j + 0.02f * lf;
+        }
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[mm][j] = 0.0f;
+        const float t0 = 0.5f + 1e-3f * lf, t1 = 0.25f + 1e-7f * lf;
+        const unsigned base = (unsigned)lane * 4u;
+        for (int it = 0; it < iters; ++it) {
+            const int m0 = (it * 8) & (kValuProbeTokens - 1);
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm) {
+                const float4 xv = load_uniform4(tok + m0 + mm);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float cp = xv.x - wp[j], cn = xv.x - wn[j];
+                    keep_live(((unsigned)cp << 3) + base);
+                    keep_live(((unsigned)cn << 3) + base);
+                    acc[mm][j] = fmaf(fmaf(cp, t1, t0) - fmaf(cn, t1, t0), xv.y, acc[mm][j]);
+                }
+            }
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(acc[mm][j]));
+        }
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) res += acc[mm][j];
+    }
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = res;
     if (clocks && threadIdx.x == 0) {
         const long long c1 = clock64(), w1 = wall_clock64();
         clocks[2 * blockIdx.x] = c1 - c0;
@@ -3968,6 +4155,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
     set_split(p, ws, fa);
     ProfiledLaunch* prof = nullptr;
     if (timed) prof_start(s, 0, &prof);
+    if (timed && !cs.exact) fa.clock_acc = clock_acc(0);
     launch_forward(cs.exact, gtab, p.mr, p.wpb, dim3(p.blocks), lds, s, fa);
     err = hipGetLastError();
     if (err == hipSuccess) err = finish_split(p, fa, !cs.exact, s);
@@ -4149,6 +4337,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     }
     ProfiledLaunch* prof;
     prof_start(s, 1, &prof);
+    if (!cs.exact) ba.clock_acc = clock_acc(1);
     if (p.halves)
         launch_backward_halves(need_x, need_w, grid, block, p.lds_bytes, s, ba);
     else if (copies) {
@@ -4542,7 +4731,50 @@ int isa_ekv_profile_begin(void) {
         (void)hipEventDestroy(g_prof[i].stop);
     }
     g_prof_count = 0;
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) {  // no device: event timing only (nothing will launch)
+        (void)hipGetLastError();
+        g_profiling = true;
+        return 0;
+    }
+    if (dev >= 0 && dev < kClockMaxDevices) {
+        const size_t bytes = 3 * kClockKinds * sizeof(unsigned long long);
+        if (!g_clock_buf[dev]) {
+            err = hipMalloc(reinterpret_cast<void**>(&g_clock_buf[dev]), bytes);
+            if (err != hipSuccess) {
+                g_clock_buf[dev] = nullptr;
+                return hip_fail(err, "clock sample buffer");
+            }
+        }
+        err = hipMemset(g_clock_buf[dev], 0, bytes);  // synchronous: before any profiled launch
+        if (err != hipSuccess) return hip_fail(err, "clock sample buffer clear");
+    }
     g_profiling = true;
+    return 0;
+}
+
+int isa_ekv_profile_clock(double* out) {
+    static_assert(kClockKinds == 4, "isa_ekv_profile_clock writes 12 values");
+    if (!out) return fail(ISA_EKV_EINVAL, "out is null");
+    for (int i = 0; i < 3 * kClockKinds; ++i) out[i] = 0.0;
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {  // no device: nothing was sampled
+        (void)hipGetLastError();
+        return 0;
+    }
+    if (dev < 0 || dev >= kClockMaxDevices || !g_clock_buf[dev]) return 0;
+    hipError_t err = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+    if (err != hipSuccess) return hip_fail(err, "wall clock rate query");
+    if (khz <= 0) return 0;
+    unsigned long long h[3 * kClockKinds];
+    err = hipMemcpy(h, g_clock_buf[dev], sizeof(h), hipMemcpyDeviceToHost);  // after the profiled work
+    if (err != hipSuccess) return hip_fail(err, "clock sample read");
+    for (int k = 0; k < kClockKinds; ++k) {
+        out[3 * k] = (double)h[3 * k];
+        out[3 * k + 1] = (double)h[3 * k + 1] / (1e3 * khz);
+        out[3 * k + 2] = (double)h[3 * k + 2];
+    }
     return 0;
 }
 
@@ -4831,6 +5063,40 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "lds probe launch");
     if (gathers_per_cu) *gathers_per_cu = kProbeBlocksPerCU * 16 * 8 * iterations;
+    return 0;
+}
+
+int isa_ekv_probe_valu_issue(int mix, int iterations, const float* tokens, float* out, int64_t out_floats,
+                             int64_t* clocks, double* instr_per_cu, int* wall_clock_khz, void* stream) {
+    if (mix < 0 || mix > 2) return fail(ISA_EKV_EINVAL, "mix must be 0, 1 or 2 (got %d)", mix);
+    if (iterations < 1 || iterations > (1 << 20))
+        return fail(ISA_EKV_EINVAL, "iterations must be in [1, 2^20] (got %d)", iterations);
+    if (!tokens) return fail(ISA_EKV_EINVAL, "tokens is null (%d float4 token records)", kValuProbeTokens);
+    int dev = 0, cus = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return hip_fail(err, "device query");
+    const int blocks = 2 * cus, threads = kValuMixWaves[mix] * 64;
+    if (!out || out_floats < (int64_t)blocks * threads)
+        return fail(ISA_EKV_EINVAL, "out needs %lld floats (one per thread of %d blocks)",
+                    (long long)blocks * threads, blocks);
+    if (wall_clock_khz) {
+        err = hipDeviceGetAttribute(wall_clock_khz, hipDeviceAttributeWallClockRate, dev);
+        if (err != hipSuccess) return hip_fail(err, "wall clock rate query");
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const float4* tok = reinterpret_cast<const float4*>(tokens);
+    long long* clk = reinterpret_cast<long long*>(clocks);
+    if (mix == 0)
+        hipLaunchKernelGGL(valu_probe_kernel<0>, dim3(blocks), dim3(threads), 0, s, iterations, tok, out, clk);
+    else if (mix == 1)
+        hipLaunchKernelGGL(valu_probe_kernel<1>, dim3(blocks), dim3(threads), 0, s, iterations, tok, out, clk);
+    else
+        hipLaunchKernelGGL(valu_probe_kernel<2>, dim3(blocks), dim3(threads), 0, s, iterations, tok, out, clk);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "valu probe launch");
+    // VALU wave-instructions each CU issues in the loops: two blocks per CU
+    if (instr_per_cu) *instr_per_cu = 2.0 * kValuMixWaves[mix] * (double)kValuMixInstr[mix] * iterations;
     return 0;
 }
 

@@ -1,14 +1,21 @@
-"""Flash-EKV delta-V lookup tables, built on the device by the HIP library.
+"""Flash-EKV delta-V lookup tables.
 
 Mirrors `src/isa/approximations/delta_lut.py:41-63` (`get_ekv_lut_tables(cfg, device)`,
-cached per device and parameters). Differences, by design:
+cached per device and parameters). Two table modes:
 
-* the table is evaluated on the GPU in fp64 and rounded once (`isa_ekv_lut_build`)
-  instead of fp32 torch ops on the CPU plus an upload;
-* the default precision is fp32; `cfg["LUT_DTYPE"] == "bfloat16"` gives the reference's
-  bf16 tables (`delta_lut.py:35`);
-* `get_packed_tables` adds the padded kernel records (forward {I, dI}, backward
-  {I, dI, D, dD}) derived from the plain pair, cached under the same key.
+* the default, `LUT_DTYPE = "float32"`: the table is evaluated on the GPU in fp64 and
+  rounded once to fp32 (`isa_ekv_lut_build`), which follows the closed form to ~2e-7
+  relative everywhere (the fp32 torch steps of the reference lose the derivative table's
+  subthreshold end to cancellation in `1 - exp(-sp)`);
+* `LUT_DTYPE = "bfloat16"`: the reference's own tables, byte for byte. The fp32
+  intermediate is built on the host with the reference's fp32 torch steps
+  (`delta_lut.py:25-34`: fp32 `linspace`, `F.softplus`, `1 - exp(-sp)` under the
+  `sp > 20` switch, the scalar factors applied in the same order), cast to bf16 with
+  round-to-nearest-even (`:35`) and uploaded once (`:62`); the kernels then read the
+  widened bf16 values, as the reference's CUDA backward does (`cuda_backend.py:68-69`).
+
+`get_packed_tables` adds the padded kernel records (forward {I, dI}, backward
+{I, dI, D, dD}) derived from the plain pair, cached under the same key.
 """
 
 from __future__ import annotations
@@ -16,6 +23,7 @@ from __future__ import annotations
 from typing import Any, Dict, Tuple
 
 import torch
+import torch.nn.functional as F
 
 from isa.kernels.transformer_ffn import _hip, ops
 
@@ -56,6 +64,27 @@ def _cpu_key(cfg: Dict[str, Any]) -> Tuple:
     )
 
 
+def reference_bf16_tables(n: float, i_s: float, u_t: float, v_d: float, delta_min: float, delta_max: float,
+                          size: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The reference's bf16 (table_i, table_ddelta) on the host (`delta_lut.py:25-35`).
+
+    Every step is the fp32 torch operation the reference runs, in its order, because the
+    bytes depend on each rounding: the grid is fp32 `linspace`; the Python-float factors
+    (1/(2 n U_T), V_D, I_S, 2 I_S/(2 n U_T)) enter each op as fp32 scalars; the softplus is
+    torch's (threshold 20); the sigmoid is `1 - exp(-sp)`, switched to 1 where sp > 20.
+    """
+    grid = torch.linspace(delta_min, delta_max, size, dtype=torch.float32)
+    scale = 1.0 / (2.0 * n * u_t)
+    sp_hi = F.softplus(grid * scale)
+    sp_lo = F.softplus((grid - v_d) * scale)
+    one = torch.ones_like(sp_hi)
+    sig_hi = torch.where(sp_hi > 20.0, one, 1.0 - torch.exp(-sp_hi))
+    sig_lo = torch.where(sp_lo > 20.0, one, 1.0 - torch.exp(-sp_lo))
+    table_i = i_s * (sp_hi.square() - sp_lo.square())
+    table_d = i_s * 2.0 * scale * (sp_hi * sig_hi - sp_lo * sig_lo)
+    return table_i.contiguous().to(torch.bfloat16), table_d.contiguous().to(torch.bfloat16)
+
+
 _device_cache: dict[Tuple, Tuple[torch.Tensor, torch.Tensor]] = {}
 _packed_cache: dict[Tuple, Tuple[torch.Tensor, torch.Tensor]] = {}
 
@@ -78,7 +107,11 @@ def get_ekv_lut_tables(cfg: Dict[str, Any], device) -> Tuple[torch.Tensor, torch
         n, _v_sat, i_s, u_t, v_d, delta_min, delta_max, size, bf16 = key
         if size < 1:
             raise ValueError(f"LUT_DELTA_SIZE must be >= 1, got {size}")
-        tables = ops.build_plain_tables((n, u_t, i_s, v_d), delta_min, delta_max, size, device, bf16=bf16)
+        if bf16:
+            host = reference_bf16_tables(n, i_s, u_t, v_d, delta_min, delta_max, size)
+            tables = tuple(t.to(device=device) for t in host)
+        else:
+            tables = ops.build_plain_tables((n, u_t, i_s, v_d), delta_min, delta_max, size, device)
         # later users may run on other streams: finish the one-time build first
         torch.cuda.current_stream(device).synchronize()
         _device_cache[cache_key] = tables

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 LIB_NAME = "libisa_ekv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -57,7 +57,9 @@ EXPORTS = (
     "isa_ekv_measured_backward",
     "isa_ekv_profile_begin",
     "isa_ekv_profile_end",
+    "isa_ekv_profile_clock",
     "isa_ekv_probe_lds_gather",
+    "isa_ekv_probe_valu_issue",
     "isa_ekv_plan_info",
     "isa_ekv_set_option",
 )
@@ -188,6 +190,10 @@ def _declare(lib) -> None:
     lib.isa_ekv_profile_end.restype = ci
     lib.isa_ekv_probe_lds_gather.argtypes = [ci, ci, ci, vp, i64, ctypes.POINTER(ci), vp, ctypes.POINTER(ci), vp]
     lib.isa_ekv_probe_lds_gather.restype = ci
+    lib.isa_ekv_profile_clock.argtypes = [ctypes.POINTER(f64)]
+    lib.isa_ekv_profile_clock.restype = ci
+    lib.isa_ekv_probe_valu_issue.argtypes = [ci, ci, vp, vp, i64, vp, ctypes.POINTER(f64), ctypes.POINTER(ci), vp]
+    lib.isa_ekv_probe_valu_issue.restype = ci
     lib.isa_ekv_plan_info.argtypes = [ci, i64, i64, i64, ci, ci, ci, ctypes.POINTER(i64), ci]
     lib.isa_ekv_plan_info.restype = ci
     lib.isa_ekv_set_option.argtypes = [ci, i64, ctypes.POINTER(i64)]
@@ -228,7 +234,8 @@ def check(rc: int, what: str) -> None:
 
 class KernelTimer:
     """Context manager summing HIP-event durations the library records: main kernels
-    (fwd_ms, bwd_ms) and whole calls including prep and reductions (fwd_call_ms, bwd_call_ms)."""
+    (fwd_ms, bwd_ms) and whole calls including prep and reductions (fwd_call_ms, bwd_call_ms);
+    and the mean shader clock the LUT main kernels' blocks ran at (clocks)."""
 
     def __enter__(self):
         check(load().isa_ekv_profile_begin(), "isa_ekv_profile_begin")
@@ -241,6 +248,16 @@ class KernelTimer:
         self.fwd_ms, self.bwd_ms, self.fwd_call_ms, self.bwd_call_ms = ms
         self.fwd_launches, self.bwd_launches, self.fwd_calls, self.bwd_calls = n
         check(rc, "isa_ekv_profile_end")
+        clk = (ctypes.c_double * 12)()
+        check(load().isa_ekv_profile_clock(clk), "isa_ekv_profile_clock")
+        # per LUT main kernel, the mean shader clock (GHz) of its blocks, their count and their
+        # summed seconds (None / 0 when none ran)
+        self.clocks = {}
+        for name, k in (("fwd_kernel", 0), ("bwd_kernel", 1), ("bwd_two_copies_kernel", 2),
+                        ("bwd_ranked_kernel", 3)):
+            cyc, sec, blocks = clk[3 * k], clk[3 * k + 1], clk[3 * k + 2]
+            self.clocks[name] = {"ghz": cyc / sec / 1e9 if sec > 0 else None, "blocks": int(blocks),
+                                 "block_seconds": sec}
         return False
 
 

@@ -584,3 +584,52 @@ def probe_lds_gather(window_records: int, record_bytes: int = 8, iterations: int
         clock["ghz"] = float(ghz.median())
         clock["wall_clock_khz"] = khz.value
     return ms * 1e6 / per_cu.value
+
+
+VALU_MIXES = {"fma": 0, "ranked_backward": 1, "forward": 2}
+
+
+def probe_valu_issue(mix: str, iterations: int = 4096, device: Optional[torch.device] = None,
+                     repeats: int = 3) -> dict:
+    """VALU wave-instructions a CU issues per shader cycle for one of the table kernels'
+    instruction mixes replayed on registers only (isa_ekv_probe_valu_issue): "fma" (32
+    independent fma chains), "ranked_backward" or "forward". One untimed launch, then
+    `repeats` launches; returns {"instr_per_cu_cycle": median over blocks and launches of the
+    CU's loop instructions / its blocks' clock64 cycles, "ghz": the shader clock over the same
+    blocks (clock64 / wall_clock64), "ms": mean launch time by HIP events}. A measurement aid:
+    the issue rate a kernel of that mix cannot exceed."""
+    lib = _hip.load()
+    code = VALU_MIXES[mix]
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    waves = 8 if mix == "forward" else 16
+    out = torch.empty(2 * cus * 64 * waves, dtype=torch.float32, device=dev)
+    clocks = torch.zeros((repeats, 2 * cus, 2), dtype=torch.int64, device=dev)
+    g = torch.Generator().manual_seed(1)
+    tok = torch.stack([torch.rand(64, generator=g) * 3000.0 + 600.0, torch.rand(64, generator=g) * 0.5 + 0.5,
+                       -torch.rand(64, generator=g) * 0.1, torch.zeros(64)], dim=1).to(dev).contiguous()
+    per_cu = ctypes.c_double(0.0)
+    khz = ctypes.c_int(0)
+    with _hip.on_device(dev):
+        stream = _hip.stream_handle(dev)
+
+        def launch(slot):
+            ptr = None if slot is None else clocks[slot].data_ptr()
+            rc = lib.isa_ekv_probe_valu_issue(code, int(iterations), tok.data_ptr(), out.data_ptr(), out.numel(),
+                                              ptr, ctypes.byref(per_cu), ctypes.byref(khz), stream)
+            _hip.check(rc, "isa_ekv_probe_valu_issue")
+
+        launch(None)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for r in range(repeats):
+            launch(r)
+        e1.record()
+        torch.cuda.synchronize(dev)
+    c = clocks.reshape(-1, 2).double()
+    rate = per_cu.value / c[:, 0]  # both blocks of a CU run the whole time: a block's span is the CU's
+    res = {"instr_per_cu_cycle": float(rate.median()), "ms": e0.elapsed_time(e1) / repeats,
+           "instr_per_cu": per_cu.value, "mix": mix}
+    if khz.value > 0:
+        res["ghz"] = float((c[:, 0] / (c[:, 1] / (khz.value * 1e3)) / 1e9).median())
+    return res

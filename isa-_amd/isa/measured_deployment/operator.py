@@ -52,11 +52,6 @@ class _MeasuredFn(torch.autograd.Function):
         return gx, None, None, None, None, None, None, None
 
 
-# Shared codebooks (install_fused_backend): key -> the tensors of _codebook_tables, which also
-# hold the source tensors so that their ids cannot be reused while an entry is alive.
-_SHARED_CODEBOOKS: dict[tuple, dict[str, object]] = {}
-
-
 def _codebook_tables(vg: torch.Tensor, currents_a: torch.Tensor, device: torch.device, bins: int,
                      v_min: float, v_max: float) -> dict[str, object]:
     """The validated codebook on `device` and its compact coefficient tables: per-segment line
@@ -73,7 +68,7 @@ def _codebook_tables(vg: torch.Tensor, currents_a: torch.Tensor, device: torch.d
     step = mvg[1:] - mvg[:-1]
     seg_s = ((cur[:, 1:] - cur[:, :-1]) / step.unsqueeze(0)).contiguous()
     seg_c = (cur[:, :-1] - seg_s * mvg[:-1].unsqueeze(0)).contiguous()
-    book = {"source": (vg, currents_a), "vg": mvg, "currents": cur, "lookup": lookup,
+    book = {"vg": mvg, "currents": cur, "lookup": lookup,
             "segment_slopes": seg_s, "segment_intercepts": seg_c}
     if bins > 0:
         centers = torch.linspace(lookup[0], lookup[1], bins, device=device, dtype=torch.float32)
@@ -136,15 +131,13 @@ class DeploymentAwareCIMLinear(CIMLinear):
         if int(vin_lut_bins) < 0:
             raise ValueError("vin_lut_bins must be non-negative")
         device = self.vth_pos.device
-        shared = bool(getattr(type(self), "_fg50_fused_backend_installed", False))
-        key = (device.type, device.index, id(vg), id(currents_a), tuple(vg.shape), tuple(currents_a.shape),
-               int(vin_lut_bins), float(self.cfg.get("V_min", 0.0)), float(self.cfg.get("V_max", 4.0)))
-        book = _SHARED_CODEBOOKS.get(key) if shared else None
-        if book is None:
-            book = _codebook_tables(vg, currents_a, device, int(vin_lut_bins), float(self.cfg.get("V_min", 0.0)),
-                                    float(self.cfg.get("V_max", 4.0)))
-            if shared:
-                _SHARED_CODEBOOKS[key] = book
+        bins, v_min, v_max = int(vin_lut_bins), float(self.cfg.get("V_min", 0.0)), float(self.cfg.get("V_max", 4.0))
+        if bool(getattr(type(self), "_fg50_fused_backend_installed", False)):
+            from isa.measured_deployment.fused_backend import shared_codebook
+
+            book = shared_codebook(vg, currents_a, device, bins, v_min, v_max, _codebook_tables)
+        else:
+            book = _codebook_tables(vg, currents_a, device, bins, v_min, v_max)
         self.measured_vg = book["vg"]
         self.measured_currents = book["currents"]
         self.lookup_min, self.lookup_max = book["lookup"]

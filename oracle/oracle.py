@@ -118,6 +118,41 @@ def lut_tables(cfg: Optional[dict] = None, size: Optional[int] = None,
     return ti, td
 
 
+def reference_lut_tables(cfg: Optional[dict] = None, size: Optional[int] = None,
+                         delta_min: Optional[float] = None, delta_max: Optional[float] = None):
+    """The reference's own table pair, restated statement by statement from
+    `src/isa/approximations/delta_lut.py:25-35` in torch fp32 (its third-party arithmetic:
+    torch's CPU `linspace`, `softplus` and `exp`, whose roundings the bytes depend on).
+
+    Returns (fp32 table_i, fp32 table_ddelta, bf16 table_i, bf16 table_ddelta): the fp32
+    intermediate of `:31`/`:34` as numpy float32, and the `:35` cast as torch bfloat16.
+    """
+    import torch
+    import torch.nn.functional as F
+
+    cfg = dict(FLASH_PARAMS if cfg is None else cfg)
+    dmin, dmax, n_entries = lut_range(cfg)
+    if size is not None:
+        n_entries = size
+    if delta_min is not None:
+        dmin = delta_min
+    if delta_max is not None:
+        dmax = delta_max
+    n, i_s, u_t, v_d = float(cfg["n"]), float(cfg["I_S"]), float(cfg["U_T"]), float(cfg["V_D"])
+    delta = torch.linspace(dmin, dmax, n_entries, dtype=torch.float32)           # :25
+    inv_2nut = 1.0 / (2.0 * n * u_t)                                              # :26
+    u1 = delta * inv_2nut                                                         # :27
+    u2 = (delta - v_d) * inv_2nut                                                 # :28
+    sp1 = F.softplus(u1)                                                          # :29
+    sp2 = F.softplus(u2)                                                          # :30
+    base = i_s * (sp1.square() - sp2.square())                                    # :31
+    sig1 = torch.where(sp1 > 20.0, torch.ones_like(sp1), 1.0 - torch.exp(-sp1))  # :32
+    sig2 = torch.where(sp2 > 20.0, torch.ones_like(sp2), 1.0 - torch.exp(-sp2))  # :33
+    grad_delta = i_s * 2.0 * inv_2nut * (sp1 * sig1 - sp2 * sig2)                 # :34
+    return (base.numpy().copy(), grad_delta.numpy().copy(),
+            base.contiguous().to(torch.bfloat16), grad_delta.contiguous().to(torch.bfloat16))  # :35
+
+
 def lut_lookup(table: np.ndarray, delta: float, delta_min: float, delta_max: float) -> float:
     t = _f32(table)
     return float(lib().oracle_lut_lookup(_p32(t), float(delta), delta_min, delta_max, t.size))

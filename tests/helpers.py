@@ -28,6 +28,8 @@ def make_inputs(M: int, K: int, O: int, seed: int = 0, x_mode: str = "mapped", v
         x = torch.randn(M, K, generator=g).clamp(0.0, 4.0)
     elif x_mode == "signed":        # fc2-like inputs in [-4, 4]
         x = (torch.rand(M, K, generator=g) * 8.0 - 4.0)
+    elif x_mode == "fc2init":       # fc2 at initialisation: TIA outputs within +-0.3 V of 0
+        x = (torch.rand(M, K, generator=g) * 0.6 - 0.3)
     elif x_mode == "wide":          # drives coordinates past both table ends
         x = torch.rand(M, K, generator=g) * 40.0 - 20.0
     else:
@@ -47,9 +49,19 @@ def make_inputs(M: int, K: int, O: int, seed: int = 0, x_mode: str = "mapped", v
     return x, vp, vn, grad
 
 
+def oracle_tables(cfg):
+    """The oracle's fp32 (table_i, table_ddelta) for cfg's table mode: the rounded fp64 table
+    (LUT_DTYPE float32), or the reference's bf16 bytes widened to fp32 (LUT_DTYPE bfloat16,
+    delta_lut.py:25-35 and the .float() of cuda_backend.py:68-69)."""
+    if str(cfg.get("LUT_DTYPE", "float32")).lower() in ("bfloat16", "bf16"):
+        _, _, bi, bd = oracle.reference_lut_tables(cfg)
+        return bi.float().numpy(), bd.float().numpy()
+    return oracle.lut_tables(cfg)
+
+
 def oracle_all(x, vp, vn, grad, cfg, out_min=-4.0, out_max=4.0):
     dmin, dmax, n = oracle.lut_range(cfg)
-    ti, td = oracle.lut_tables(cfg)
+    ti, td = oracle_tables(cfg)
     xs, ps, ns, gs = (t.numpy() if isinstance(t, torch.Tensor) else t for t in (x, vp, vn, grad))
     out = oracle.forward(xs, ps, ns, ti, dmin, dmax, cfg["V_sat"], out_min, out_max)
     dx = oracle.grad_x(xs, ps, ns, gs, ti, td, dmin, dmax, cfg["V_sat"])

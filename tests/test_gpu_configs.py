@@ -28,7 +28,7 @@ import pytest
 import torch
 
 from oracle import oracle
-from tests.helpers import errs, flash_cfg
+from tests.helpers import errs, flash_cfg, oracle_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -90,7 +90,7 @@ def _f32(v):
 
 def _tables(cfg):
     dmin, dmax, _ = oracle.lut_range(cfg)
-    ti, td = oracle.lut_tables(cfg)
+    ti, td = oracle_tables(cfg)
     return ti, td, dmin, dmax, float(cfg["V_sat"])
 
 
@@ -163,12 +163,13 @@ def _modes_match(got, want):
     return len(got) == len(want) and all(g in w if isinstance(w, range) else g == w for g, w in zip(got, want))
 
 
-def run_physical_ffn(monkeypatch, dev, D, F, B, T, size, expect_modes, n_rows=48, n_cols=24, seed=0):
+def run_physical_ffn(monkeypatch, dev, D, F, B, T, size, expect_modes, n_rows=48, n_cols=24, seed=0, **cfg_over):
     from isa.device_models.config import make_flash_transistor_ekv_config
     from isa.operators.cim import PhysicalFFN
 
     cfg = make_flash_transistor_ekv_config(default_lut_size=size)
     cfg["LUT_DELTA_SIZE"] = size
+    cfg.update(cfg_over)
     torch.manual_seed(seed)
     ffn = PhysicalFFN(D, F, cfg).to(dev)
     x = _inputs(B, T, D, seed + 1).to(dev)
@@ -176,7 +177,8 @@ def run_physical_ffn(monkeypatch, dev, D, F, B, T, size, expect_modes, n_rows=48
     spy = LayerSpy(monkeypatch)
     out, xx = _step(ffn, x, g)
     fmodes, bmodes = spy.modes()
-    print(f"[case] PhysicalFFN {D}->{F}->{D} x[{B},{T},{D}] LUT {size}: copy modes fwd {fmodes} bwd {bmodes}")
+    print(f"[case] PhysicalFFN {D}->{F}->{D} x[{B},{T},{D}] LUT {size} {cfg.get('LUT_DTYPE', 'float32')}: "
+          f"copy modes fwd {fmodes} bwd {bmodes}")
     assert len(spy.fwd) == 2 and len(spy.bwd) == 2, "the fused layer path must serve both projections"
     assert _modes_match(fmodes, expect_modes[0]) and _modes_match(bmodes, expect_modes[1]), (fmodes, bmodes)
 
@@ -264,6 +266,15 @@ def test_config1_vitm_physical_ffn_8192(cuda_device, monkeypatch):
 def test_config3_headline_physical_ffn(cuda_device, monkeypatch):
     """configs[3], the headline Physical GPT-L FFN at full size, exactly as bench.py runs it."""
     run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([WINDOWED, 16], [2, 2]))
+
+
+def test_config3_headline_physical_ffn_bf16_tables(cuda_device, monkeypatch):
+    """The headline with LUT_DTYPE=bfloat16: the reference's own bf16 tables (delta_lut.py:35),
+    checked against the oracle fed the same bytes. fc2's inputs are the TIA outputs of the
+    initial model, within a fraction of a volt of zero, where the reference's fp32 table
+    construction and an fp64-accurate one differ most after the bf16 cast."""
+    run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([WINDOWED, 16], [2, 2]),
+                     LUT_DTYPE="bfloat16")
 
 
 def test_config2_gptm_hybrid_ffn(cuda_device, monkeypatch):

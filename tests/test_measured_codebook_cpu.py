@@ -48,8 +48,10 @@ def test_install_fused_backend_shares_one_codebook(monkeypatch):
     from isa.measured_deployment import operator
     from isa.measured_deployment.fused_backend import install_fused_backend
 
+    from isa.measured_deployment import fused_backend
+
     monkeypatch.setattr(operator.DeploymentAwareCIMLinear, "_fg50_fused_backend_installed", False, raising=False)
-    monkeypatch.setattr(operator, "_SHARED_CODEBOOKS", {})
+    monkeypatch.setattr(fused_backend, "_SHARED_CODEBOOKS", {})
     vg, cur = make_codebook(24, 61, seed=6)
     a, b = _layer(), _layer()
     a.configure_codebook(vg, cur)
@@ -71,3 +73,38 @@ def test_install_fused_backend_shares_one_codebook(monkeypatch):
     assert not torch.equal(c.pos_idx, d.pos_idx)  # assignments stay per layer
     with pytest.raises(ValueError, match="outside the codebook"):
         d.set_assignment(torch.full((10, 12), 24), torch.zeros(10, 12, dtype=torch.long))
+
+
+def test_shared_codebook_entry_follows_its_sources(monkeypatch):
+    """The shared-codebook cache holds its sources weakly: freeing them frees their entry (the
+    layers keep the device tables they were given), and an in-place edit of a source is a new
+    codebook, not a stale hit."""
+    import gc
+
+    from isa.measured_deployment import fused_backend, operator
+    from isa.measured_deployment.fused_backend import install_fused_backend
+
+    monkeypatch.setattr(operator.DeploymentAwareCIMLinear, "_fg50_fused_backend_installed", False, raising=False)
+    monkeypatch.setattr(fused_backend, "_SHARED_CODEBOOKS", {})
+    monkeypatch.setattr(fused_backend, "_WATCHED_SOURCES", set())
+    install_fused_backend()
+    vg, cur = make_codebook(24, 61, seed=8)
+    a, b = _layer(), _layer()
+    a.configure_codebook(vg, cur)
+    assert len(fused_backend._SHARED_CODEBOOKS) == 1
+    before = a.curve_slopes.clone()
+    cur.mul_(2.0)  # in place: the cached tables no longer describe this tensor
+    b.configure_codebook(vg, cur)
+    assert len(fused_backend._SHARED_CODEBOOKS) == 1
+    assert torch.allclose(b.curve_slopes, 2.0 * before, rtol=1e-6, atol=0)
+    assert torch.equal(a.curve_slopes, before)  # a keeps what it was configured with
+    c = _layer()
+    c.configure_codebook(vg, cur)
+    assert c.curve_slopes.data_ptr() == b.curve_slopes.data_ptr()  # same version: shared
+    book = next(iter(fused_backend._SHARED_CODEBOOKS.values()))
+    assert book["sources"][0]() is vg and book["sources"][1]() is cur
+    del vg, cur, book
+    gc.collect()
+    assert fused_backend._SHARED_CODEBOOKS == {}
+    assert fused_backend._WATCHED_SOURCES == set()
+    assert torch.allclose(b.curve_slopes, 2.0 * before, rtol=1e-6, atol=0)  # the layers' tables live on

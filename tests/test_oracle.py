@@ -62,21 +62,20 @@ def test_table_matches_reference_test_grid():
 
 def test_table_matches_torch_fp32_construction():
     """The reference builds the table with fp32 torch ops (delta_lut.py:25-34); ours rounds
-    the fp64 value once, so the two differ by fp32 evaluation error only."""
+    the fp64 value once. Norm-wise the two agree to fp32 evaluation error; elementwise the
+    reference's derivative table loses its subthreshold end to the fp32 cancellation of
+    1 - exp(-sp) (exactly zero below dV ~ -3.73 V, ~0.7% off at -2.5 V), which ours keeps."""
     cfg = flash_cfg(4096)
     dmin, dmax, n = oracle.lut_range(cfg)
-    delta = torch.linspace(dmin, dmax, n, dtype=torch.float32)
-    k = 1.0 / (2.0 * cfg["n"] * cfg["U_T"])
-    sp1, sp2 = F.softplus(delta * k), F.softplus((delta - cfg["V_D"]) * k)
-    base = cfg["I_S"] * (sp1.square() - sp2.square())
-    sig1 = torch.where(sp1 > 20.0, torch.ones_like(sp1), 1.0 - torch.exp(-sp1))
-    sig2 = torch.where(sp2 > 20.0, torch.ones_like(sp2), 1.0 - torch.exp(-sp2))
-    grad = cfg["I_S"] * 2.0 * k * (sp1 * sig1 - sp2 * sig2)
+    ri, rd, _, _ = oracle.reference_lut_tables(cfg)
     ti, td = oracle.lut_tables(cfg)
-    # fp32 evaluation of sp1^2 - sp2^2 cancels near the top of the range (~5e-6 there);
-    # the fp64-then-round table matches the closed form to 2e-7 (test above)
-    assert oracle.normwise_error(ti, base.numpy()) < 1e-5
-    assert oracle.normwise_error(td, grad.numpy()) < 1e-5
+    assert oracle.normwise_error(ti, ri) < 1e-5
+    assert oracle.normwise_error(td, rd) < 1e-5
+    delta = dmin + np.arange(n) * (dmax - dmin) / (n - 1)
+    assert np.all(rd[delta <= -3.8] == 0.0) and np.all(td[delta <= -3.8] > 0.0)
+    near = (delta > -2.6) & (delta < -2.4)
+    rel = np.abs(td[near].astype(np.float64) - rd[near]) / td[near]
+    assert 1e-3 < rel.max() < 2e-2
 
 
 def test_exact_formula_known_answers():

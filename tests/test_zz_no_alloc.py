@@ -15,17 +15,22 @@ pytestmark = pytest.mark.gpu
 
 
 def _both(x, vp, vn, cfg, dev):
+    """(workspace forward, no-allocation forward, the table-copy mode word of the workspace
+    call) on the same inputs."""
     from isa.approximations.delta_lut import get_packed_tables, lut_range
     from isa.kernels.transformer_ffn import ops
 
     dmin, dmax, n = lut_range(cfg)
     fwd, _ = get_packed_tables(cfg, dev)
     xd, pd, nd = (t.to(dev).contiguous() for t in (x, vp, vn))
-    ref = ops.lut_forward(xd, pd, nd, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0)
+    M, K = x.shape
+    plan = ops.plan_info("forward", M, K, vp.shape[0], n)
+    ws = torch.empty(plan["workspace_bytes"], dtype=torch.uint8, device=dev)
+    ref = ops.lut_forward(xd, pd, nd, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0, workspace=ws)
     out = torch.full_like(ref, float("nan"))
     ops.lut_forward_noalloc(xd, pd, nd, fwd, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0, out)
     torch.cuda.synchronize()
-    return ref, out
+    return ref, out, ops.copy_mode(ws, plan)
 
 
 def test_noalloc_forward_matches_workspace_forward(cuda_device):
@@ -33,20 +38,33 @@ def test_noalloc_forward_matches_workspace_forward(cuda_device):
     for M, K, O in ((300, 203, 500), (37, 64, 130)):  # second call smaller; K % 8 != 0 first
         print(f"[case] noalloc forward M={M} K={K} O={O}", flush=True)
         x, vp, vn, _ = make_inputs(M, K, O, seed=M + K + O)
-        ref, out = _both(x, vp, vn, cfg, cuda_device)
+        ref, out, _ = _both(x, vp, vn, cfg, cuda_device)
         assert torch.equal(out, ref)
         assert torch.count_nonzero(ref) > 0
 
 
 def test_noalloc_forward_table_copies(cuda_device):
-    """8192-entry table, mapped inputs, initial thresholds: the windowed two-copy forward, whose
-    mode word and reassigned threshold records live in the scratch array."""
-    cfg = flash_cfg(8192)
-    for M, K, O in ((256, 400, 600), (64, 203, 300)):
-        print(f"[case] noalloc forward 8192 entries M={M} K={K} O={O}", flush=True)
-        x, vp, vn, _ = make_inputs(M, K, O, seed=7 * M + K)
-        ref, out = _both(x, vp, vn, cfg, cuda_device)
-        assert torch.equal(out, ref)
+    """The windowed-copy forward, whose mode word, copy-assignment passes and reassigned
+    threshold records live in the scratch array. These shapes are far below the library's
+    copy threshold (ISA_EKV_OPT_COPY_MIN_CELLS), so the test lowers it to zero, as large
+    calls run, and checks the mode the workspace call took: windowed copies (about three of
+    the 8192-entry table's ~2800-record window of mapped inputs, sixteen of the 4096-entry
+    table's narrow window of fc2-like inputs)."""
+    from isa.kernels.transformer_ffn import ops
+
+    prev = ops.copy_min_cells(0)
+    try:
+        for size, x_mode in ((8192, "mapped"), (4096, "fc2init")):
+            cfg = flash_cfg(size)
+            for M, K, O in ((256, 400, 600), (64, 203, 300)):
+                print(f"[case] noalloc forward {size} entries {x_mode} M={M} K={K} O={O}", flush=True)
+                x, vp, vn, _ = make_inputs(M, K, O, seed=7 * M + K, x_mode=x_mode)
+                ref, out, mode = _both(x, vp, vn, cfg, cuda_device)
+                print(f"  mode {mode}", flush=True)
+                assert mode is not None and 3 <= mode <= 33, mode
+                assert torch.equal(out, ref)
+    finally:
+        ops.copy_min_cells(prev)
 
 
 def test_noalloc_forward_rejects_oversized_shapes(cuda_device):
