@@ -317,9 +317,15 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *     more than the copy saves). 0 lets every call consider it.
  *   ISA_EKV_OPT_RANKED: 1 (default) lets table backwards that consider the second copy run
  *     the ranked backward instead, when their coordinates need no clamp and reach a window of
- *     at most 3008 table records and their thresholds span at most 420 (decided on the
- *     device; mode word 2): each wave's gathers then read thresholds dealt to lanes in rank
- *     order. 0 never runs it.
+ *     at most 3008 table records and their thresholds span at most ISA_EKV_OPT_RANK_MAX_SPREAD
+ *     records (decided on the device; mode word 2): each wave's gathers then read thresholds
+ *     dealt to lanes within residue classes, by rank, or past ISA_EKV_OPT_RANK_GREEDY_MIN
+ *     records of spread by the greedy bank-aware deal. 0 never runs it.
+ *   ISA_EKV_OPT_RANK_MAX_SPREAD: the widest threshold spread, in table records, the ranked
+ *     backward takes (default 4128: every spread whose coordinate window fits).
+ *   ISA_EKV_OPT_RANK_GREEDY_MIN: threshold spreads (table records) past which the ranked
+ *     backward's branches are dealt by the greedy bank-aware deal instead of by rank
+ *     (default 100).
  *   ISA_EKV_OPT_WINDOW_COPIES: the most bank-rotated copies of the coordinate window (3 to 32;
  *     default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
  *     LDS when its coordinates need no clamp, and a table backward's two-copy launch when the
@@ -332,6 +338,8 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
 #define ISA_EKV_OPT_COPY_MIN_CELLS 1
 #define ISA_EKV_OPT_RANKED 2
 #define ISA_EKV_OPT_WINDOW_COPIES 3
+#define ISA_EKV_OPT_RANK_MAX_SPREAD 4
+#define ISA_EKV_OPT_RANK_GREEDY_MIN 5
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous);
 
 /* Measurement aid, no reference counterpart: launches two 1024-thread blocks per CU, each

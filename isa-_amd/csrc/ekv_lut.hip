@@ -118,6 +118,13 @@ constexpr int kBwdWavesPerEU = ISA_EKV_BWD_MIN_BLOCKS * 16 / 4;
 // halves sit kSplitRecords * 8 bytes after the I halves: within the 16-bit ds offset).
 constexpr int kSplitRecords = 4096 + 2 * kPad;
 
+#ifndef ISA_EKV_RANK_MAX_SPREAD
+#define ISA_EKV_RANK_MAX_SPREAD 4128
+#endif
+#ifndef ISA_EKV_RANK_GREEDY_MIN
+#define ISA_EKV_RANK_GREEDY_MIN 100
+#endif
+
 __host__ __device__ inline int lut_records(int n) { return n + 2 * kPad; }
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int64_t kCUs = 256;  // MI355X compute units (a fixed plan input: workspace sizes must not depend on the device)
@@ -136,6 +143,12 @@ std::atomic<int64_t> g_ranked{1};
 // headline's narrow fc2 window 8, 16 and 32 copies run the forward in the same time within
 // 1%, and the assignment pass costs ~10 us more per doubling: 16.
 std::atomic<int64_t> g_window_copies{16};
+
+// Planning options ISA_EKV_OPT_RANK_MAX_SPREAD / ISA_EKV_OPT_RANK_GREEDY_MIN: the widest threshold
+// spread (table records) the ranked backward takes, and the spread past which its branches are
+// dealt by the greedy bank-aware deal (bwd_deal_kernel) instead of by rank (bwd_rank_kernel).
+std::atomic<int64_t> g_rank_max_spread{ISA_EKV_RANK_MAX_SPREAD};
+std::atomic<int64_t> g_rank_greedy_min{ISA_EKV_RANK_GREEDY_MIN};
 
 bool copies_pay(int64_t M, int64_t K, int64_t O) {
     return (double)M * (double)K * (double)O >= (double)g_copy_min_cells.load(std::memory_order_relaxed);
@@ -1271,7 +1284,8 @@ __device__ inline MultiLayout fwd_multi_layout(const CoordRange& cr, int NP, int
     return multi_layout(cr, NP, budget, max_copies, 0, NP);
 }
 
-__device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP);
+__device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP, float max_spread,
+                                   float* spread);
 
 // Copy choice for the windowed copies. A problem is the 32 thresholds one half-wave gather
 // reads (as in fwd_copy_assign_kernel<32>: input k, sign, output slot j, half of an output
@@ -1371,14 +1385,14 @@ __device__ inline unsigned multi_lo_mask(float w, float fl) {
 
 // Block 0 records the launch's mode in the mode word: the number of copies, or 0 (the two-copy
 // pass that follows then decides between one and two copies).
-// (The backward's two-copy launch takes the same pass with dhalf > 0; after_rank: the ranked
-// backward, when its mode applies, keeps the word its pass wrote.)
+// (The backward's two-copy launch takes the same pass with dhalf > 0; after_rank > 0: the
+// ranked backward's spread limit, and when its mode applies it keeps the word its pass wrote.)
 __global__ __launch_bounds__(kMcThreads) void fwd_multi_assign_kernel(float2* __restrict__ wsT,
                                                           const float2* __restrict__ partials, int NP, int budget,
                                                           int max_copies, int* __restrict__ mode_word, int64_t Kp,
                                                           int64_t Op, int dhalf, int max_window, int wide_dhalf,
-                                                          int after_rank) {
-    if (after_rank && ranked_mode(partials, NP)) return;
+                                                          float after_rank) {
+    if (after_rank > 0.0f && ranked_mode(partials, NP, after_rank, nullptr)) return;
     const MultiLayout ml =
         multi_layout(read_coord_range(partials), NP, budget, max_copies, dhalf, max_window, wide_dhalf);
     if (blockIdx.x == 0 && threadIdx.x == 0) *mode_word = multi_mode_word(ml.copies);
@@ -2126,6 +2140,8 @@ struct RankArgs {
     const float2* partials;
     int* mode_word;
     int Kp, Op, n_ob, NP;
+    float max_spread;     // the widest threshold spread (records) the ranked launch takes
+    float greedy_min;     // spreads past this are dealt by bwd_deal_kernel, the rest by rank
 };
 
 // Thresholds spread over more table records than this leave a half-wave's ranks hundreds of
@@ -2134,17 +2150,16 @@ struct RankArgs {
 #ifndef ISA_EKV_RANK_MERGE_MAX
 #define ISA_EKV_RANK_MERGE_MAX 2  // most token splits the ranked launch merges per block
 #endif
-#ifndef ISA_EKV_RANK_MAX_SPREAD
-#define ISA_EKV_RANK_MAX_SPREAD 420
-#endif
-constexpr float kRankMaxSpread = (float)ISA_EKV_RANK_MAX_SPREAD;
 
 // Whether the ranked launch works (wave-uniform): the clamp-free loop, thresholds spread over at
-// most kRankMaxSpread records, and a coordinate window that fits the launch's table halves.
-__device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP) {
+// most max_spread records, and a coordinate window that fits the launch's table halves. *spread
+// (nullable) receives the thresholds' spread in records.
+__device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP, float max_spread,
+                                   float* spread = nullptr) {
     if (!coords_in_padded_range(partials, NP)) return false;
     const CoordRange c = read_coord_range(partials);
-    if (!(c.whi - c.wlo <= kRankMaxSpread)) return false;
+    if (spread) *spread = c.whi - c.wlo;
+    if (!(c.whi - c.wlo <= max_spread)) return false;
     int lo, n;
     coord_window(c, NP, lo, n);
     return n <= kRankWindow;
@@ -2158,9 +2173,10 @@ __device__ inline bool ranked_mode(const float2* __restrict__ partials, int NP) 
 // as one contiguous run (each thread's own stores would land 32 bytes apart across a wave).
 constexpr int kRankQ = 256 / kRankClasses;
 __global__ __launch_bounds__(256) void bwd_rank_kernel(RankArgs a) {
-    const bool on = ranked_mode(a.partials, a.NP);  // block-uniform: every wave reads the same partials
+    float spread = 0.0f;
+    const bool on = ranked_mode(a.partials, a.NP, a.max_spread, &spread);  // block-uniform
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.mode_word = on ? kModeRanked : 0;
-    if (!on) return;
+    if (!on || spread > a.greedy_min) return;  // (wide spreads: bwd_deal_kernel deals)
     __shared__ float4 s_dealt[kRankQ * 64 * 2];  // per pair: 64 lanes x 8 slots
     const int64_t n_q = (int64_t)a.Kp * a.n_ob;
     const int64_t q0 = (int64_t)blockIdx.x * kRankQ;
@@ -2209,6 +2225,123 @@ __global__ __launch_bounds__(256) void bwd_rank_kernel(RankArgs a) {
     const int n = (int)min<int64_t>(kRankQ, n_q - q0) * 64 * 2;
     float4* out = reinterpret_cast<float4*>(a.ws_ranked + q0 * 64 * 8);
     for (int i = threadIdx.x; i < n; i += 256) out[i] = s_dealt[i];
+}
+
+// ----------------------------------------------------------------------------------
+// Greedy bank-aware deal (spreads past RankArgs::greedy_min records). Dealt by rank, a
+// half-wave's 32 lanes read two adjacent ranks of 16 classes, which spread over a window that
+// grows with the thresholds' spread (~0.09 of it per rank), so past ~100 records they collide
+// in the LDS bank pairs (modelled 1.2 conflict cycles per gather at 135 records, the 8192-entry
+// table's initial spread, and 4.5 at 1576, thresholds over [0, 5] V). Any deal within a class
+// keeps the G reads conflict-free, so this one chooses, for each class in turn and each of its
+// 32 branches in threshold order, the instruction (slot s and half-wave h: 16 per wave, each
+// taking two branches of every class, lanes c + 16 i + 32 h) where it adds the fewest bank
+// conflicts: the record a threshold w reads for a token at coordinate X + f is X + floor(f - w),
+// so at kDealSamples token fractions f each instruction keeps, per bank pair, the number of
+// distinct records (saturating at 3) and the first one's id; a record already there costs 0
+// (a broadcast), a new bank pair 1, a bank pair holding n others 2 n + 1 (the growth of the
+// squared load). Ties go to the lowest instruction. Modelled: 0.55 conflict cycles per gather
+// at 135 records, 2.1 at 1576. One wave per (input, output block); its 64 lanes are the 16
+// instructions x 4 fractions, each lane keeping its instruction's bank state for its fraction
+// in LDS, so the per-branch choice is a quad sum and a ballot.
+// ----------------------------------------------------------------------------------
+constexpr int kDealWaves = 4;     // (input, output block) problems per block, one per wave
+constexpr int kDealSamples = 4;   // token fractions each instruction's bank state is kept at
+static_assert(kRankClasses == 16 && kRankBranches == 32, "16 classes of 32 branches in 16 instructions");
+
+__device__ inline void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(kDealWaves * 64) void bwd_deal_kernel(RankArgs a) {
+    float spread = 0.0f;
+    if (!ranked_mode(a.partials, a.NP, a.max_spread, &spread) || !(spread > a.greedy_min)) return;
+    __shared__ float s_key[kDealWaves][16 * 32];      // [class][branch], then [class][rank]
+    __shared__ float s_sorted[kDealWaves][16 * 32];
+    __shared__ unsigned char s_code[kDealWaves][16 * 32];
+    __shared__ __align__(16) unsigned short s_state[kDealWaves][16 * kDealSamples * 32];  // [instruction][fraction][bank pair]
+    __shared__ __align__(16) float s_out[kDealWaves][64 * 8];      // [lane][slot] dealt thresholds
+    __shared__ __align__(16) unsigned char s_bcode[kDealWaves][64 * 8];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t n_q = (int64_t)a.Kp * a.n_ob;
+    const int64_t q = (int64_t)blockIdx.x * kDealWaves + wave;
+    if (q >= n_q) return;  // wave-uniform: the rest of the kernel syncs within the wave only
+    const int ob = (int)(q % a.n_ob);
+    const int64_t k = q / a.n_ob;
+
+    // the class's 32 thresholds in (coordinate, branch) order: lane = class c x quarter p,
+    // holding branches 8 p .. 8 p + 7 (branch i: output c + 16 (i / 2), sign i % 2)
+    {
+        const int c = lane & 15, p = lane >> 4;
+        const float2* src = a.wsT + k * a.Op + (int64_t)ob * 256 + c;
+        float key[8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float2 w = src[16 * (4 * p + u)];
+            key[2 * u] = w.x;
+            key[2 * u + 1] = w.y;
+        }
+        float* kc = &s_key[wave][c * 32];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) kc[8 * p + u] = key[u];
+        wave_lds_sync();
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = 8 * p + u;
+            int rank = 0;
+            for (int jj = 0; jj < 32; ++jj) {
+                const float kj = kc[jj];
+                rank += (kj < key[u] || (kj == key[u] && jj < i)) ? 1 : 0;
+            }
+            s_sorted[wave][c * 32 + rank] = key[u];
+            s_code[wave][c * 32 + rank] = (unsigned char)((i >> 1) | ((i & 1) << 4));
+        }
+        unsigned* st32 = reinterpret_cast<unsigned*>(s_state[wave]);
+        for (int u = lane; u < 16 * kDealSamples * 32 / 2; u += 64) st32[u] = 0u;
+        wave_lds_sync();
+    }
+
+    const int j = lane >> 2, qs = lane & 3;  // this lane's instruction and token fraction
+    const float frac = ((float)qs + 0.5f) / (float)kDealSamples;
+    unsigned short* st = s_state[wave] + (j * kDealSamples + qs) * 32;
+    for (int c = 0; c < 16; ++c) {
+        int cap = 0;  // branches of class c this lane's instruction holds
+        for (int r = 0; r < 32; ++r) {
+            const float w = s_sorted[wave][c * 32 + r];
+            const int rec = (int)floorf(frac - w);
+            const int b = rec & 31;
+            const unsigned e = st[b];
+            const unsigned n = e >> 14, id = e & 0x3FFFu, rid = (unsigned)rec & 0x3FFFu;
+            int cost = n == 0u ? 1 : (id == rid ? 0 : 2 * (int)n + 1);
+            cost += __builtin_amdgcn_update_dpp(0, cost, 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+            cost += __builtin_amdgcn_update_dpp(0, cost, 0x4e, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+            if (cap >= 2) cost = 1 << 20;
+            // the lowest lane of the cheapest instruction (4 fractions x (2 x 3 + 1) bounds a
+            // cost with room by 28; one instruction always has room)
+            int m = 0;
+            unsigned long long mask;
+            while ((mask = __ballot(cost <= m)) == 0ull) ++m;
+            const int jstar = (int)(__builtin_ctzll(mask) >> 2);
+            if (j == jstar) {
+                st[b] = (unsigned short)(n == 0u ? ((1u << 14) | rid) : (id == rid ? e : ((min(n + 1u, 3u) << 14) | id)));
+                if (qs == 0) {
+                    const int L = c + 16 * cap + 32 * (jstar >> 3), slot = jstar & 7;
+                    s_out[wave][L * 8 + slot] = w;
+                    s_bcode[wave][L * 8 + slot] = s_code[wave][c * 32 + r];
+                }
+                ++cap;
+            }
+        }
+    }
+    wave_lds_sync();
+    float4* out = reinterpret_cast<float4*>(a.ws_ranked + q * 64 * 8);
+    const float4* so = reinterpret_cast<const float4*>(s_out[wave]);
+    out[lane] = so[lane];
+    out[lane + 64] = so[lane + 64];
+    const uint2 bc = *reinterpret_cast<const uint2*>(&s_bcode[wave][lane * 8]);
+    a.branch[q * 64 + lane] = bc;
 }
 
 // Block = kRankWaves waves: inputs kg*W .. kg*W+W-1 (one per wave), one output block, one token split.
@@ -4139,7 +4272,7 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
             hipLaunchKernelGGL(fwd_multi_assign_kernel, dim3((unsigned)((problems + kMcProblems - 1) / kMcProblems)),
                                dim3(kMcThreads), 0, s,
                                reinterpret_cast<float2*>(ws + p.off_wsT), fa.partials, fa.NP, tc.mc_budget,
-                               tc.mc_max, mode, p.Kp, p.Op, 0, fa.NP, 0, 0);
+                               tc.mc_max, mode, p.Kp, p.Op, 0, fa.NP, 0, 0.0f);
             err = hipGetLastError();
             if (err != hipSuccess) return hip_fail(err, "forward windowed-copy assignment launch");
         }
@@ -4300,15 +4433,21 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
     }
     const dim3 grid(p.blocks), block(p.waves_per_block * 64);
     const bool copies = bwd_may_use_copies(p, cs.exact, need_x);
+    const float rank_max_spread = (float)g_rank_max_spread.load(std::memory_order_relaxed);
     if (copies) {
         int* mode = reinterpret_cast<int*>(ws + p.off_mode);
         if (p.ranked) {  // the branch deal first: it records the ranked mode when that launch works
             const RankArgs ra{reinterpret_cast<const float2*>(ws + p.off_wsT),
                               reinterpret_cast<float*>(ws + p.off_rank_ws),
                               reinterpret_cast<uint2*>(ws + p.off_rank_branch), ba.partials, mode,
-                              (int)p.Kp, (int)p.Op, p.n_ob, ba.NP};
+                              (int)p.Kp, (int)p.Op, p.n_ob, ba.NP, rank_max_spread,
+                              (float)g_rank_greedy_min.load(std::memory_order_relaxed)};
             const int64_t threads = p.Kp * p.n_ob * kRankClasses;
             hipLaunchKernelGGL(bwd_rank_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, ra);
+            // the greedy deal of wide spreads (exits at once when the rank deal applies)
+            const int64_t problems_q = p.Kp * p.n_ob;
+            hipLaunchKernelGGL(bwd_deal_kernel, dim3((unsigned)((problems_q + kDealWaves - 1) / kDealWaves)),
+                               dim3(kDealWaves * 64), 0, s, ra);
         }
         // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
         const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * (p.split ? 4 : 8);
@@ -4319,7 +4458,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
             hipLaunchKernelGGL(fwd_multi_assign_kernel, dim3((unsigned)((problems + kMcProblems - 1) / kMcProblems)),
                                dim3(kMcThreads), 0, s, reinterpret_cast<float2*>(ws + p.off_wsT), ba.partials,
                                ba.NP, kBwdWinBudget, p.mc_max, mode, p.Kp, p.Op, kBwdWinDOffset, kBwdWinWindow,
-                               kBwdWinWideDOffset, p.ranked ? 1 : 0);
+                               kBwdWinWideDOffset, p.ranked ? rank_max_spread : 0.0f);
         }
         // (a pass before it recorded the ranked mode or the windowed copies: skip_from)
         const int skip_from = p.ranked ? kModeRanked : p.mc_max > 0 ? kModeMultiMin : 0;
@@ -5021,10 +5160,12 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
 }
 
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous) {
-    std::atomic<int64_t>* opt = option == ISA_EKV_OPT_COPY_MIN_CELLS ? &g_copy_min_cells
-                                : option == ISA_EKV_OPT_RANKED      ? &g_ranked
-                                : option == ISA_EKV_OPT_WINDOW_COPIES  ? &g_window_copies
-                                                                    : nullptr;
+    std::atomic<int64_t>* opt = option == ISA_EKV_OPT_COPY_MIN_CELLS      ? &g_copy_min_cells
+                                : option == ISA_EKV_OPT_RANKED          ? &g_ranked
+                                : option == ISA_EKV_OPT_WINDOW_COPIES   ? &g_window_copies
+                                : option == ISA_EKV_OPT_RANK_MAX_SPREAD ? &g_rank_max_spread
+                                : option == ISA_EKV_OPT_RANK_GREEDY_MIN ? &g_rank_greedy_min
+                                                                        : nullptr;
     if (!opt) return fail(ISA_EKV_EINVAL, "unknown option %d", option);
     const int64_t old = value >= 0 ? opt->exchange(value) : opt->load();
     if (previous) *previous = old;

@@ -30,6 +30,8 @@ NOALLOC_MAX_BYTES = 64 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
 OPT_COPY_MIN_CELLS = 1
 OPT_RANKED = 2
 OPT_WINDOW_COPIES = 3
+OPT_RANK_MAX_SPREAD = 4
+OPT_RANK_GREEDY_MIN = 5
 
 EXPORTS = (
     "isa_ekv_abi_version",

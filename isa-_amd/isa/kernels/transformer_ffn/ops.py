@@ -106,6 +106,28 @@ def window_copies(value: Optional[int] = None) -> int:
     return int(prev.value)
 
 
+def _int_option(option: int, value: Optional[int]) -> int:
+    lib = _hip.load()
+    prev = ctypes.c_int64()
+    rc = lib.isa_ekv_set_option(option, -1 if value is None else int(value), ctypes.byref(prev))
+    _hip.check(rc, "isa_ekv_set_option")
+    return int(prev.value)
+
+
+def rank_max_spread(value: Optional[int] = None) -> int:
+    """The library's ISA_EKV_OPT_RANK_MAX_SPREAD (the widest threshold spread, in table records,
+    the ranked backward takes; default 4128); sets it when value is given. Returns the value
+    before the call."""
+    return _int_option(_hip.OPT_RANK_MAX_SPREAD, value)
+
+
+def rank_greedy_min(value: Optional[int] = None) -> int:
+    """The library's ISA_EKV_OPT_RANK_GREEDY_MIN (threshold spreads, in table records, past which
+    the ranked backward's branches are dealt by the greedy bank-aware deal instead of by rank;
+    default 100); sets it when value is given. Returns the value before the call."""
+    return _int_option(_hip.OPT_RANK_GREEDY_MIN, value)
+
+
 def copy_mode(workspace: torch.Tensor, plan: dict) -> Optional[int]:
     """After a call that used `workspace` (and synchronised), which table mode its main kernel
     ran in: 1 the second table copy, 0 one copy, 2 the ranked backward, 3 to 32 the forward's

@@ -46,5 +46,12 @@ def test_bench_json_line(cuda_device, capsys, monkeypatch):
     assert 0 < lds["conflict_free_ns_per_gather_per_cu"] <= 1.05 * lds["ns_per_gather_per_cu"]
     assert lds["conflict_free_frac"]["forward"] > 0 and lds["conflict_free_frac"]["backward"] > 0
     assert rec["ms_per_step_median"] > 0
-    clock = roof["sustained_clock"]
-    assert 0.5 < clock["ghz"] < 3.5, clock  # the shader clock, in GHz
+    assert 0.5 < lds["probe_ghz"] < 3.5, lds  # the shader clock, in GHz
+    mc = roof["measured_ceiling"]
+    for side in ("backward", "forward"):
+        r = mc[side]
+        assert 0.5 < r["kernel_ghz"] < 3.5, r  # the clock the kernel's own blocks ran at
+        assert r["issued_valu_per_cell"] > 0 and r["replay_instr_per_cu_cycle"] > 0.25, r
+        assert 0 < r["frac"] <= 1.05, r  # a ceiling: the kernel cannot issue faster than its replay
+    assert mc["backward"]["kernel"] == "bwd_kernel"  # config 1 is below the copy threshold: one copy
+    assert mc["fma_issue_instr_per_cu_cycle"] > 0.25

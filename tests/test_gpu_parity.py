@@ -376,29 +376,80 @@ def test_windowed_copies_wide_spread(cuda_device, M, K, O, x_mode):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("spread_records", [380, 460])
-def test_ranked_spread_limit(cuda_device, spread_records):
-    """The ranked backward runs while the thresholds span at most 420 table records (decided
-    on the device from the range partials) and the two-copy launch's windowed copies past
-    that: thresholds uniform over 380 and 460 records (4096 entries: 315 records per volt)
-    from 1 V, mapped inputs. Both sides of the limit match the oracle."""
-    cfg = flash_cfg(4096)
-    M, K, O = 64, 96, 300
-    x, _, _, g = make_inputs(M, K, O, seed=spread_records)
-    gen = torch.Generator().manual_seed(spread_records + 1)
+def _spread_inputs(M, K, O, spread_records, seed):
+    """Mapped inputs and thresholds uniform over spread_records table records (4096 entries:
+    315 records per volt) from 1 V."""
+    x, _, _, g = make_inputs(M, K, O, seed=seed)
+    gen = torch.Generator().manual_seed(seed + 1)
     span = spread_records * 13.0 / 4095.0  # volts
     vp = 1.0 + torch.rand(O, K, generator=gen) * span
     vn = 1.0 + torch.rand(O, K, generator=gen) * span
+    return x, vp, vn, g
+
+
+@pytest.mark.parametrize("spread_records,max_spread", [(80, None), (380, None), (460, None), (460, 420),
+                                                       (1500, None)])
+def test_ranked_spread_limit(cuda_device, spread_records, max_spread):
+    """The ranked backward runs while the thresholds span at most ISA_EKV_OPT_RANK_MAX_SPREAD
+    table records (default: any spread whose coordinate window fits), dealt by rank up to
+    ISA_EKV_OPT_RANK_GREEDY_MIN (100) records and by the greedy bank-aware deal past it, and the
+    two-copy launch's windowed copies run past the limit (here lowered to 420). Every case
+    matches the oracle."""
+    from isa.kernels.transformer_ffn import ops
+
+    cfg = flash_cfg(4096)
+    M, K, O = 64, 96, 300
+    x, vp, vn, g = _spread_inputs(M, K, O, spread_records, spread_records)
     ref = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
     modes = {}
-    got = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
+    prev = ops.rank_max_spread(max_spread)
+    try:
+        got = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
+    finally:
+        ops.rank_max_spread(prev)
     e = [errs(got[i], ref[i])[0] for i in range(4)]
-    print(spread_records, modes, [f"{v:.2e}" for v in e])
-    if spread_records <= 420:
+    print(spread_records, max_spread, modes, [f"{v:.2e}" for v in e])
+    if max_spread is None or spread_records <= max_spread:
         assert modes["bwd"] == 2, modes
     else:
         assert 3 <= modes["bwd"] <= 16, modes
     assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL, e
+
+
+@pytest.mark.parametrize("spread_records,M,K,O", [(135, 70, 129, 300), (460, 40, 203, 520), (1500, 96, 40, 768),
+                                                  (1700, 333, 64, 256), (300, 1, 700, 5)])
+def test_greedy_deal_matches_one_copy(cuda_device, spread_records, M, K, O):
+    """The greedy bank-aware deal (spreads past ISA_EKV_OPT_RANK_GREEDY_MIN records) places every
+    branch of an (input, output block) exactly once: the ranked backward's dVth+- are bitwise
+    those of the one-copy kernel on the same plan (a dropped, repeated or mis-signed branch
+    would show), its dX agrees to rounding, and both match the oracle. With the greedy
+    threshold raised past the spread, the rank deal gives the same dVth."""
+    from isa.kernels.transformer_ffn import ops
+
+    print(f"[case] greedy deal spread {spread_records} M={M} K={K} O={O}", flush=True)
+    cfg = flash_cfg(4096)
+    x, vp, vn, g = _spread_inputs(M, K, O, spread_records, 7 * spread_records + M)
+    res = {}
+    for mode in ("greedy", "rank", "one"):
+        prev = ops.ranked_backward(mode != "one")
+        prev_w = ops.window_copies(0 if mode == "one" else 16)
+        prev_g = ops.rank_greedy_min(100 if mode == "greedy" else 100000)
+        try:
+            modes = {}
+            res[mode] = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
+        finally:
+            ops.ranked_backward(prev)
+            ops.window_copies(prev_w)
+            ops.rank_greedy_min(prev_g)
+        assert modes["bwd"] == (0 if mode == "one" else 2), (mode, modes)
+    (_, dx_g, gp_g, gn_g), (_, dx_r, gp_r, gn_r), (_, dx_1, gp_1, gn_1) = res["greedy"], res["rank"], res["one"]
+    assert torch.equal(gp_g, gp_1) and torch.equal(gn_g, gn_1)
+    assert torch.equal(gp_r, gp_1) and torch.equal(gn_r, gn_1)
+    e = errs(dx_g, dx_1.cpu().numpy())[0]
+    print(f"dX greedy vs one copy {e:.2e}")
+    assert e <= 1e-6
+    _, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
+    assert max(errs(dx_g, ref_dx)[0], errs(gp_g, ref_gp)[0], errs(gn_g, ref_gn)[0]) <= BWD_TOL
 
 
 def test_nan_semantics(cuda_device):
