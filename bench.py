@@ -515,6 +515,15 @@ def main() -> int:
                     help="the most windowed table copies a LUT forward or the two-copy backward may hold "
                          "(isa_ekv_set_option "
                          "ISA_EKV_OPT_WINDOW_COPIES: 3 to 32, default 16; 0 none)")
+    ap.add_argument("--rank-max-spread", type=int, default=None,
+                    help="the widest threshold spread (table records) the ranked backward takes "
+                         "(isa_ekv_set_option ISA_EKV_OPT_RANK_MAX_SPREAD, default 420)")
+    ap.add_argument("--rank-greedy-min", type=int, default=None,
+                    help="threshold spreads (table records) past which the ranked backward deals its branches "
+                         "greedily by LDS bank instead of by rank (ISA_EKV_OPT_RANK_GREEDY_MIN, default 4128: never)")
+    ap.add_argument("--rank-xcd-order", type=int, default=None, choices=[0, 1],
+                    help="1: each XCD runs a contiguous range of the ranked backward's blocks "
+                         "(ISA_EKV_OPT_RANK_XCD_ORDER); 0: the hardware's round-robin order")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -546,6 +555,18 @@ def main() -> int:
         from isa.kernels.transformer_ffn import ops
 
         ops.copy_min_cells(args.copy_min_cells)
+    if args.rank_max_spread is not None:
+        from isa.kernels.transformer_ffn import ops
+
+        ops.rank_max_spread(args.rank_max_spread)
+    if args.rank_greedy_min is not None:
+        from isa.kernels.transformer_ffn import ops
+
+        ops.rank_greedy_min(args.rank_greedy_min)
+    if args.rank_xcd_order is not None:
+        from isa.kernels.transformer_ffn import ops
+
+        ops.rank_xcd_order(bool(args.rank_xcd_order))
     if args.config == "gptl_train":
         return gpt_train_step(args)
     if args.config == "measured_fc1":

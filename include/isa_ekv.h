@@ -322,10 +322,14 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *     dealt to lanes within residue classes, by rank, or past ISA_EKV_OPT_RANK_GREEDY_MIN
  *     records of spread by the greedy bank-aware deal. 0 never runs it.
  *   ISA_EKV_OPT_RANK_MAX_SPREAD: the widest threshold spread, in table records, the ranked
- *     backward takes (default 4128: every spread whose coordinate window fits).
+ *     backward takes (default 420; 4128 takes every spread whose coordinate window fits).
  *   ISA_EKV_OPT_RANK_GREEDY_MIN: threshold spreads (table records) past which the ranked
- *     backward's branches are dealt by the greedy bank-aware deal instead of by rank
- *     (default 100).
+ *     backward's branches are dealt by the greedy bank-aware deal instead of by rank (default
+ *     4128: never; the deal halves the gathers' bank conflicts past ~100 records but costs as
+ *     much time as the ranked kernel then saves at the GPT-L shapes).
+ *   ISA_EKV_OPT_RANK_XCD_ORDER: 1 runs each XCD on a contiguous range of the ranked
+ *     backward's blocks (consecutive inputs of one output block and token split, which share
+ *     their G rows in that XCD's L2); 0 (default) keeps the hardware's round-robin order.
  *   ISA_EKV_OPT_WINDOW_COPIES: the most bank-rotated copies of the coordinate window (3 to 32;
  *     default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
  *     LDS when its coordinates need no clamp, and a table backward's two-copy launch when the
@@ -340,6 +344,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
 #define ISA_EKV_OPT_WINDOW_COPIES 3
 #define ISA_EKV_OPT_RANK_MAX_SPREAD 4
 #define ISA_EKV_OPT_RANK_GREEDY_MIN 5
+#define ISA_EKV_OPT_RANK_XCD_ORDER 6
 int isa_ekv_set_option(int option, int64_t value, int64_t* previous);
 
 /* Measurement aid, no reference counterpart: launches two 1024-thread blocks per CU, each
@@ -363,10 +368,12 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
  * LUT forward's cell (320 VALU per iteration), 8-wave blocks. tokens: device, 64 float4 token
  * records {coordinate, r, -r/V_sat, 0} read with scalar loads, as the kernels read theirs
  * (coordinates within [4, 4000]). out: device scratch of >= 2 x CU count x (64 x waves per
- * block) floats. clocks (nullable, device, 2 x blocks int64): per block, the clock64 cycles and
- * wall_clock64 ticks of its first wave; *wall_clock_khz (nullable) the wall clock's rate.
- * *instr_per_cu (nullable) receives the VALU wave-instructions each CU issues in the loops, so
- * instr_per_cu / cycles is the issue rate per CU-cycle. Asynchronous on `stream`. */
+ * block) floats. clocks (nullable, device, 4 x blocks int64): per block, the clock64 cycles and
+ * the wall_clock64 ticks of its first wave, its start tick and its CU (XCC x 256 + HW_ID bits
+ * 8-14); *wall_clock_khz (nullable) the wall clock's rate. Each block requests half the CU's
+ * LDS, so a CU holds two. *instr_per_cu (nullable) receives the VALU wave-instructions each
+ * CU's two blocks issue in the loops: over the interval a CU's blocks kept it busy, in shader
+ * cycles, that is the CU's issue rate. Asynchronous on `stream`. */
 int isa_ekv_probe_valu_issue(int mix, int iterations, const float* tokens, float* out, int64_t out_floats,
                              int64_t* clocks, double* instr_per_cu, int* wall_clock_khz, void* stream);
 

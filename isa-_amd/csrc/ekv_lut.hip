@@ -118,11 +118,17 @@ constexpr int kBwdWavesPerEU = ISA_EKV_BWD_MIN_BLOCKS * 16 / 4;
 // halves sit kSplitRecords * 8 bytes after the I halves: within the 16-bit ds offset).
 constexpr int kSplitRecords = 4096 + 2 * kPad;
 
+// Thresholds spread over more table records than ISA_EKV_RANK_MAX_SPREAD leave a half-wave's
+// ranks hundreds of records apart; there the two-copy launch's windowed copies do better
+// (GPT-L fc1 backward, 16-class rank deal: 11.93 ms ranked against 12.12 ms with two copies at
+// 400 records, 12.27 against 12.18 at 450). The greedy deal (ISA_EKV_RANK_GREEDY_MIN) halves
+// the conflicts past ~100 records but costs ~0.5 ms per GPT-L call, as much as it saves: off
+// (4128 records, past any spread) unless set.
 #ifndef ISA_EKV_RANK_MAX_SPREAD
-#define ISA_EKV_RANK_MAX_SPREAD 4128
+#define ISA_EKV_RANK_MAX_SPREAD 420
 #endif
 #ifndef ISA_EKV_RANK_GREEDY_MIN
-#define ISA_EKV_RANK_GREEDY_MIN 100
+#define ISA_EKV_RANK_GREEDY_MIN 4128
 #endif
 
 __host__ __device__ inline int lut_records(int n) { return n + 2 * kPad; }
@@ -149,6 +155,11 @@ std::atomic<int64_t> g_window_copies{16};
 // dealt by the greedy bank-aware deal (bwd_deal_kernel) instead of by rank (bwd_rank_kernel).
 std::atomic<int64_t> g_rank_max_spread{ISA_EKV_RANK_MAX_SPREAD};
 std::atomic<int64_t> g_rank_greedy_min{ISA_EKV_RANK_GREEDY_MIN};
+
+// Planning option ISA_EKV_OPT_RANK_XCD_ORDER: 1 gives each XCD a contiguous range of the ranked
+// launch's blocks (consecutive inputs of one output block and token split), 0 keeps the
+// hardware's round-robin order.
+std::atomic<int64_t> g_rank_xcd_order{0};
 
 bool copies_pay(int64_t M, int64_t K, int64_t O) {
     return (double)M * (double)K * (double)O >= (double)g_copy_min_cells.load(std::memory_order_relaxed);
@@ -1598,6 +1609,7 @@ struct BwdArgs {
     float k2, c2;           // exact: 2^(-V_D a), V_D a
     int mc_budget, mc_max;  // split tables: the two-copy launch may hold up to mc_max windowed copies
     unsigned long long* clock_acc;  // profiling: {cycles, wall ticks, blocks} of this kernel (BlockClock), or null
+    int xcd_order;          // ranked launch: 1 runs each token split's blocks on one XCD (xcd_work_index)
 };
 
 // LDS table views for the backward. Interleaved: one 16-byte record {A_I, dI, A_D, dD} per
@@ -1975,8 +1987,9 @@ __device__ inline void bwd_windowed_copies(const BwdArgs& a) {
         bwd_windowed_items<NEED_X, NEED_W, BwdTableWinWide>(a, ml, kBwdWinWideDOffset);
 }
 
+// Returns whether this launch is the working one of its set (false: it exited on the mode word).
 template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED, int MODE>
-__device__ inline void bwd_table_body(const BwdArgs& a) {
+__device__ inline bool bwd_table_body(const BwdArgs& a) {
     static_assert(kSplitRecords % 16 == 0 && kBwdCopyOffsetI % 16 == 8, "copy 1 eight bank quads away");
     extern __shared__ float4 s_lut_bwd[];
     float2* s_split = reinterpret_cast<float2*>(s_lut_bwd);
@@ -1989,9 +2002,9 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
         if constexpr (SPLIT && LANE_RED)
             if (mode >= kModeMultiMin) {
                 bwd_windowed_copies<NEED_X, NEED_W>(a);
-                return;
+                return true;
             }
-        if (mode != 1) return;
+        if (mode != 1) return false;
         // tables past kSplitRecords hold the window the launch's coordinates reach (the mode
         // word is set only when it fits)
         if (a.NP > kSplitRecords) {
@@ -2000,7 +2013,7 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
         }
     }
     if constexpr (MODE == kBwdOneCopy)
-        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return;
+        if (__builtin_amdgcn_readfirstlane(*a.copy_mode) != 0) return false;
     stage_to_lds<8>(a.lut + lo, n_rec, [&](int i, float4 rec) {
         if constexpr (SPLIT) {
             s_split[i] = make_float2(rec.x, rec.y);
@@ -2033,6 +2046,7 @@ __device__ inline void bwd_table_body(const BwdArgs& a) {
     else
         t = BwdTableInterleaved{s_lut_bwd - lo};
     bwd_table_items<NEED_X, NEED_W, LANE_RED, MODE, Table, false>(a, t, fast, red);
+    return true;
 }
 
 // The work items of a table-backward launch (the two-copy launch: persistent, one block per CU,
@@ -2067,15 +2081,13 @@ template <bool NEED_X, bool NEED_W, bool SPLIT, bool LANE_RED = false, int MODE 
 __global__ __launch_bounds__(1024, kBwdWavesPerEU) void bwd_kernel(BwdArgs a) {
     static_assert(MODE != kBwdTwoCopies, "bwd_two_copies_kernel");
     const BlockClock clk(a.clock_acc);
-    bwd_table_body<NEED_X, NEED_W, SPLIT, LANE_RED, MODE>(a);
-    clk.stop();  // (blocks of a launch that is not the working one exit in ~5 us and add little)
+    if (bwd_table_body<NEED_X, NEED_W, SPLIT, LANE_RED, MODE>(a)) clk.stop();  // (idle launches add nothing)
 }
 
 template <bool NEED_X, bool NEED_W, bool SPLIT>
 __global__ __launch_bounds__(1024) void bwd_two_copies_kernel(BwdArgs a) {
     const BlockClock clk(a.clock_acc ? a.clock_acc + 3 : nullptr);  // the two-copy kind
-    bwd_table_body<NEED_X, NEED_W, SPLIT, true, kBwdTwoCopies>(a);
-    clk.stop();
+    if (bwd_table_body<NEED_X, NEED_W, SPLIT, true, kBwdTwoCopies>(a)) clk.stop();
 }
 
 // ----------------------------------------------------------------------------------
@@ -2144,9 +2156,6 @@ struct RankArgs {
     float greedy_min;     // spreads past this are dealt by bwd_deal_kernel, the rest by rank
 };
 
-// Thresholds spread over more table records than this leave a half-wave's ranks hundreds of
-// records apart; there the second table copy does better (GPT-L fc1 backward, 16-class deal:
-// 11.93 ms ranked against 12.12 ms with two copies at 400 records, 12.27 against 12.18 at 450).
 #ifndef ISA_EKV_RANK_MERGE_MAX
 #define ISA_EKV_RANK_MERGE_MAX 2  // most token splits the ranked launch merges per block
 #endif
@@ -2241,9 +2250,8 @@ __global__ __launch_bounds__(256) void bwd_rank_kernel(RankArgs a) {
 // distinct records (saturating at 3) and the first one's id; a record already there costs 0
 // (a broadcast), a new bank pair 1, a bank pair holding n others 2 n + 1 (the growth of the
 // squared load). Ties go to the lowest instruction. Modelled: 0.55 conflict cycles per gather
-// at 135 records, 2.1 at 1576. One wave per (input, output block); its 64 lanes are the 16
-// instructions x 4 fractions, each lane keeping its instruction's bank state for its fraction
-// in LDS, so the per-branch choice is a quad sum and a ballot.
+// at 135 records, 2.1 at 1576. The 512 choices of a problem are sequential, and the kernel
+// costs ~0.5 ms per GPT-L call (9216 problems): it pays where the ranked kernel saves more.
 // ----------------------------------------------------------------------------------
 constexpr int kDealWaves = 4;     // (input, output block) problems per block, one per wave
 constexpr int kDealSamples = 4;   // token fractions each instruction's bank state is kept at
@@ -2255,15 +2263,18 @@ __device__ inline void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__global__ __launch_bounds__(kDealWaves * 64) void bwd_deal_kernel(RankArgs a) {
+// One wave per (input, output block): while ranking, lane = class c x quarter p of its branches;
+// then lane = instruction j (lane / 4) x token fraction (lane % 4), keeping the instruction's
+// bank state at that fraction in LDS (per bank pair 16 bits: the distinct records there, 2
+// bits saturating at 3, and the first one's id). 9 KB per wave: four blocks of four waves per CU.
+__global__ __launch_bounds__(kDealWaves * 64, 4) void bwd_deal_kernel(RankArgs a) {
     float spread = 0.0f;
     if (!ranked_mode(a.partials, a.NP, a.max_spread, &spread) || !(spread > a.greedy_min)) return;
-    __shared__ float s_key[kDealWaves][16 * 32];      // [class][branch], then [class][rank]
-    __shared__ float s_sorted[kDealWaves][16 * 32];
+    __shared__ __align__(16) float s_key[kDealWaves][16 * 32];  // [class][branch]; then the dealt [lane][slot]
+    __shared__ __align__(16) float s_sorted[kDealWaves][16 * 32];  // [class][rank]
     __shared__ unsigned char s_code[kDealWaves][16 * 32];
     __shared__ __align__(16) unsigned short s_state[kDealWaves][16 * kDealSamples * 32];  // [instruction][fraction][bank pair]
-    __shared__ __align__(16) float s_out[kDealWaves][64 * 8];      // [lane][slot] dealt thresholds
-    __shared__ __align__(16) unsigned char s_bcode[kDealWaves][64 * 8];
+    __shared__ __align__(16) unsigned char s_bcode[kDealWaves][64 * 8];  // [lane][slot] branch codes
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t n_q = (int64_t)a.Kp * a.n_ob;
     const int64_t q = (int64_t)blockIdx.x * kDealWaves + wave;
@@ -2287,57 +2298,78 @@ __global__ __launch_bounds__(kDealWaves * 64) void bwd_deal_kernel(RankArgs a) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) kc[8 * p + u] = key[u];
         wave_lds_sync();
+        int rank[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rank[u] = 0;
+        for (int jj = 0; jj < 32; ++jj) {
+            const float kj = kc[jj];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) rank[u] += (kj < key[u] || (kj == key[u] && jj < 8 * p + u)) ? 1 : 0;
+        }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int i = 8 * p + u;
-            int rank = 0;
-            for (int jj = 0; jj < 32; ++jj) {
-                const float kj = kc[jj];
-                rank += (kj < key[u] || (kj == key[u] && jj < i)) ? 1 : 0;
-            }
-            s_sorted[wave][c * 32 + rank] = key[u];
-            s_code[wave][c * 32 + rank] = (unsigned char)((i >> 1) | ((i & 1) << 4));
+            s_sorted[wave][c * 32 + rank[u]] = key[u];
+            s_code[wave][c * 32 + rank[u]] = (unsigned char)((i >> 1) | ((i & 1) << 4));
         }
         unsigned* st32 = reinterpret_cast<unsigned*>(s_state[wave]);
         for (int u = lane; u < 16 * kDealSamples * 32 / 2; u += 64) st32[u] = 0u;
         wave_lds_sync();
     }
 
+    // the greedy, one branch per step (class t / 32, rank t % 32). The chain from one step's
+    // choice to the next step's costs is what the time goes to, so each step reads the next
+    // step's threshold and bank entry before it writes its own update, and patches the entry
+    // when both steps touch the same one.
     const int j = lane >> 2, qs = lane & 3;  // this lane's instruction and token fraction
     const float frac = ((float)qs + 0.5f) / (float)kDealSamples;
     unsigned short* st = s_state[wave] + (j * kDealSamples + qs) * 32;
-    for (int c = 0; c < 16; ++c) {
-        int cap = 0;  // branches of class c this lane's instruction holds
-        for (int r = 0; r < 32; ++r) {
-            const float w = s_sorted[wave][c * 32 + r];
-            const int rec = (int)floorf(frac - w);
-            const int b = rec & 31;
-            const unsigned e = st[b];
-            const unsigned n = e >> 14, id = e & 0x3FFFu, rid = (unsigned)rec & 0x3FFFu;
-            int cost = n == 0u ? 1 : (id == rid ? 0 : 2 * (int)n + 1);
-            cost += __builtin_amdgcn_update_dpp(0, cost, 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
-            cost += __builtin_amdgcn_update_dpp(0, cost, 0x4e, 0xf, 0xf, false);  // quad_perm 2,3,0,1
-            if (cap >= 2) cost = 1 << 20;
-            // the lowest lane of the cheapest instruction (4 fractions x (2 x 3 + 1) bounds a
-            // cost with room by 28; one instruction always has room)
-            int m = 0;
-            unsigned long long mask;
-            while ((mask = __ballot(cost <= m)) == 0ull) ++m;
-            const int jstar = (int)(__builtin_ctzll(mask) >> 2);
-            if (j == jstar) {
-                st[b] = (unsigned short)(n == 0u ? ((1u << 14) | rid) : (id == rid ? e : ((min(n + 1u, 3u) << 14) | id)));
-                if (qs == 0) {
-                    const int L = c + 16 * cap + 32 * (jstar >> 3), slot = jstar & 7;
-                    s_out[wave][L * 8 + slot] = w;
-                    s_bcode[wave][L * 8 + slot] = s_code[wave][c * 32 + r];
-                }
-                ++cap;
+    const float* srt = s_sorted[wave];
+    float* s_out = s_key[wave];  // the keys are dead once sorted
+    float w = srt[0];
+    int rec = (int)floorf(frac - w);
+    int b = rec & 31;
+    unsigned e = st[b];
+    int cap = 0;  // branches of the current class this lane's instruction holds
+    for (int t = 0; t < 16 * 32; ++t) {
+        const float wn = srt[min(t + 1, 16 * 32 - 1)];
+        const int recn = (int)floorf(frac - wn);
+        const int bn = recn & 31;
+        unsigned en = st[bn];
+        const unsigned n = e >> 14, id = e & 0x3FFFu, rid = (unsigned)rec & 0x3FFFu;
+        int cost = n == 0u ? 1 : (id == rid ? 0 : 2 * (int)n + 1);
+        cost += __builtin_amdgcn_update_dpp(0, cost, 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+        cost += __builtin_amdgcn_update_dpp(0, cost, 0x4e, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+        // the cheapest instruction with room, ties to the lowest: min of cost x 16 + j over the
+        // wave (4 fractions x (2 x 3 + 1) bound a cost by 28; one instruction always has room):
+        // the quads of a 16-lane row by two row rotations, the rows in scalar code
+        int key = cap < 2 ? (cost << 4) | j : 0xFFFF;
+        key = min(key, __builtin_amdgcn_update_dpp(0xFFFF, key, 0x124, 0xf, 0xf, false));  // row_ror:4
+        key = min(key, __builtin_amdgcn_update_dpp(0xFFFF, key, 0x128, 0xf, 0xf, false));  // row_ror:8
+        const int k01 = min(__builtin_amdgcn_readlane(key, 0), __builtin_amdgcn_readlane(key, 16));
+        const int k23 = min(__builtin_amdgcn_readlane(key, 32), __builtin_amdgcn_readlane(key, 48));
+        const int jstar = min(k01, k23) & 15;
+        if (j == jstar) {
+            const unsigned eu = n == 0u ? ((1u << 14) | rid) : (id == rid ? e : ((min(n + 1u, 3u) << 14) | id));
+            st[b] = (unsigned short)eu;
+            if (bn == b) en = eu;  // the read above saw the entry before this write
+            if (qs == 0) {
+                const int c = t >> 5;
+                const int L = c + 16 * cap + 32 * (jstar >> 3), slot = jstar & 7;
+                s_out[L * 8 + slot] = w;
+                s_bcode[wave][L * 8 + slot] = s_code[wave][t];
             }
+            ++cap;
         }
+        if ((t & 31) == 31) cap = 0;  // the next class
+        w = wn;
+        rec = recn;
+        b = bn;
+        e = en;
     }
     wave_lds_sync();
     float4* out = reinterpret_cast<float4*>(a.ws_ranked + q * 64 * 8);
-    const float4* so = reinterpret_cast<const float4*>(s_out[wave]);
+    const float4* so = reinterpret_cast<const float4*>(s_out);
     out[lane] = so[lane];
     out[lane + 64] = so[lane + 64];
     const uint2 bc = *reinterpret_cast<const uint2*>(&s_bcode[wave][lane * 8]);
@@ -2364,7 +2396,7 @@ __global__ __launch_bounds__(kRankWaves * 64, kRankWaves * 2 / 4) void bwd_ranke
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n_kg = (a.Kp + kRankWaves - 1) / kRankWaves;
-    int b = blockIdx.x;
+    int b = a.xcd_order ? xcd_work_index() : (int)blockIdx.x;
     const int kg = b % n_kg;
     b /= n_kg;
     const int ob = b % a.n_ob;
@@ -3342,6 +3374,10 @@ __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int 
 //      difference and the accumulate), 8 tokens x 4 outputs, 8-wave blocks, two per CU (320).
 // The counts are the instructions the compiler emits for these loops (the replay's own
 // SQ_INSTS_VALU agrees); the addresses are kept live by empty asm statements, not consumed.
+// A CU's waves do not share its issue evenly (older waves go first, so some finish long before
+// others), so the rate is a CU's: each block records the span to its last wave's end, its
+// start and its CU, and the caller divides a CU's instructions by the interval its two blocks
+// kept it busy.
 // ----------------------------------------------------------------------------------
 
 constexpr int kValuProbeTokens = 64;  // token records the replay cycles through (uniform loads)
@@ -3353,6 +3389,8 @@ __device__ inline void keep_live(unsigned v) { asm volatile("" ::"v"(v)); }
 template <int MIX>
 __global__ __launch_bounds__(1024, 8) void valu_probe_kernel(int iters, const float4* __restrict__ tok, float* out,
                                                             long long* clocks) {
+    extern __shared__ float valu_probe_lds[];  // sized at launch to hold two blocks per CU; untouched
+    (void)valu_probe_lds;
     const int lane = threadIdx.x & 63;
     const float lf = (float)lane;
     const long long c0 = clock64(), w0 = wall_clock64();
@@ -3452,10 +3490,17 @@ __global__ __launch_bounds__(1024, 8) void valu_probe_kernel(int iters, const fl
             for (int j = 0; j < 4; ++j) res += acc[mm][j];
     }
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = res;
+    if (clocks) __syncthreads();  // the block's span ends with its last wave (the oldest wave ends first)
     if (clocks && threadIdx.x == 0) {
         const long long c1 = clock64(), w1 = wall_clock64();
-        clocks[2 * blockIdx.x] = c1 - c0;
-        clocks[2 * blockIdx.x + 1] = w1 - w0;
+        // the CU the block ran on: HW_ID's CU, shader array and engine fields (bits 8-14) and
+        // the XCC (XCC_ID bits 0-3), read from the hardware registers
+        const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4);
+        const unsigned xcc = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20);
+        clocks[4 * blockIdx.x] = c1 - c0;
+        clocks[4 * blockIdx.x + 1] = w1 - w0;
+        clocks[4 * blockIdx.x + 2] = w0;
+        clocks[4 * blockIdx.x + 3] = (long long)((xcc << 8) | ((hw >> 8) & 0x7Fu));
     }
 }
 
@@ -4485,6 +4530,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
         if (p.ranked) {
             // the ranked launch sums p.rank_merge consecutive token splits per block
             BwdArgs br = ba;
+            br.xcd_order = g_rank_xcd_order.load(std::memory_order_relaxed) != 0 ? 1 : 0;
             br.n_split = p.n_split / p.rank_merge;
             br.m_chunk = p.m_chunk * p.rank_merge;
             const dim3 rgrid((unsigned)(((p.Kp + kRankWaves - 1) / kRankWaves) * p.n_ob * br.n_split));
@@ -5165,6 +5211,7 @@ int isa_ekv_set_option(int option, int64_t value, int64_t* previous) {
                                 : option == ISA_EKV_OPT_WINDOW_COPIES   ? &g_window_copies
                                 : option == ISA_EKV_OPT_RANK_MAX_SPREAD ? &g_rank_max_spread
                                 : option == ISA_EKV_OPT_RANK_GREEDY_MIN ? &g_rank_greedy_min
+                                : option == ISA_EKV_OPT_RANK_XCD_ORDER  ? &g_rank_xcd_order
                                                                         : nullptr;
     if (!opt) return fail(ISA_EKV_EINVAL, "unknown option %d", option);
     const int64_t old = value >= 0 ? opt->exchange(value) : opt->load();
@@ -5228,12 +5275,15 @@ int isa_ekv_probe_valu_issue(int mix, int iterations, const float* tokens, float
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const float4* tok = reinterpret_cast<const float4*>(tokens);
     long long* clk = reinterpret_cast<long long*>(clocks);
+    // half the CU's LDS per block (unused by the loops): exactly two blocks fit a CU, as the
+    // table kernels run, so the blocks of a CU overlap and each CU holds two
+    const size_t lds = (size_t)kLdsBytes / 2;
     if (mix == 0)
-        hipLaunchKernelGGL(valu_probe_kernel<0>, dim3(blocks), dim3(threads), 0, s, iterations, tok, out, clk);
+        hipLaunchKernelGGL(valu_probe_kernel<0>, dim3(blocks), dim3(threads), lds, s, iterations, tok, out, clk);
     else if (mix == 1)
-        hipLaunchKernelGGL(valu_probe_kernel<1>, dim3(blocks), dim3(threads), 0, s, iterations, tok, out, clk);
+        hipLaunchKernelGGL(valu_probe_kernel<1>, dim3(blocks), dim3(threads), lds, s, iterations, tok, out, clk);
     else
-        hipLaunchKernelGGL(valu_probe_kernel<2>, dim3(blocks), dim3(threads), 0, s, iterations, tok, out, clk);
+        hipLaunchKernelGGL(valu_probe_kernel<2>, dim3(blocks), dim3(threads), lds, s, iterations, tok, out, clk);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "valu probe launch");
     // VALU wave-instructions each CU issues in the loops: two blocks per CU

@@ -32,6 +32,7 @@ OPT_RANKED = 2
 OPT_WINDOW_COPIES = 3
 OPT_RANK_MAX_SPREAD = 4
 OPT_RANK_GREEDY_MIN = 5
+OPT_RANK_XCD_ORDER = 6
 
 EXPORTS = (
     "isa_ekv_abi_version",

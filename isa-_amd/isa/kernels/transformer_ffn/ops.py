@@ -116,7 +116,7 @@ def _int_option(option: int, value: Optional[int]) -> int:
 
 def rank_max_spread(value: Optional[int] = None) -> int:
     """The library's ISA_EKV_OPT_RANK_MAX_SPREAD (the widest threshold spread, in table records,
-    the ranked backward takes; default 4128); sets it when value is given. Returns the value
+    the ranked backward takes; default 420); sets it when value is given. Returns the value
     before the call."""
     return _int_option(_hip.OPT_RANK_MAX_SPREAD, value)
 
@@ -124,8 +124,14 @@ def rank_max_spread(value: Optional[int] = None) -> int:
 def rank_greedy_min(value: Optional[int] = None) -> int:
     """The library's ISA_EKV_OPT_RANK_GREEDY_MIN (threshold spreads, in table records, past which
     the ranked backward's branches are dealt by the greedy bank-aware deal instead of by rank;
-    default 100); sets it when value is given. Returns the value before the call."""
+    default 4128, i.e. never); sets it when value is given. Returns the value before the call."""
     return _int_option(_hip.OPT_RANK_GREEDY_MIN, value)
+
+
+def rank_xcd_order(value: Optional[bool] = None) -> bool:
+    """The library's ISA_EKV_OPT_RANK_XCD_ORDER (whether each XCD runs a contiguous range of the
+    ranked backward's blocks); sets it when value is given. Returns the value before the call."""
+    return bool(_int_option(_hip.OPT_RANK_XCD_ORDER, None if value is None else int(bool(value))))
 
 
 def copy_mode(workspace: torch.Tensor, plan: dict) -> Optional[int]:
@@ -616,17 +622,17 @@ def probe_valu_issue(mix: str, iterations: int = 4096, device: Optional[torch.de
     """VALU wave-instructions a CU issues per shader cycle for one of the table kernels'
     instruction mixes replayed on registers only (isa_ekv_probe_valu_issue): "fma" (32
     independent fma chains), "ranked_backward" or "forward". One untimed launch, then
-    `repeats` launches; returns {"instr_per_cu_cycle": median over blocks and launches of the
-    CU's loop instructions / its blocks' clock64 cycles, "ghz": the shader clock over the same
-    blocks (clock64 / wall_clock64), "ms": mean launch time by HIP events}. A measurement aid:
-    the issue rate a kernel of that mix cannot exceed."""
+    `repeats` launches; returns {"instr_per_cu_cycle": median over CUs and launches of the CU's
+    loop instructions / the shader cycles of the interval its two blocks kept it busy, "ghz":
+    the CUs' shader clock (clock64 / wall_clock64), "ms": mean launch time by HIP events, ...}.
+    A measurement aid: the issue rate a kernel of that mix cannot exceed."""
     lib = _hip.load()
     code = VALU_MIXES[mix]
     dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     waves = 8 if mix == "forward" else 16
     out = torch.empty(2 * cus * 64 * waves, dtype=torch.float32, device=dev)
-    clocks = torch.zeros((repeats, 2 * cus, 2), dtype=torch.int64, device=dev)
+    clocks = torch.zeros((repeats, 2 * cus, 4), dtype=torch.int64, device=dev)
     g = torch.Generator().manual_seed(1)
     tok = torch.stack([torch.rand(64, generator=g) * 3000.0 + 600.0, torch.rand(64, generator=g) * 0.5 + 0.5,
                        -torch.rand(64, generator=g) * 0.1, torch.zeros(64)], dim=1).to(dev).contiguous()
@@ -648,10 +654,30 @@ def probe_valu_issue(mix: str, iterations: int = 4096, device: Optional[torch.de
             launch(r)
         e1.record()
         torch.cuda.synchronize(dev)
-    c = clocks.reshape(-1, 2).double()
-    rate = per_cu.value / c[:, 0]  # both blocks of a CU run the whole time: a block's span is the CU's
-    res = {"instr_per_cu_cycle": float(rate.median()), "ms": e0.elapsed_time(e1) / repeats,
-           "instr_per_cu": per_cu.value, "mix": mix}
-    if khz.value > 0:
-        res["ghz"] = float((c[:, 0] / (c[:, 1] / (khz.value * 1e3)) / 1e9).median())
+    ms = e0.elapsed_time(e1) / repeats
+    res = {"ms": ms, "instr_per_cu": per_cu.value, "mix": mix}
+    if khz.value <= 0:
+        raise RuntimeError("isa_ekv_probe_valu_issue: the device reports no wall clock rate")
+    # per launch and CU: the interval its blocks kept it busy (first start to last end, wall
+    # ticks) in shader cycles at its blocks' clock; the CU's loop instructions over that
+    c = clocks.cpu().double()
+    rates, ghzs = [], []
+    per_block_instr = per_cu.value / 2.0
+    for r in range(repeats):
+        groups = {}
+        for cyc, span, start, cu in c[r].tolist():
+            groups.setdefault(int(cu), []).append((cyc, span, start))
+        for blocks in groups.values():
+            t0 = min(b[2] for b in blocks)
+            t1 = max(b[2] + b[1] for b in blocks)
+            ghz = sum(b[0] for b in blocks) / (sum(b[1] for b in blocks) / (khz.value * 1e3)) / 1e9
+            rates.append(per_block_instr * len(blocks) / ((t1 - t0) / (khz.value * 1e3) * ghz * 1e9))
+            ghzs.append(ghz)
+    rt = torch.tensor(rates, dtype=torch.float64)
+    res["instr_per_cu_cycle"] = float(rt.median())
+    res["instr_per_cu_cycle_max"] = float(rt.max())
+    res["ghz"] = float(torch.tensor(ghzs, dtype=torch.float64).median())
+    res["blocks_per_cu"] = float(c.shape[1] / len(groups))
+    # the same over the whole launch time (HIP events: dispatch ramp and tail included)
+    res["instr_per_cu_cycle_launch"] = per_cu.value / (ms * 1e-3 * res["ghz"] * 1e9)
     return res

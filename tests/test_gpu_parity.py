@@ -387,13 +387,14 @@ def _spread_inputs(M, K, O, spread_records, seed):
     return x, vp, vn, g
 
 
-@pytest.mark.parametrize("spread_records,max_spread", [(80, None), (380, None), (460, None), (460, 420),
-                                                       (1500, None)])
-def test_ranked_spread_limit(cuda_device, spread_records, max_spread):
+@pytest.mark.parametrize("spread_records,max_spread,greedy_min,expect", [
+    (80, None, None, "ranked"), (380, None, None, "ranked"), (460, None, None, "copies"),
+    (460, 4128, 100, "ranked"), (1500, 4128, 100, "ranked"), (1500, 4128, None, "ranked")])
+def test_ranked_spread_limit(cuda_device, spread_records, max_spread, greedy_min, expect):
     """The ranked backward runs while the thresholds span at most ISA_EKV_OPT_RANK_MAX_SPREAD
-    table records (default: any spread whose coordinate window fits), dealt by rank up to
-    ISA_EKV_OPT_RANK_GREEDY_MIN (100) records and by the greedy bank-aware deal past it, and the
-    two-copy launch's windowed copies run past the limit (here lowered to 420). Every case
+    table records (default 420; raised here to take every spread whose window fits), dealt by
+    rank, or past ISA_EKV_OPT_RANK_GREEDY_MIN records (off by default; 100 here) by the greedy
+    bank-aware deal; past the limit the two-copy launch's windowed copies run. Every case
     matches the oracle."""
     from isa.kernels.transformer_ffn import ops
 
@@ -403,13 +404,15 @@ def test_ranked_spread_limit(cuda_device, spread_records, max_spread):
     ref = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
     modes = {}
     prev = ops.rank_max_spread(max_spread)
+    prev_g = ops.rank_greedy_min(greedy_min)
     try:
         got = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
     finally:
         ops.rank_max_spread(prev)
+        ops.rank_greedy_min(prev_g)
     e = [errs(got[i], ref[i])[0] for i in range(4)]
-    print(spread_records, max_spread, modes, [f"{v:.2e}" for v in e])
-    if max_spread is None or spread_records <= max_spread:
+    print(spread_records, max_spread, greedy_min, modes, [f"{v:.2e}" for v in e])
+    if expect == "ranked":
         assert modes["bwd"] == 2, modes
     else:
         assert 3 <= modes["bwd"] <= 16, modes
@@ -420,33 +423,32 @@ def test_ranked_spread_limit(cuda_device, spread_records, max_spread):
                                                   (1700, 333, 64, 256), (300, 1, 700, 5)])
 def test_greedy_deal_matches_one_copy(cuda_device, spread_records, M, K, O):
     """The greedy bank-aware deal (spreads past ISA_EKV_OPT_RANK_GREEDY_MIN records) places every
-    branch of an (input, output block) exactly once: the ranked backward's dVth+- are bitwise
-    those of the one-copy kernel on the same plan (a dropped, repeated or mis-signed branch
-    would show), its dX agrees to rounding, and both match the oracle. With the greedy
-    threshold raised past the spread, the rank deal gives the same dVth."""
+    branch of an (input, output block) exactly once: a branch's dVth sum is the same products
+    in the same token order wherever it is dealt, so the greedy deal's dVth+- are bitwise those
+    of the rank deal on the same plan (with the greedy threshold raised past the spread; the
+    rank deal is checked bitwise against the one-copy kernel in test_ranked_matches_one_copy):
+    a dropped, repeated or mis-signed branch would show. dX, summed over an input's branches in
+    another lane order, agrees to rounding, and both match the oracle."""
     from isa.kernels.transformer_ffn import ops
 
     print(f"[case] greedy deal spread {spread_records} M={M} K={K} O={O}", flush=True)
     cfg = flash_cfg(4096)
     x, vp, vn, g = _spread_inputs(M, K, O, spread_records, 7 * spread_records + M)
     res = {}
-    for mode in ("greedy", "rank", "one"):
-        prev = ops.ranked_backward(mode != "one")
-        prev_w = ops.window_copies(0 if mode == "one" else 16)
+    for mode in ("greedy", "rank"):
         prev_g = ops.rank_greedy_min(100 if mode == "greedy" else 100000)
+        prev = ops.rank_max_spread(4128)
         try:
             modes = {}
             res[mode] = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
         finally:
-            ops.ranked_backward(prev)
-            ops.window_copies(prev_w)
             ops.rank_greedy_min(prev_g)
-        assert modes["bwd"] == (0 if mode == "one" else 2), (mode, modes)
-    (_, dx_g, gp_g, gn_g), (_, dx_r, gp_r, gn_r), (_, dx_1, gp_1, gn_1) = res["greedy"], res["rank"], res["one"]
-    assert torch.equal(gp_g, gp_1) and torch.equal(gn_g, gn_1)
-    assert torch.equal(gp_r, gp_1) and torch.equal(gn_r, gn_1)
-    e = errs(dx_g, dx_1.cpu().numpy())[0]
-    print(f"dX greedy vs one copy {e:.2e}")
+            ops.rank_max_spread(prev)
+        assert modes["bwd"] == 2, (mode, modes)
+    (_, dx_g, gp_g, gn_g), (_, dx_r, gp_r, gn_r) = res["greedy"], res["rank"]
+    assert torch.equal(gp_g, gp_r) and torch.equal(gn_g, gn_r)
+    e = errs(dx_g, dx_r.cpu().numpy())[0]
+    print(f"dX greedy vs rank deal {e:.2e}")
     assert e <= 1e-6
     _, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
     assert max(errs(dx_g, ref_dx)[0], errs(gp_g, ref_gp)[0], errs(gn_g, ref_gn)[0]) <= BWD_TOL
@@ -538,6 +540,9 @@ def test_valu_issue_probe(cuda_device):
         print(f"  {r}", flush=True)
         assert 0.25 < r["instr_per_cu_cycle"] < 4.0, r
         assert 0.5 < r["ghz"] < 3.5, r
+        # every CU held two blocks, and no CU issued faster than its busy interval allows
+        assert r["blocks_per_cu"] == 2.0, r
+        assert r["instr_per_cu_cycle_launch"] <= 1.05 * r["instr_per_cu_cycle"], r
 
 
 def test_kernel_clock_sampling(cuda_device):
