@@ -162,17 +162,28 @@ def cpu_lut_oracle(d_model: int, d_ffn: int, target_s: float) -> dict:
 
 
 def measured_traffic(config: str):
-    """(HBM bytes per backward main-kernel launch, source) from the committed rocprofv3 counter
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel), or (None, None): the
-    counters need a rocprofv3 --pmc run of their own, so this run does not measure them."""
+    """(HBM bytes per backward main-kernel launch, source, per-layer measured and algorithmic
+    bytes) from the committed rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on
+    a plain copy kernel), or (None, None, None): the counters need a rocprofv3 --pmc run of
+    their own, so this run does not measure them."""
     path = ROOT / "profiles" / f"bwd_kernel_{config}_hbm_traffic.txt"
+    total, fields = None, {}
     try:
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch:"):
-                return float(line.split(":", 1)[1]), f"profiles/{path.name} (rocprofv3 --pmc, not this run)"
+                total = float(line.split(":", 1)[1])
+            elif line.startswith(("traffic_fc", "algorithmic_fc")):
+                key, val = line.split(":", 1)
+                fields[key.strip()] = float(val)
     except OSError:
-        pass
-    return None, None
+        return None, None, None
+    layers = {}
+    for layer in ("fc1", "fc2"):
+        t, a = fields.get(f"traffic_{layer}_bytes"), fields.get(f"algorithmic_{layer}_bytes")
+        if t and a:
+            layers[layer] = {"measured_bytes": t, "algorithmic_bytes": a, "ratio": round(t / a, 2)}
+    src = f"profiles/{path.name} (rocprofv3 --pmc, not this run)" if total else None
+    return total, src, layers or None
 
 
 def issued_valu_per_cell() -> dict:
@@ -719,6 +730,7 @@ def main() -> int:
                  "VALU instruction per CU-cycle, so these fractions are not utilisation (measured_ceiling is)",
         "traffic": None if exact else measured_traffic(args.config)[0],
         "traffic_source": None if exact else measured_traffic(args.config)[1],
+        "traffic_per_layer": None if exact else measured_traffic(args.config)[2],
         "kernel": ("bwd_exact_kernel<true,true> (backward main kernel, dominant)" if exact else
                    "table backward main kernel, dominant: bwd_ranked_kernel<true> where the ranked mode applies "
                    "(the initial thresholds), else bwd_kernel / bwd_two_copies_kernel"),
