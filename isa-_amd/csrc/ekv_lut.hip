@@ -1502,10 +1502,15 @@ __device__ inline void stage_table2(float2* dst, const float2* __restrict__ src,
     }
 }
 
-// WIN: the launch may hold copies of only the coordinate window (the windowed copies, or two
-// copies of tables whose two full copies do not fit); the range is then read before the table
-// load. Without WIN the load comes first (reading the range first costs the 4096-entry kernels
-// ~1%).
+// WIN: the range is read before the table load, and the launch holds only the coordinate
+// window its coordinates reach: as windowed copies, two copies of tables whose two full copies
+// do not fit, or one copy. Launches that cannot hold copies (calls below the copy threshold)
+// take the variant without WIN, which loads the whole table first, unless built with
+// ISA_EKV_FWD_SMALL_WIN=1 (configs[0]'s forward: 35.6 against 35.2 us per launch, so reading
+// the range before a third of the table costs as much as the smaller load saves).
+#ifndef ISA_EKV_FWD_SMALL_WIN
+#define ISA_EKV_FWD_SMALL_WIN 0
+#endif
 template <int MR, bool SPLITS, bool WIN = false>
 __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     extern __shared__ float2 s_lut_fwd[];
@@ -1532,7 +1537,14 @@ __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
                 copies = n_rec <= a.copy_window;
                 if (!copies) lo = 0, n_rec = a.NP;
             }
-            if (!copies) stage_table2(s_lut_fwd, a.lut, a.NP);
+            if (!copies) {
+                // one copy: of the coordinate window the launch reaches when no coordinate
+                // needs the clamp (a third of the table for mapped inputs at the initial
+                // thresholds), else of the whole table
+                if (fast) coord_window(cr, a.NP, lo, n_rec);
+                else lo = 0, n_rec = a.NP;
+                stage_table2(s_lut_fwd, a.lut + lo, n_rec);
+            }
         }
     }
     if (copies) {  // record i of copy 1 holds {A - T1 dT, dT}: fma(c + T1, dT, A') = fma(c, dT, A)
@@ -3867,7 +3879,7 @@ void launch_forward_split(bool exact, bool gtab, int mr, int wpb, dim3 grid, siz
             hipLaunchKernelGGL((fwd_exact_kernel<2, SPLITS>), grid, block, 0, s, fa);
         return;
     }
-    if (fa.copy_window > 0 || fa.mc_budget > 0) {
+    if (fa.copy_window > 0 || fa.mc_budget > 0 || ISA_EKV_FWD_SMALL_WIN) {
         if (mr == 8)
             hipLaunchKernelGGL((fwd_kernel<8, SPLITS, true>), grid, block, lds, s, fa);
         else if (mr == 4)
