@@ -365,8 +365,9 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
  * instruction mixes, replayed on registers only (no LDS or memory access in the loop), two
  * blocks per CU. mix 0: 32 independent fma chains (the raw issue rate), 16-wave blocks; mix 1:
  * the ranked backward's branch-token body (288 VALU per iteration), 16-wave blocks; mix 2: the
- * LUT forward's cell (320 VALU per iteration), 8-wave blocks. tokens: device, 64 float4 token
- * records {coordinate, r, -r/V_sat, 0} read with scalar loads, as the kernels read theirs
+ * LUT forward's cell (320 VALU per iteration, record addresses from float bits), 8-wave blocks;
+ * mix 3: mix 2 with integer record addresses (v_cvt_u32_f32, v_lshl_add_u32). tokens: device,
+ * 64 float4 token records {coordinate, r, -r/V_sat, 0} read with scalar loads, as the kernels read theirs
  * (coordinates within [4, 4000]). out: device scratch of >= 2 x CU count x (64 x waves per
  * block) floats. clocks (nullable, device, 4 x blocks int64): per block, the clock64 cycles and
  * the wall_clock64 ticks of its first wave, its start tick and its CU (XCC x 256 + HW_ID bits

@@ -24,7 +24,8 @@
 //    kPad replicated end records on each side reproduce the reference's coordinate clamp
 //    exactly for coordinates within kPad-1 entries of the table range, so a kernel whose
 //    operand ranges fit (checked on device from the prep kernel's range partials) runs a
-//    clamp-free inner loop: sub, cvt_u32, lshl_add, ds_read, fma per branch.
+//    clamp-free inner loop: sub, cvt_u32, lshl_add, ds_read, fma per branch (the forward:
+//    sub, add, and, ds_read, fma, its record address formed from the bits of a float sum).
 //  * A prep kernel writes the token-side operands pre-scaled into LUT-index units
 //    (xs = (x - dmin) * s + kPad, r, and -r/V_sat for the backward) and the threshold
 //    operands transposed to [K][O] as {vth_pos * s, vth_neg * s}, padded so the hot loops
@@ -688,17 +689,46 @@ __device__ inline float coord(float xs, float ws, float cmin, float cmax) {
 //          (ekv_triton.py:33-66).
 // ----------------------------------------------------------------------------------
 
+// LDS record address from the bits of a float sum, for coordinates c with 1/16 <= c - lo <
+// 2^20 and lo <= 2^19: t = fl(c + (2^20 - lo - 1/16)) lies in [2^20, 2^21), where the float
+// grid is 1/8, and rounding c - lo - 1/16 to nearest (ties to even) on that grid keeps the
+// integer part floor(c) - lo (an integer c is a tie that goes to the even neighbour, the
+// integer itself; a c just below the next integer rounds to at most 7/8 past it). Below
+// lo + 1/16 the sum stays under 2^20 and the bits are no address: the kernels' coordinates
+// lie at least one record past lo (their windows keep two records of margin; with lo = 0 the
+// clamp-free condition holds c >= 1 and the clamp c >= kPad). The
+// mantissa bits of t above its three fraction bits are then (floor(c) - lo) * 8: the LDS
+// byte address of the record when the table's record lo sits at LDS address 0, which is
+// where the kernels that use this put their dynamic LDS (they declare no static LDS; the
+// launch code checks that). The add and the mask issue at the VALU's full rate, where the
+// v_cvt_u32_f32 and v_lshl_add_u32 of table[(unsigned)c] each take two issue cycles on
+// gfx950, and an address formed from the table's pointer would cost one more add per gather
+// (the dynamic LDS base is not known when the loads are formed).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+using lds_f32x2 = __attribute__((address_space(3))) const f32x2;
+constexpr unsigned kRecAddrMask = 0x7FFFF8u;
+__device__ inline float rec_addr_bias(int lo) { return (float)((1 << 20) - lo) - 0.0625f; }
+__device__ inline float2 lds_record(float c, float bias) {
+    const f32x2 v = *(lds_f32x2*)(size_t)(__float_as_uint(c + bias) & kRecAddrMask);
+    return make_float2(v.x, v.y);
+}
+
 // Cells take both thresholds of a (token, output, input) cell at once: forward cells return
-// l(+) - l(-); the LUT cells issue both gathers before using either.
-template <bool CLAMP>
+// l(+) - l(-); the LUT cells issue both gathers before using either. FLOAT_ADDR cells read
+// an LDS table at LDS address 0 whose first record is record lo of the padded table, with
+// lds_record and bias = rec_addr_bias(lo) (lut, that table, is then unused); the others read
+// lut[c].
+template <bool CLAMP, bool FLOAT_ADDR = false>
 struct LutFwdCell {
     const float2* lut;
     float cmin, cmax;
+    float bias;
+    __device__ float2 record(float c) const { return FLOAT_ADDR ? lds_record(c, bias) : lut[(unsigned)c]; }
     __device__ float operator()(float xs, float wsp, float wsn) const {
         const float cp = coord<CLAMP>(xs, wsp, cmin, cmax);
         const float cn = coord<CLAMP>(xs, wsn, cmin, cmax);
-        const float2 ep = lut[(unsigned)cp];
-        const float2 en = lut[(unsigned)cn];
+        const float2 ep = record(cp);
+        const float2 en = record(cn);
         return fmaf(cp, ep.y, ep.x) - fmaf(cn, en.y, en.x);
     }
     // token record {coordinate, r}; threshold record {+, -}
@@ -715,8 +745,8 @@ struct LutFwdCell {
         Pending q;
         q.cp = coord<CLAMP>(xs, w.x, cmin, cmax);
         q.cn = coord<CLAMP>(xs, w.y, cmin, cmax);
-        q.ep = lut[(unsigned)q.cp];
-        q.en = lut[(unsigned)q.cn];
+        q.ep = record(q.cp);
+        q.en = record(q.cn);
         return q;
     }
     __device__ float finish(float acc, const Pending& q, float r) const {
@@ -736,8 +766,8 @@ struct LutFwdCell {
 
 template <class Cell>
 struct TwoPhaseCell : std::false_type {};
-template <bool CLAMP>
-struct TwoPhaseCell<LutFwdCell<CLAMP>> : std::true_type {};
+template <bool CLAMP, bool FLOAT_ADDR>
+struct TwoPhaseCell<LutFwdCell<CLAMP, FLOAT_ADDR>> : std::true_type {};
 
 // Backward cells return a pair view whose dp()/dn() (derivative terms) and lp()/ln()
 // (current terms) the loop reads where it uses them; the LUT view holds the two gathered
@@ -1558,11 +1588,13 @@ __global__ __launch_bounds__(2 * kFwdWaves * 64) void fwd_kernel(FwdArgs a) {
     __syncthreads();
     FwdTile t;
     if (fwd_tile<SPLITS>(a, MR, t)) {
-        const float2* tab = WIN ? s_lut_fwd - lo : s_lut_fwd;  // record i of the table at LDS record i - lo
+        // record i of the table at LDS record i - lo (lo > 0 only for clamp-free launches, whose
+        // coordinates, and those of every copy, lie two or more records past lo)
+        const float bias = rec_addr_bias(lo);
         if (fast)
-            fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+            fwd_body<MR, kFwdORR, true>(a, LutFwdCell<false, true>{s_lut_fwd, a.cmin, a.cmax, bias}, a.xrec, a.wsT, t);
         else
-            fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true>{tab, a.cmin, a.cmax}, a.xrec, a.wsT, t);
+            fwd_body<MR, kFwdORR, true>(a, LutFwdCell<true, true>{s_lut_fwd, a.cmin, a.cmax, bias}, a.xrec, a.wsT, t);
     }
     clk.stop();
 }
@@ -3382,8 +3414,11 @@ __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int 
 //   1  the ranked backward's branch-token body (bwd_ranked_kernel's group: per slot and token
 //      coordinate, cvt, address, L_I and L_D, G r, the dVth and the two dX fmas), 8 slots x 4
 //      tokens, token records by scalar loads, 16-wave blocks, two per CU (288);
-//   2  the forward's cell (LutFwdCell: per branch coordinate, cvt, address, interpolation; the
-//      difference and the accumulate), 8 tokens x 4 outputs, 8-wave blocks, two per CU (320).
+//   2  the forward's cell (LutFwdCell on an LDS table: per branch coordinate, the float add and
+//      the mask of its record address, interpolation; the difference and the accumulate),
+//      8 tokens x 4 outputs, 8-wave blocks, two per CU (320);
+//   3  mix 2 with the integer record address (v_cvt_u32_f32 and v_lshl_add_u32, as
+//      table[(unsigned)c] compiles and the other LUT kernels issue), for comparison (320).
 // The counts are the instructions the compiler emits for these loops (the replay's own
 // SQ_INSTS_VALU agrees); the addresses are kept live by empty asm statements, not consumed.
 // A CU's waves do not share its issue evenly (older waves go first, so some finish long before
@@ -3393,8 +3428,8 @@ __global__ __launch_bounds__(1024) void lds_gather_probe_kernel(int window, int 
 // ----------------------------------------------------------------------------------
 
 constexpr int kValuProbeTokens = 64;  // token records the replay cycles through (uniform loads)
-constexpr int kValuMixInstr[3] = {32, 288, 320};
-constexpr int kValuMixWaves[3] = {16, 16, 8};  // waves per block; two blocks per CU
+constexpr int kValuMixInstr[4] = {32, 288, 320, 320};
+constexpr int kValuMixWaves[4] = {16, 16, 8, 8};  // waves per block; two blocks per CU
 
 __device__ inline void keep_live(unsigned v) { asm volatile("" ::"v"(v)); }
 
@@ -3477,6 +3512,7 @@ __global__ __launch_bounds__(1024, 8) void valu_probe_kernel(int iters, const fl
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[mm][j] = 0.0f;
         const float t0 = 0.5f + 1e-3f * lf, t1 = 0.25f + 1e-7f * lf;
+        const float bias = rec_addr_bias((int)(lf * 0.0f));  // 0: a VGPR operand, as the kernel's
         const unsigned base = (unsigned)lane * 4u;
         for (int it = 0; it < iters; ++it) {
             const int m0 = (it * 8) & (kValuProbeTokens - 1);
@@ -3486,8 +3522,13 @@ __global__ __launch_bounds__(1024, 8) void valu_probe_kernel(int iters, const fl
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float cp = xv.x - wp[j], cn = xv.x - wn[j];
-                    keep_live(((unsigned)cp << 3) + base);
-                    keep_live(((unsigned)cn << 3) + base);
+                    if constexpr (MIX == 2) {
+                        keep_live(__float_as_uint(cp + bias) & kRecAddrMask);
+                        keep_live(__float_as_uint(cn + bias) & kRecAddrMask);
+                    } else {
+                        keep_live(((unsigned)cp << 3) + base);
+                        keep_live(((unsigned)cn << 3) + base);
+                    }
                     acc[mm][j] = fmaf(fmaf(cp, t1, t0) - fmaf(cn, t1, t0), xv.y, acc[mm][j]);
                 }
             }
@@ -3894,6 +3935,24 @@ void launch_forward_split(bool exact, bool gtab, int mr, int wpb, dim3 grid, siz
         hipLaunchKernelGGL((fwd_kernel<4, SPLITS>), grid, block, lds, s, fa);
     else
         hipLaunchKernelGGL((fwd_kernel<2, SPLITS>), grid, block, lds, s, fa);
+}
+
+// The LDS-table forward kernels read their table at LDS address 0 (lds_record): their dynamic
+// LDS starts there only while they declare no static LDS. Checked once per process.
+template <class Kernel>
+bool no_static_lds(Kernel kernel) {
+    hipFuncAttributes at{};
+    return hipFuncGetAttributes(&at, reinterpret_cast<const void*>(kernel)) == hipSuccess && at.sharedSizeBytes == 0;
+}
+
+bool fwd_tables_at_lds_zero() {
+    static const bool ok = no_static_lds(fwd_kernel<8, false>) && no_static_lds(fwd_kernel<4, false>) &&
+                           no_static_lds(fwd_kernel<2, false>) && no_static_lds(fwd_kernel<8, true>) &&
+                           no_static_lds(fwd_kernel<4, true>) && no_static_lds(fwd_kernel<2, true>) &&
+                           no_static_lds(fwd_kernel<8, false, true>) && no_static_lds(fwd_kernel<4, false, true>) &&
+                           no_static_lds(fwd_kernel<2, false, true>) && no_static_lds(fwd_kernel<8, true, true>) &&
+                           no_static_lds(fwd_kernel<4, true, true>) && no_static_lds(fwd_kernel<2, true, true>);
+    return ok;
 }
 
 void launch_forward(bool exact, bool gtab, int mr, int wpb, dim3 grid, size_t lds, hipStream_t s,
@@ -4343,6 +4402,9 @@ int run_forward(const CallSetup& cs, const float* x, const float* vth_pos, const
         }
     }
     set_split(p, ws, fa);
+    if (!cs.exact && !gtab && !fwd_tables_at_lds_zero())
+        return fail(ISA_EKV_EINVAL, "forward: the LDS-table kernels declare static LDS, so their table is not "
+                                          "at LDS address 0 (rebuild without static __shared__ in fwd_kernel)");
     ProfiledLaunch* prof = nullptr;
     if (timed) prof_start(s, 0, &prof);
     if (timed && !cs.exact) fa.clock_acc = clock_acc(0);
@@ -5268,7 +5330,7 @@ int isa_ekv_probe_lds_gather(int window_records, int record_bytes, int iteration
 
 int isa_ekv_probe_valu_issue(int mix, int iterations, const float* tokens, float* out, int64_t out_floats,
                              int64_t* clocks, double* instr_per_cu, int* wall_clock_khz, void* stream) {
-    if (mix < 0 || mix > 2) return fail(ISA_EKV_EINVAL, "mix must be 0, 1 or 2 (got %d)", mix);
+    if (mix < 0 || mix > 3) return fail(ISA_EKV_EINVAL, "mix must be 0, 1, 2 or 3 (got %d)", mix);
     if (iterations < 1 || iterations > (1 << 20))
         return fail(ISA_EKV_EINVAL, "iterations must be in [1, 2^20] (got %d)", iterations);
     if (!tokens) return fail(ISA_EKV_EINVAL, "tokens is null (%d float4 token records)", kValuProbeTokens);
@@ -5294,8 +5356,10 @@ int isa_ekv_probe_valu_issue(int mix, int iterations, const float* tokens, float
         hipLaunchKernelGGL(valu_probe_kernel<0>, dim3(blocks), dim3(threads), lds, s, iterations, tok, out, clk);
     else if (mix == 1)
         hipLaunchKernelGGL(valu_probe_kernel<1>, dim3(blocks), dim3(threads), lds, s, iterations, tok, out, clk);
-    else
+    else if (mix == 2)
         hipLaunchKernelGGL(valu_probe_kernel<2>, dim3(blocks), dim3(threads), lds, s, iterations, tok, out, clk);
+    else
+        hipLaunchKernelGGL(valu_probe_kernel<3>, dim3(blocks), dim3(threads), lds, s, iterations, tok, out, clk);
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "valu probe launch");
     // VALU wave-instructions each CU issues in the loops: two blocks per CU

@@ -614,14 +614,15 @@ def probe_lds_gather(window_records: int, record_bytes: int = 8, iterations: int
     return ms * 1e6 / per_cu.value
 
 
-VALU_MIXES = {"fma": 0, "ranked_backward": 1, "forward": 2}
+VALU_MIXES = {"fma": 0, "ranked_backward": 1, "forward": 2, "forward_int_address": 3}
 
 
 def probe_valu_issue(mix: str, iterations: int = 4096, device: Optional[torch.device] = None,
                      repeats: int = 3) -> dict:
     """VALU wave-instructions a CU issues per shader cycle for one of the table kernels'
     instruction mixes replayed on registers only (isa_ekv_probe_valu_issue): "fma" (32
-    independent fma chains), "ranked_backward" or "forward". One untimed launch, then
+    independent fma chains), "ranked_backward", "forward" or "forward_int_address" (the forward's
+    cell with the cvt and shift-add record address in place of the float-bits one). One untimed launch, then
     `repeats` launches; returns {"instr_per_cu_cycle": median over CUs and launches of the CU's
     loop instructions / the shader cycles of the interval its two blocks kept it busy, "ghz":
     the CUs' shader clock (clock64 / wall_clock64), "ms": mean launch time by HIP events, ...}.
@@ -630,7 +631,7 @@ def probe_valu_issue(mix: str, iterations: int = 4096, device: Optional[torch.de
     code = VALU_MIXES[mix]
     dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    waves = 8 if mix == "forward" else 16
+    waves = 8 if mix.startswith("forward") else 16
     out = torch.empty(2 * cus * 64 * waves, dtype=torch.float32, device=dev)
     clocks = torch.zeros((repeats, 2 * cus, 4), dtype=torch.int64, device=dev)
     g = torch.Generator().manual_seed(1)

@@ -534,7 +534,7 @@ def test_valu_issue_probe(cuda_device):
     a shader clock in the board's range."""
     from isa.kernels.transformer_ffn import ops
 
-    for mix in ("fma", "forward", "ranked_backward"):
+    for mix in ("fma", "forward", "ranked_backward", "forward_int_address"):
         print(f"[case] valu issue probe {mix}", flush=True)
         r = ops.probe_valu_issue(mix, iterations=256, device=cuda_device)
         print(f"  {r}", flush=True)
