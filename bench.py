@@ -439,6 +439,61 @@ def gpt_train_step(args) -> int:
     return 0
 
 
+def _smi_snapshot() -> dict:
+    """The board's firmware counters from `rocm-smi -a --json`: energy accumulator, its clock,
+    and the power-limit (PPT) and thermal residency counters."""
+    out = subprocess.run(["rocm-smi", "-a", "--json"], capture_output=True, text=True, timeout=30).stdout
+    card = json.loads(out)["card0"]
+    num = lambda key: float(card[key])
+    return {"energy_j": num("energy_accumulator (15.259uJ (2^-16))") * 15.259e-6,
+            "ns": num("system_clock_counter (ns)"), "ppt": num("ppt_residency_acc (Count)"),
+            "thm": num("socket_thm_residency_acc (Count)"), "acc": num("accumulation_counter (Count)"),
+            "cap_w": card.get("Max Graphics Package Power (W)"), "gfxclk_mhz": card.get("current_gfxclks (MHz)")}
+
+
+def board_power(step, seconds: float) -> dict:
+    """Mean board power and power-limit residency while `step` runs back to back for `seconds`:
+    two snapshots of the firmware counters taken from a second thread 1 s into the loop and
+    0.5 s before its end, so that both fall inside the run."""
+    import threading
+
+    import torch
+
+    snaps, errors = [], []
+
+    def take():
+        try:
+            time.sleep(1.0)
+            snaps.append(_smi_snapshot())
+            time.sleep(max(0.5, seconds - 2.0))
+            snaps.append(_smi_snapshot())
+        except Exception as e:  # rocm-smi absent or its output without these fields
+            errors.append(repr(e))
+
+    th = threading.Thread(target=take)
+    th.start()
+    t0 = time.perf_counter()
+    steps = 0
+    while time.perf_counter() - t0 < seconds or th.is_alive():
+        step()
+        steps += 1
+        if steps % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    th.join()
+    if errors or len(snaps) != 2:
+        return {"error": errors[0] if errors else "no snapshots"}
+    a, b = snaps
+    dt = (b["ns"] - a["ns"]) * 1e-9
+    ticks = max(1.0, b["acc"] - a["acc"])
+    return {"watts": round((b["energy_j"] - a["energy_j"]) / dt, 1), "interval_s": round(dt, 3),
+            "ppt_residency": round((b["ppt"] - a["ppt"]) / ticks, 4),
+            "thermal_residency": round((b["thm"] - a["thm"]) / ticks, 4),
+            "cap_watts": b["cap_w"], "gfxclk_mhz_per_xcd": b["gfxclk_mhz"], "steps": steps,
+            "source": "rocm-smi -a --json energy accumulator and PPT residency counters, two snapshots inside a "
+                      f"{seconds:.0f} s loop of the step after the timed region"}
+
+
 def lds_roofline(model, cfg: dict, cells_launch: float, fwd_ms: float, bwd_ms: float, dev) -> dict:
     """The table kernels' second bound: their LDS gathers. Each cell-eval gathers 2 records
     (forward: the + and - branch, ds_read_b64) or 4 (backward: the I and D halves of both
@@ -535,6 +590,9 @@ def main() -> int:
     ap.add_argument("--rank-xcd-order", type=int, default=None, choices=[0, 1],
                     help="1: each XCD runs a contiguous range of the ranked backward's blocks "
                          "(ISA_EKV_OPT_RANK_XCD_ORDER); 0: the hardware's round-robin order")
+    ap.add_argument("--power-seconds", type=float, default=0.0,
+                    help="after timing, run the step back to back this long and report the board's mean power "
+                         "and power-limit residency from its firmware counters (board_power; rocm-smi)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -702,6 +760,11 @@ def main() -> int:
         f"{' (graph replay)' if graph is not None else ''} "
         f"(wall {1e3 * wall / args.steps:.3f}), {value:.4e} cell-evals/s")
 
+    power = None
+    if args.power_seconds > 0:
+        power = board_power(graph.replay if graph is not None else step, args.power_seconds)
+        log(f"[bench] board power over the step loop: {power}")
+
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.empty(n, device=dev).uniform_()
@@ -805,6 +868,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "cpu_lut_oracle": lut_cpu,
         "host": host,
+        "board_power": power,
     }
     print(json.dumps(result), flush=True)
     return 0

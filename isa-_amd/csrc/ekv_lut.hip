@@ -4563,10 +4563,12 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
                               (float)g_rank_greedy_min.load(std::memory_order_relaxed)};
             const int64_t threads = p.Kp * p.n_ob * kRankClasses;
             hipLaunchKernelGGL(bwd_rank_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, ra);
-            // the greedy deal of wide spreads (exits at once when the rank deal applies)
+            // the greedy deal of spreads past greedy_min (exits at once when the rank deal
+            // applies); not launched when no spread the ranked mode takes can exceed greedy_min
             const int64_t problems_q = p.Kp * p.n_ob;
-            hipLaunchKernelGGL(bwd_deal_kernel, dim3((unsigned)((problems_q + kDealWaves - 1) / kDealWaves)),
-                               dim3(kDealWaves * 64), 0, s, ra);
+            if (ra.greedy_min < ra.max_spread)
+                hipLaunchKernelGGL(bwd_deal_kernel, dim3((unsigned)((problems_q + kDealWaves - 1) / kDealWaves)),
+                                   dim3(kDealWaves * 64), 0, s, ra);
         }
         // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
         const int64_t problems = p.Kp * (p.Op / (64 * kBwdORR)) * kBwdORR * (p.split ? 4 : 8);
