@@ -116,6 +116,45 @@ def test_parity_input_ranges(cuda_device, x_mode, vth_mode):
     assert e[0] <= FWD_TOL and max(e[1:]) <= BWD_TOL
 
 
+@pytest.mark.parametrize("vth_mode", ["init", "full"])
+def test_parity_grid_aligned_coordinates(cuda_device, vth_mode):
+    """Inputs and thresholds on the table's grid (x = j h, vth = i h, h = (dmax - dmin)/(N - 1),
+    rounded to fp32, and their fp32 neighbours), so that most coordinates fall on or within a few
+    ulps of a record boundary: the ties of the forward's float-bits record address and the
+    segment choice at every boundary, against the oracle. Thresholds near the initial spread
+    (windowed forward copies, ranked backward) and over [0, 5] V."""
+    from isa.approximations.delta_lut import lut_range
+
+    cfg = flash_cfg(4096)
+    dmin, dmax, n = lut_range(cfg)
+    h = (dmax - dmin) / (n - 1)
+    rng = np.random.default_rng(4242 if vth_mode == "init" else 4343)
+    M, K, O = 64, 192, 512
+    j = rng.integers(int(-4.0 / h), int(4.0 / h) + 1, size=(M, K))
+    if vth_mode == "init":  # the initial thresholds' spread (about 69 records) around the middle
+        lo_i, hi_i = int(2.4 / h), int(2.62 / h)
+    else:
+        lo_i, hi_i = 0, int(5.0 / h)
+    ip = rng.integers(lo_i, hi_i + 1, size=(O, K))
+    im = rng.integers(lo_i, hi_i + 1, size=(O, K))
+    x = (j * h).astype(np.float32)
+    nudge = rng.integers(-1, 2, size=x.shape)  # one ulp down, none, one ulp up
+    x = np.where(nudge < 0, np.nextafter(x, np.float32(-np.inf)),
+                 np.where(nudge > 0, np.nextafter(x, np.float32(np.inf)), x)).astype(np.float32)
+    vp = (ip * h).astype(np.float32)
+    vn = (im * h).astype(np.float32)
+    g = rng.standard_normal((M, O)).astype(np.float32)
+    x, vp, vn, g = (torch.from_numpy(np.ascontiguousarray(a)) for a in (x, vp, vn, g))
+    print(f"[case] grid-aligned coordinates, thresholds {vth_mode}", flush=True)
+    ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg, -math.inf, math.inf)
+    modes = {}
+    out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, out_min=-math.inf, out_max=math.inf, modes=modes)
+    e = {"fwd": errs(out, ref_out), "dX": errs(gx, ref_dx), "dVth+": errs(gp, ref_gp), "dVth-": errs(gn, ref_gn)}
+    print(modes, {k: f"{v[0]:.2e}/{v[1]:.2e}" for k, v in e.items()})
+    assert e["fwd"][0] <= FWD_TOL
+    assert e["dX"][0] <= BWD_TOL and e["dVth+"][0] <= BWD_TOL and e["dVth-"][0] <= BWD_TOL
+
+
 @pytest.mark.parametrize("size", [257, 1024, 8192])
 def test_parity_table_sizes(cuda_device, size):
     print(f"[case] table size {size}", flush=True)
