@@ -580,7 +580,7 @@ def main() -> int:
     ap.add_argument("--window-copies", type=int, default=None,
                     help="the most windowed table copies a LUT forward or the two-copy backward may hold "
                          "(isa_ekv_set_option "
-                         "ISA_EKV_OPT_WINDOW_COPIES: 3 to 32, default 16; 0 none)")
+                         "ISA_EKV_OPT_WINDOW_COPIES: 3 to 32, default 32; 0 none)")
     ap.add_argument("--rank-max-spread", type=int, default=None,
                     help="the widest threshold spread (table records) the ranked backward takes "
                          "(isa_ekv_set_option ISA_EKV_OPT_RANK_MAX_SPREAD, default 420)")

@@ -331,7 +331,7 @@ int isa_ekv_plan_info(int which, int64_t M, int64_t K, int64_t O, int n_entries,
  *     backward's blocks (consecutive inputs of one output block and token split, which share
  *     their G rows in that XCD's L2); 0 (default) keeps the hardware's round-robin order.
  *   ISA_EKV_OPT_WINDOW_COPIES: the most bank-rotated copies of the coordinate window (3 to 32;
- *     default 16) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
+ *     default 32) a LUT forward of at least ISA_EKV_OPT_COPY_MIN_CELLS cells may hold in
  *     LDS when its coordinates need no clamp, and a table backward's two-copy launch when the
  *     ranked backward does not apply (decided on the device, which takes the most copies
  *     that fit, two where three do not; mode word = the number of copies, 33 for two): each

@@ -146,10 +146,10 @@ std::atomic<int64_t> g_ranked{1};
 
 // Planning option ISA_EKV_OPT_WINDOW_COPIES: the most bank-rotated copies of the coordinate
 // window a LUT forward, or a table backward's two-copy launch, may hold (3 to 32; below 3
-// neither holds them). At the
-// headline's narrow fc2 window 8, 16 and 32 copies run the forward in the same time within
-// 1%, and the assignment pass costs ~10 us more per doubling: 16.
-std::atomic<int64_t> g_window_copies{16};
+// neither holds them). With record addresses from float bits the forward waits on its LDS
+// reads (index unit 88-92% busy), and at the headline's narrow fc2 window 32 copies run the
+// forward ~2% faster than 16, the assignment pass included: 32.
+std::atomic<int64_t> g_window_copies{32};
 
 // Planning options ISA_EKV_OPT_RANK_MAX_SPREAD / ISA_EKV_OPT_RANK_GREEDY_MIN: the widest threshold
 // spread (table records) the ranked backward takes, and the spread past which its branches are

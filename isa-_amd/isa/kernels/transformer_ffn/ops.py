@@ -96,7 +96,7 @@ def ranked_backward(value: Optional[bool] = None) -> bool:
 
 def window_copies(value: Optional[int] = None) -> int:
     """The library's ISA_EKV_OPT_WINDOW_COPIES (the most windowed table copies a LUT forward, or
-    a table backward's two-copy launch, may hold: 3 to 32, default 16; below 3 none); sets it
+    a table backward's two-copy launch, may hold: 3 to 32, default 32; below 3 none); sets it
     when value is given. Returns the value before
     the call."""
     lib = _hip.load()

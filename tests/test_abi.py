@@ -267,7 +267,7 @@ def test_plan_info_reports_the_call_plans():
         assert ops.window_copies() == 0
     finally:
         ops.window_copies(prev)
-    assert prev == 16
+    assert prev == 32
     # a dVth-only backward runs no copy pair
     assert ops.plan_info("backward", 512, 64, 256, 4096, need_grad_x=False)["mode_offset"] == -1
     info = (ctypes.c_int64 * 7)()

@@ -154,8 +154,8 @@ def _inputs(B, T, D, seed):
 
 
 # the forward's windowed table copies: their number depends on the coordinate window the
-# inputs reach (3 up to ISA_EKV_OPT_WINDOW_COPIES, default 16)
-WINDOWED = range(3, 17)
+# inputs reach (3 up to ISA_EKV_OPT_WINDOW_COPIES, default 32)
+WINDOWED = range(3, 33)
 
 
 def _modes_match(got, want):
@@ -249,23 +249,24 @@ def run_physical_ffn(monkeypatch, dev, D, F, B, T, size, expect_modes, n_rows=48
 def test_config1_vitm_physical_ffn_4096(cuda_device, monkeypatch):
     """configs[1] with the 4096-entry table: the initial thresholds span ~67 records; fc1's
     mapped inputs reach a coordinate window of ~1400 records (as many windowed forward copies
-    as fit its LDS, about seven), fc2's TIA outputs a narrow one (sixteen); the backward runs
+    as fit its LDS, about seven), fc2's TIA outputs a narrow one (the cap, 32); the backward runs
     ranked."""
-    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 4096, ([WINDOWED, 16], [2, 2]))
+    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 4096, ([WINDOWED, 32], [2, 2]))
 
 
 def test_config1_vitm_physical_ffn_8192(cuda_device, monkeypatch):
     """configs[1] with the vision default of 8192 entries: the initial thresholds span ~135
     records and both layers' inputs reach a coordinate window that fits (fc1's mapped inputs in
     [0, 4] V, fc2's TIA outputs within a fraction of a volt of zero): fc1's forward holds three
-    bank-rotated copies of its ~2800-record window (what fits its 80 KB), fc2's sixteen of its
-    narrow one, and every backward runs ranked."""
-    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 8192, ([WINDOWED, 16], [2, 2]))
+    bank-rotated copies of its ~2800-record window (what fits its 80 KB), fc2's as many of its
+    narrow one as fit (about two dozen: twice the records per volt of the 4096-entry table),
+    and every backward runs ranked."""
+    run_physical_ffn(monkeypatch, cuda_device, 256, 1024, 128, 65, 8192, ([WINDOWED, range(16, 33)], [2, 2]))
 
 
 def test_config3_headline_physical_ffn(cuda_device, monkeypatch):
     """configs[3], the headline Physical GPT-L FFN at full size, exactly as bench.py runs it."""
-    run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([WINDOWED, 16], [2, 2]))
+    run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([WINDOWED, 32], [2, 2]))
 
 
 def test_config3_headline_physical_ffn_bf16_tables(cuda_device, monkeypatch):
@@ -273,7 +274,7 @@ def test_config3_headline_physical_ffn_bf16_tables(cuda_device, monkeypatch):
     checked against the oracle fed the same bytes. fc2's inputs are the TIA outputs of the
     initial model, within a fraction of a volt of zero, where the reference's fp32 table
     construction and an fp64-accurate one differ most after the bf16 cast."""
-    run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([WINDOWED, 16], [2, 2]),
+    run_physical_ffn(monkeypatch, cuda_device, 768, 3072, 8, 1024, 4096, ([WINDOWED, 32], [2, 2]),
                      LUT_DTYPE="bfloat16")
 
 
