@@ -470,7 +470,7 @@ def board_power(step, seconds: float) -> dict:
         except Exception as e:  # rocm-smi absent or its output without these fields
             errors.append(repr(e))
 
-    th = threading.Thread(target=take)
+    th = threading.Thread(target=take, daemon=True)
     th.start()
     t0 = time.perf_counter()
     steps = 0
