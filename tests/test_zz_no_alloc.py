@@ -48,7 +48,7 @@ def test_noalloc_forward_table_copies(cuda_device):
     threshold records live in the scratch array. These shapes are far below the library's
     copy threshold (ISA_EKV_OPT_COPY_MIN_CELLS), so the test lowers it to zero, as large
     calls run, and checks the mode the workspace call took: windowed copies (about three of
-    the 8192-entry table's ~2800-record window of mapped inputs, sixteen of the 4096-entry
+    the 8192-entry table's ~2800-record window of mapped inputs, up to 32 of the 4096-entry
     table's narrow window of fc2-like inputs)."""
     from isa.kernels.transformer_ffn import ops
 
