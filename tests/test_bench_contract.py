@@ -55,3 +55,44 @@ def test_bench_json_line(cuda_device, capsys, monkeypatch):
         assert 0 < r["frac"] <= 1.05, r  # a ceiling: the kernel cannot issue faster than its replay
     assert mc["backward"]["kernel"] == "bwd_kernel"  # config 1 is below the copy threshold: one copy
     assert mc["fma_issue_instr_per_cu_cycle"] > 0.25
+
+
+def _smi_json(energy_ticks: float, ns: float, ppt: float, acc: float) -> str:
+    card = {"energy_accumulator (15.259uJ (2^-16))": str(energy_ticks), "system_clock_counter (ns)": str(ns),
+            "ppt_residency_acc (Count)": str(ppt), "socket_thm_residency_acc (Count)": "0",
+            "accumulation_counter (Count)": str(acc), "Max Graphics Package Power (W)": "1400.0",
+            "current_gfxclks (MHz)": "[2100, 2100]"}
+    return json.dumps({"card0": card, "system": {}})
+
+
+def test_board_power_from_firmware_counters(monkeypatch):
+    """bench.board_power: mean power = energy accumulator delta (15.259 uJ ticks) over the
+    firmware clock delta, power-limit residency = PPT count delta over the accumulation count
+    delta, from two rocm-smi snapshots taken while the step loop runs; an absent tool gives an
+    error entry, not a failed bench."""
+    import torch
+
+    import bench
+
+    snaps = iter([_smi_json(1e9, 1e9, 100.0, 1000.0), _smi_json(1e9 + 2.0e8, 3e9, 400.0, 2000.0)])
+
+    class Done:
+        def __init__(self, out):
+            self.stdout = out
+
+    monkeypatch.setattr(bench.subprocess, "run", lambda *a, **k: Done(next(snaps)))
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    calls = []
+    res = bench.board_power(lambda: calls.append(1), 0.5)
+    assert calls, "the step ran while the snapshots were taken"
+    # 2e8 ticks x 15.259 uJ = 3051.8 J over 2 s
+    assert res["watts"] == pytest.approx(2.0e8 * 15.259e-6 / 2.0, rel=1e-6)
+    assert res["ppt_residency"] == pytest.approx(0.3) and res["thermal_residency"] == 0.0
+    assert res["cap_watts"] == "1400.0" and res["interval_s"] == pytest.approx(2.0)
+
+    def missing(*a, **k):
+        raise FileNotFoundError("rocm-smi")
+
+    monkeypatch.setattr(bench.subprocess, "run", missing)
+    res = bench.board_power(lambda: None, 0.5)
+    assert "error" in res and "rocm-smi" in res["error"]
