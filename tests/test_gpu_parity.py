@@ -155,6 +155,27 @@ def test_parity_grid_aligned_coordinates(cuda_device, vth_mode):
     assert e["dX"][0] <= BWD_TOL and e["dVth+"][0] <= BWD_TOL and e["dVth-"][0] <= BWD_TOL
 
 
+@pytest.mark.parametrize("value", [0.0, 4.0])
+def test_parity_constant_inputs(cuda_device, value):
+    """Every input at one of the voltage mapping's clamps (0 V: negative activations; 4 V): all
+    tokens share one coordinate, so the coordinate window is the thresholds' own (~70
+    records), the forward takes the most windowed copies, and the lanes of a gather read a
+    handful of records (broadcasts). Against the oracle, forward and backward."""
+    cfg = flash_cfg(4096)
+    M, K, O = 128, 256, 1024
+    _, vp, vn, g = make_inputs(M, K, O, seed=77)
+    x = torch.full((M, K), value, dtype=torch.float32)
+    print(f"[case] constant inputs {value} V", flush=True)
+    ref_out, ref_dx, ref_gp, ref_gn = oracle_all(x, vp, vn, g, cfg)
+    modes = {}
+    out, gx, gp, gn = _dev_run(x, vp, vn, g, cfg, cuda_device, modes=modes)
+    e = {"fwd": errs(out, ref_out), "dX": errs(gx, ref_dx), "dVth+": errs(gp, ref_gp), "dVth-": errs(gn, ref_gn)}
+    print(modes, {k: f"{v[0]:.2e}/{v[1]:.2e}" for k, v in e.items()})
+    assert 3 <= modes["fwd"] <= 32 and modes["bwd"] == 2, modes
+    assert e["fwd"][0] <= FWD_TOL
+    assert e["dX"][0] <= BWD_TOL and e["dVth+"][0] <= BWD_TOL and e["dVth-"][0] <= BWD_TOL
+
+
 @pytest.mark.parametrize("size", [257, 1024, 8192])
 def test_parity_table_sizes(cuda_device, size):
     print(f"[case] table size {size}", flush=True)
