@@ -2293,13 +2293,22 @@ __global__ __launch_bounds__(256) void bwd_rank_kernel(RankArgs a) {
 // so at kDealSamples token fractions f each instruction keeps, per bank pair, the number of
 // distinct records (saturating at 3) and the first one's id; a record already there costs 0
 // (a broadcast), a new bank pair 1, a bank pair holding n others 2 n + 1 (the growth of the
-// squared load). Ties go to the lowest instruction. Modelled: 0.55 conflict cycles per gather
-// at 135 records, 2.1 at 1576. The 512 choices of a problem are sequential, and the kernel
-// costs ~0.5 ms per GPT-L call (9216 problems): it pays where the ranked kernel saves more.
+// squared load). Ties go to the lowest instruction. Modelled: 0.59 conflict cycles per gather
+// at 135 records, 2.1 at 1576 (with four fractions 0.53 and 2.1); measured 0.49-0.53 at 135.
+// The 512 choices of a problem are sequential: ~0.42 ms per GPT-L call (9216 problems, two per
+// wave, ~33 instructions per placement), the chain of dependent steps with two waves per SIMD.
 // ----------------------------------------------------------------------------------
-constexpr int kDealWaves = 4;     // (input, output block) problems per block, one per wave
-constexpr int kDealSamples = 4;   // token fractions each instruction's bank state is kept at
+constexpr int kDealWaves = 4;     // waves per block
+constexpr int kDealPerWave = 2;   // (input, output block) problems per wave, one per 32-lane half
+constexpr int kDealProblems = kDealWaves * kDealPerWave;  // per block
+constexpr int kDealSamples = 2;   // token fractions each instruction's bank state is kept at
+// bank-state column of one (instruction, fraction), in 16-bit entries: 32 bank pairs and two of
+// padding, so that the 32 lanes of a half, each reading its own column, start 17 LDS banks apart
+// (all distinct), and a problem's 32 columns (1088 entries) put the wave's second problem 32
+// banks on (64-byte columns put every lane of a half on one of four banks)
+constexpr int kDealCol = 34;
 static_assert(kRankClasses == 16 && kRankBranches == 32, "16 classes of 32 branches in 16 instructions");
+static_assert(16 * kDealSamples == 32, "a half-wave: 16 instructions x the fractions");
 
 __device__ inline void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -2307,69 +2316,77 @@ __device__ inline void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// One wave per (input, output block): while ranking, lane = class c x quarter p of its branches;
-// then lane = instruction j (lane / 4) x token fraction (lane % 4), keeping the instruction's
-// bank state at that fraction in LDS (per bank pair 16 bits: the distinct records there, 2
-// bits saturating at 3, and the first one's id). 9 KB per wave: four blocks of four waves per CU.
-__global__ __launch_bounds__(kDealWaves * 64, 4) void bwd_deal_kernel(RankArgs a) {
+// Two problems per wave, one per 32-lane half (a half past the last problem runs on zeros and
+// writes nothing). While ranking, lane = class c x half p of its branches; then lane =
+// instruction j x token fraction qs, owning that instruction's bank state at that fraction in
+// LDS (per bank pair 16 bits: the distinct records there, 2 bits saturating at 3, and the first
+// one's id), so only the cross-lane minima leave a lane. 7 KB per problem: two blocks per CU.
+__global__ __launch_bounds__(kDealWaves * 64, 2) void bwd_deal_kernel(RankArgs a) {
     float spread = 0.0f;
     if (!ranked_mode(a.partials, a.NP, a.max_spread, &spread) || !(spread > a.greedy_min)) return;
-    __shared__ __align__(16) float s_key[kDealWaves][16 * 32];  // [class][branch]; then the dealt [lane][slot]
-    __shared__ __align__(16) float s_sorted[kDealWaves][16 * 32];  // [class][rank]
-    __shared__ unsigned char s_code[kDealWaves][16 * 32];
-    __shared__ __align__(16) unsigned short s_state[kDealWaves][16 * kDealSamples * 32];  // [instruction][fraction][bank pair]
-    __shared__ __align__(16) unsigned char s_bcode[kDealWaves][64 * 8];  // [lane][slot] branch codes
+    __shared__ __align__(16) float s_key[kDealProblems][16 * 32];  // [class][branch]; then the dealt [lane][slot]
+    __shared__ __align__(16) float s_sorted[kDealProblems][16 * 32];  // [class][rank]
+    __shared__ unsigned char s_code[kDealProblems][16 * 32];
+    __shared__ __align__(16) unsigned short s_state[kDealProblems][16 * kDealSamples * kDealCol];  // [instruction][fraction][bank pair]
+    __shared__ __align__(16) unsigned char s_bcode[kDealProblems][64 * 8];  // [lane][slot] branch codes
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int half = lane >> 5, hl = lane & 31;
+    const int pi = wave * kDealPerWave + half;  // the half's problem slot in the block
     const int64_t n_q = (int64_t)a.Kp * a.n_ob;
-    const int64_t q = (int64_t)blockIdx.x * kDealWaves + wave;
-    if (q >= n_q) return;  // wave-uniform: the rest of the kernel syncs within the wave only
-    const int ob = (int)(q % a.n_ob);
-    const int64_t k = q / a.n_ob;
+    const int64_t q0 = ((int64_t)blockIdx.x * kDealWaves + wave) * kDealPerWave;
+    if (q0 >= n_q) return;  // wave-uniform: the rest of the kernel syncs within the wave only
+    const int64_t q = q0 + half;
+    const bool live = q < n_q;  // uniform within the half
 
-    // the class's 32 thresholds in (coordinate, branch) order: lane = class c x quarter p,
-    // holding branches 8 p .. 8 p + 7 (branch i: output c + 16 (i / 2), sign i % 2)
+    // the class's 32 thresholds in (coordinate, branch) order: lane = class c x half p,
+    // holding branches 16 p .. 16 p + 15 (branch i: output c + 16 (i / 2), sign i % 2)
     {
-        const int c = lane & 15, p = lane >> 4;
-        const float2* src = a.wsT + k * a.Op + (int64_t)ob * 256 + c;
-        float key[8];
+        const int c = hl & 15, p = hl >> 4;
+        float key[16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float2 w = src[16 * (4 * p + u)];
-            key[2 * u] = w.x;
-            key[2 * u + 1] = w.y;
+        for (int u = 0; u < 16; ++u) key[u] = 0.0f;
+        if (live) {
+            const int ob = (int)(q % a.n_ob);
+            const int64_t k = q / a.n_ob;
+            const float2* src = a.wsT + k * a.Op + (int64_t)ob * 256 + c;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float2 w = src[16 * (8 * p + u)];
+                key[2 * u] = w.x;
+                key[2 * u + 1] = w.y;
+            }
         }
-        float* kc = &s_key[wave][c * 32];
+        float* kc = &s_key[pi][c * 32];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) kc[8 * p + u] = key[u];
+        for (int u = 0; u < 16; ++u) kc[16 * p + u] = key[u];
         wave_lds_sync();
-        int rank[8];
+        int rank[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) rank[u] = 0;
+        for (int u = 0; u < 16; ++u) rank[u] = 0;
         for (int jj = 0; jj < 32; ++jj) {
             const float kj = kc[jj];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) rank[u] += (kj < key[u] || (kj == key[u] && jj < 8 * p + u)) ? 1 : 0;
+            for (int u = 0; u < 16; ++u) rank[u] += (kj < key[u] || (kj == key[u] && jj < 16 * p + u)) ? 1 : 0;
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = 8 * p + u;
-            s_sorted[wave][c * 32 + rank[u]] = key[u];
-            s_code[wave][c * 32 + rank[u]] = (unsigned char)((i >> 1) | ((i & 1) << 4));
+        for (int u = 0; u < 16; ++u) {
+            const int i = 16 * p + u;
+            s_sorted[pi][c * 32 + rank[u]] = key[u];
+            s_code[pi][c * 32 + rank[u]] = (unsigned char)((i >> 1) | ((i & 1) << 4));
         }
-        unsigned* st32 = reinterpret_cast<unsigned*>(s_state[wave]);
-        for (int u = lane; u < 16 * kDealSamples * 32 / 2; u += 64) st32[u] = 0u;
+        unsigned* st32 = reinterpret_cast<unsigned*>(s_state[pi]);
+        for (int u = hl; u < 16 * kDealSamples * kDealCol / 2; u += 32) st32[u] = 0u;
         wave_lds_sync();
     }
 
-    // the greedy, one branch per step (class t / 32, rank t % 32). The chain from one step's
-    // choice to the next step's costs is what the time goes to, so each step reads the next
+    // the greedy, one branch per step (class t / 32, rank t % 32). Each step reads the next
     // step's threshold and bank entry before it writes its own update, and patches the entry
     // when both steps touch the same one.
-    const int j = lane >> 2, qs = lane & 3;  // this lane's instruction and token fraction
+    const int j = hl >> 1, qs = hl & 1;  // this lane's instruction and token fraction
     const float frac = ((float)qs + 0.5f) / (float)kDealSamples;
-    unsigned short* st = s_state[wave] + (j * kDealSamples + qs) * 32;
-    const float* srt = s_sorted[wave];
-    float* s_out = s_key[wave];  // the keys are dead once sorted
+    unsigned short* st = s_state[pi] + (j * kDealSamples + qs) * kDealCol;
+    const float* srt = s_sorted[pi];
+    float* s_out = s_key[pi];  // the keys are dead once sorted
     float w = srt[0];
     int rec = (int)floorf(frac - w);
     int b = rec & 31;
@@ -2382,17 +2399,17 @@ __global__ __launch_bounds__(kDealWaves * 64, 4) void bwd_deal_kernel(RankArgs a
         unsigned en = st[bn];
         const unsigned n = e >> 14, id = e & 0x3FFFu, rid = (unsigned)rec & 0x3FFFu;
         int cost = n == 0u ? 1 : (id == rid ? 0 : 2 * (int)n + 1);
-        cost += __builtin_amdgcn_update_dpp(0, cost, 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
-        cost += __builtin_amdgcn_update_dpp(0, cost, 0x4e, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+        cost += __builtin_amdgcn_update_dpp(0, cost, 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2: the pair
         // the cheapest instruction with room, ties to the lowest: min of cost x 16 + j over the
-        // wave (4 fractions x (2 x 3 + 1) bound a cost by 28; one instruction always has room):
-        // the quads of a 16-lane row by two row rotations, the rows in scalar code
+        // half (2 fractions x (2 x 3 + 1) bound a cost by 14; one instruction always has room):
+        // a row's eight instructions by three row rotations, then the half's two rows by a
+        // lane swap (rows 0-1 and 2-3: each half separately)
         int key = cap < 2 ? (cost << 4) | j : 0xFFFF;
+        key = min(key, __builtin_amdgcn_update_dpp(0xFFFF, key, 0x122, 0xf, 0xf, false));  // row_ror:2
         key = min(key, __builtin_amdgcn_update_dpp(0xFFFF, key, 0x124, 0xf, 0xf, false));  // row_ror:4
         key = min(key, __builtin_amdgcn_update_dpp(0xFFFF, key, 0x128, 0xf, 0xf, false));  // row_ror:8
-        const int k01 = min(__builtin_amdgcn_readlane(key, 0), __builtin_amdgcn_readlane(key, 16));
-        const int k23 = min(__builtin_amdgcn_readlane(key, 32), __builtin_amdgcn_readlane(key, 48));
-        const int jstar = min(k01, k23) & 15;
+        const auto rw = __builtin_amdgcn_permlane16_swap((unsigned)key, (unsigned)key, false, false);
+        const int jstar = min((int)rw[0], (int)rw[1]) & 15;
         if (j == jstar) {
             const unsigned eu = n == 0u ? ((1u << 14) | rid) : (id == rid ? e : ((min(n + 1u, 3u) << 14) | id));
             st[b] = (unsigned short)eu;
@@ -2401,7 +2418,7 @@ __global__ __launch_bounds__(kDealWaves * 64, 4) void bwd_deal_kernel(RankArgs a
                 const int c = t >> 5;
                 const int L = c + 16 * cap + 32 * (jstar >> 3), slot = jstar & 7;
                 s_out[L * 8 + slot] = w;
-                s_bcode[wave][L * 8 + slot] = s_code[wave][t];
+                s_bcode[pi][L * 8 + slot] = s_code[pi][t];
             }
             ++cap;
         }
@@ -2412,12 +2429,12 @@ __global__ __launch_bounds__(kDealWaves * 64, 4) void bwd_deal_kernel(RankArgs a
         e = en;
     }
     wave_lds_sync();
-    float4* out = reinterpret_cast<float4*>(a.ws_ranked + q * 64 * 8);
-    const float4* so = reinterpret_cast<const float4*>(s_out);
-    out[lane] = so[lane];
-    out[lane + 64] = so[lane + 64];
-    const uint2 bc = *reinterpret_cast<const uint2*>(&s_bcode[wave][lane * 8]);
-    a.branch[q * 64 + lane] = bc;
+    if (live) {
+        float4* out = reinterpret_cast<float4*>(a.ws_ranked + q * 64 * 8);
+        const float4* so = reinterpret_cast<const float4*>(s_out);
+        for (int i = hl; i < 64 * 8 / 4; i += 32) out[i] = so[i];
+        for (int i = hl; i < 64; i += 32) a.branch[q * 64 + i] = *reinterpret_cast<const uint2*>(&s_bcode[pi][i * 8]);
+    }
 }
 
 // Block = kRankWaves waves: inputs kg*W .. kg*W+W-1 (one per wave), one output block, one token split.
@@ -4567,7 +4584,7 @@ int run_backward(const CallSetup& cs, const float* x, const float* vth_pos, cons
             // applies); not launched when no spread the ranked mode takes can exceed greedy_min
             const int64_t problems_q = p.Kp * p.n_ob;
             if (ra.greedy_min < ra.max_spread)
-                hipLaunchKernelGGL(bwd_deal_kernel, dim3((unsigned)((problems_q + kDealWaves - 1) / kDealWaves)),
+                hipLaunchKernelGGL(bwd_deal_kernel, dim3((unsigned)((problems_q + kDealProblems - 1) / kDealProblems)),
                                    dim3(kDealWaves * 64), 0, s, ra);
         }
         // split tables: 8-byte records (half-wave banks); interleaved: 16-byte (quarter-wave)
