@@ -763,6 +763,8 @@ def main() -> int:
     power = None
     if args.power_seconds > 0:
         power = board_power(graph.replay if graph is not None else step, args.power_seconds)
+        if "watts" in power:  # the board's energy per cell-eval at the timed rate
+            power["nj_per_cell_eval"] = round(power["watts"] / value * 1e9, 4)
         log(f"[bench] board power over the step loop: {power}")
 
     if args.copy_calibration_mib > 0:
