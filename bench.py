@@ -466,7 +466,14 @@ def board_power(step, seconds: float) -> dict:
             time.sleep(1.0)
             snaps.append(_smi_snapshot())
             time.sleep(max(0.5, seconds - 2.0))
-            snaps.append(_smi_snapshot())
+            # the firmware refreshes its counters periodically: read again (a few times at most)
+            # until its clock has moved on by half a second
+            for _ in range(8):
+                last = _smi_snapshot()
+                if last["ns"] - snaps[0]["ns"] >= 0.5e9:
+                    break
+                time.sleep(0.5)
+            snaps.append(last)
         except Exception as e:  # rocm-smi absent or its output without these fields
             errors.append(repr(e))
 
@@ -485,6 +492,8 @@ def board_power(step, seconds: float) -> dict:
         return {"error": errors[0] if errors else "no snapshots"}
     a, b = snaps
     dt = (b["ns"] - a["ns"]) * 1e-9
+    if dt <= 0.0:
+        return {"error": "the firmware counters did not advance between the snapshots"}
     ticks = max(1.0, b["acc"] - a["acc"])
     return {"watts": round((b["energy_j"] - a["energy_j"]) / dt, 1), "interval_s": round(dt, 3),
             "ppt_residency": round((b["ppt"] - a["ppt"]) / ticks, 4),
@@ -590,9 +599,9 @@ def main() -> int:
     ap.add_argument("--rank-xcd-order", type=int, default=None, choices=[0, 1],
                     help="1: each XCD runs a contiguous range of the ranked backward's blocks "
                          "(ISA_EKV_OPT_RANK_XCD_ORDER); 0: the hardware's round-robin order")
-    ap.add_argument("--power-seconds", type=float, default=0.0,
+    ap.add_argument("--power-seconds", type=float, default=6.0,
                     help="after timing, run the step back to back this long and report the board's mean power "
-                         "and power-limit residency from its firmware counters (board_power; rocm-smi)")
+                         "and power-limit residency from its firmware counters (board_power; rocm-smi); 0 skips")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")

@@ -27,9 +27,9 @@ def test_more_than_one_gpu_is_refused():
 def test_bench_json_line(cuda_device, capsys, monkeypatch):
     import bench
 
-    print("[case] bench.py --config vits_up --steps 2 --warmup 1 --no-cpu-baseline", flush=True)
+    print("[case] bench.py --config vits_up --steps 2 --warmup 1 --no-cpu-baseline --power-seconds 2", flush=True)
     monkeypatch.setattr(sys, "argv", ["bench.py", "--config", "vits_up", "--steps", "2", "--warmup", "1",
-                                      "--no-cpu-baseline"])
+                                      "--no-cpu-baseline", "--power-seconds", "2"])
     assert bench.main() == 0
     lines = [ln for ln in capsys.readouterr().out.splitlines() if ln.startswith("{")]
     assert len(lines) == 1
@@ -38,6 +38,10 @@ def test_bench_json_line(cuda_device, capsys, monkeypatch):
     assert rec["n_gpus"] == 1 and rec["steps"] == 2 and rec["warmup"] == 1
     assert rec["value"] > 0 and rec["ms_per_step"] > 0 and rec["higher_is_better"] is True
     assert "workload" in rec["config"]
+    # the board power leg: the firmware counters' reading, or why there is none
+    bp = rec["board_power"]
+    assert ("watts" in bp and bp["watts"] > 0 and 0.0 <= bp["ppt_residency"] <= 1.0 and bp["nj_per_cell_eval"] > 0) \
+        or "error" in bp, bp
     roof = rec["roofline"]
     assert {"bound", "achieved", "peak", "unit", "frac", "traffic"} <= set(roof)
     assert 0 < roof["frac"] < 2 and roof["achieved"] > 0
@@ -96,3 +100,14 @@ def test_board_power_from_firmware_counters(monkeypatch):
     monkeypatch.setattr(bench.subprocess, "run", missing)
     res = bench.board_power(lambda: None, 0.5)
     assert "error" in res and "rocm-smi" in res["error"]
+
+    # a firmware sample that has not moved on is read again, and one that never does gives an
+    # error entry, not a division by zero
+    stale = iter([_smi_json(1e9, 1e9, 0.0, 1000.0)] * 3 + [_smi_json(1e9 + 1e8, 2e9, 0.0, 1500.0)])
+    monkeypatch.setattr(bench.subprocess, "run", lambda *a, **k: Done(next(stale)))
+    monkeypatch.setattr(bench.time, "sleep", lambda s: None)
+    res = bench.board_power(lambda: None, 0.5)
+    assert res["interval_s"] == pytest.approx(1.0) and res["watts"] == pytest.approx(1e8 * 15.259e-6)
+    monkeypatch.setattr(bench.subprocess, "run", lambda *a, **k: Done(_smi_json(1e9, 1e9, 0.0, 1000.0)))
+    res = bench.board_power(lambda: None, 0.5)
+    assert "did not advance" in res["error"]
