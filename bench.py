@@ -503,6 +503,47 @@ def board_power(step, seconds: float) -> dict:
                       f"{seconds:.0f} s loop of the step after the timed region"}
 
 
+def power_phases(cfg: dict, d_model: int, d_ffn: int, tokens: int, dev, seconds: float) -> dict:
+    """board_power for one kernel family at a time: the first CIM layer's table backward and
+    table forward through the library's ops (the workload's fc1 shapes, mapped inputs
+    clamp(N(0,1), 0, 4), the reference's initial thresholds), the register-only VALU replay of
+    independent fmas, and the LDS gather probe at the thresholds' window; then the idle board."""
+    import torch
+
+    from isa.approximations.delta_lut import get_packed_tables, lut_range
+    from isa.kernels.transformer_ffn import ops
+
+    dmin, dmax, n = lut_range(cfg)
+    fwd_t, bwd_t = get_packed_tables(cfg, dev)
+    g = torch.Generator().manual_seed(0)
+    lo = 2.5 - 0.5 * 2 * cfg["n"] * cfg["U_T"]
+    hi = 2.5 + 0.5 * 2 * cfg["n"] * cfg["U_T"]
+    x = torch.randn(tokens, d_model, generator=g).clamp(0.0, 4.0).to(dev)
+    vp = torch.empty(d_ffn, d_model).uniform_(lo, hi, generator=g).to(dev)
+    vn = torch.empty(d_ffn, d_model).uniform_(lo, hi, generator=g).to(dev)
+    grad = torch.randn(tokens, d_ffn, generator=g).to(dev)
+    pf = ops.plan_info("forward", tokens, d_model, d_ffn, n)
+    pb = ops.plan_info("backward", tokens, d_model, d_ffn, n, True, True)
+    wsf = torch.empty(pf["workspace_bytes"], dtype=torch.uint8, device=dev)
+    wsb = torch.empty(pb["workspace_bytes"], dtype=torch.uint8, device=dev)
+    phases = {
+        "table_backward": lambda: ops.lut_backward(x, vp, vn, grad, bwd_t, n, dmin, dmax, cfg["V_sat"], True, True,
+                                                   workspace=wsb),
+        "table_forward": lambda: ops.lut_forward(x, vp, vn, fwd_t, n, dmin, dmax, cfg["V_sat"], -4.0, 4.0,
+                                                 workspace=wsf),
+        "valu_replay_fma": lambda: ops.probe_valu_issue("fma", iterations=16384, device=dev, repeats=1),
+        "lds_gather_probe": lambda: ops.probe_lds_gather(69, 8, iterations=8192, device=dev, repeats=1),
+        "idle": lambda: time.sleep(0.05),
+    }
+    out = {"workload": f"fc1 {tokens} x {d_model} -> {d_ffn}, mapped inputs, initial thresholds"}
+    for name, fn in phases.items():
+        fn()
+        torch.cuda.synchronize()
+        out[name] = board_power(fn, seconds)
+        log(f"[bench] board power, {name}: {out[name]}")
+    return out
+
+
 def lds_roofline(model, cfg: dict, cells_launch: float, fwd_ms: float, bwd_ms: float, dev) -> dict:
     """The table kernels' second bound: their LDS gathers. Each cell-eval gathers 2 records
     (forward: the + and - branch, ds_read_b64) or 4 (backward: the I and D halves of both
@@ -602,6 +643,9 @@ def main() -> int:
     ap.add_argument("--power-seconds", type=float, default=6.0,
                     help="after timing, run the step back to back this long and report the board's mean power "
                          "and power-limit residency from its firmware counters (board_power; rocm-smi); 0 skips")
+    ap.add_argument("--power-phases", type=float, default=0.0,
+                    help="after the run, board_power for one kernel family at a time, this many seconds each "
+                         "(board_power_phases: table backward, table forward, VALU replay, LDS probe, idle)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run one plain device-to-device copy of this many MiB (a reference "
                          "kernel of known HBM traffic for counter runs)")
@@ -776,6 +820,10 @@ def main() -> int:
             power["nj_per_cell_eval"] = round(power["watts"] / value * 1e9, 4)
         log(f"[bench] board power over the step loop: {power}")
 
+    phases = None
+    if args.power_phases > 0 and args.ekv_approx == "lut":
+        phases = power_phases(cfg, layers[0][1], layers[0][2], layers[0][0], dev, args.power_phases)
+
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.empty(n, device=dev).uniform_()
@@ -880,6 +928,7 @@ def main() -> int:
         "cpu_lut_oracle": lut_cpu,
         "host": host,
         "board_power": power,
+        "board_power_phases": phases,
     }
     print(json.dumps(result), flush=True)
     return 0
