@@ -100,7 +100,7 @@ int isa_ekv_forward(const float* x, const float* vth_pos, const float* vth_neg, 
  * ends; shapes whose forward needs more (isa_ekv_plan_info slot [0]) are rejected with
  * ISA_EKV_EINVAL before anything is enqueued. All calls on one device share that array:
  * calls that overlap on a device (different streams, or threads without ordering) race. */
-#define ISA_EKV_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+#define ISA_EKV_NOALLOC_MAX_BYTES ((size_t)128 << 20)
 int isa_ekv_forward_noalloc(const float* x, const float* vth_pos, const float* vth_neg, const void* lut_fwd,
                             int64_t M, int64_t K, int64_t O, int n_entries, float delta_min, float delta_max,
                             float v_sat, float out_min, float out_max, float* out, void* stream);

@@ -4911,7 +4911,7 @@ int run_measured_backward(const float* x, const short* ids_a, const short* ids_b
 // needs clearing between calls; calls that overlap on one device share the array and race.
 // ----------------------------------------------------------------------------------
 
-constexpr size_t kScratchBytes = ISA_EKV_NOALLOC_MAX_BYTES;  // 64 MiB per device
+constexpr size_t kScratchBytes = ISA_EKV_NOALLOC_MAX_BYTES;  // 128 MiB per device (the GPT-L fc1 forward needs 66)
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {

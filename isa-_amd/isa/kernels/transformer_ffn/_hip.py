@@ -26,7 +26,7 @@ PLAN_FORWARD = 0
 PLAN_BACKWARD = 1
 PLAN_LAYER_BACKWARD = 2
 PLAN_INFO_LEN = 8
-NOALLOC_MAX_BYTES = 64 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
+NOALLOC_MAX_BYTES = 128 << 20  # ISA_EKV_NOALLOC_MAX_BYTES
 OPT_COPY_MIN_CELLS = 1
 OPT_RANKED = 2
 OPT_WINDOW_COPIES = 3

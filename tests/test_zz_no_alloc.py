@@ -1,8 +1,8 @@
 """isa_ekv_forward_noalloc (the forward without a workspace argument, for callers that
 cannot allocate) against isa_ekv_forward, through the C ABI: the same kernels on the same
 inputs, so outputs must be bitwise equal. Two calls in a row, the second smaller than the
-first (the scratch array keeps the first call's contents), then a call in the windowed
-two-copy regime of the 8192-entry table, and the size limit."""
+first (the scratch array keeps the first call's contents), then calls in the windowed
+table-copy regimes, the headline fc1 forward, and the size limit."""
 
 from __future__ import annotations
 
@@ -67,12 +67,28 @@ def test_noalloc_forward_table_copies(cuda_device):
         ops.copy_min_cells(prev)
 
 
+def test_noalloc_forward_headline_fc1(cuda_device):
+    """The GPT-L fc1 forward (8192 x 768 -> 3072, 66 MiB of scratch): windowed table copies
+    at the library's default options, as the headline runs it."""
+    from isa.kernels.transformer_ffn import _hip, ops
+
+    cfg = flash_cfg(4096)
+    M, K, O = 8192, 768, 3072
+    print(f"[case] noalloc forward headline fc1 M={M} K={K} O={O}", flush=True)
+    assert ops.plan_info("forward", M, K, O, 4096)["workspace_bytes"] <= _hip.NOALLOC_MAX_BYTES
+    x, vp, vn, _ = make_inputs(M, K, O, seed=11, x_mode="mapped")
+    ref, out, mode = _both(x, vp, vn, cfg, cuda_device)
+    print(f"  mode {mode}", flush=True)
+    assert mode is not None and 3 <= mode <= 33, mode
+    assert torch.equal(out, ref)
+
+
 def test_noalloc_forward_rejects_oversized_shapes(cuda_device):
     from isa.approximations.delta_lut import get_packed_tables, lut_range
     from isa.kernels.transformer_ffn import _hip, ops
 
     cfg = flash_cfg(4096)
-    M, K, O = 8192, 768, 3072  # headline fc1: ~69 MB of workspace
+    M, K, O = 8192, 3072, 768  # headline fc2: 306 MiB of workspace (token records, K-split planes)
     assert ops.plan_info("forward", M, K, O, 4096)["workspace_bytes"] > _hip.NOALLOC_MAX_BYTES
     dmin, dmax, n = lut_range(cfg)
     fwd, _ = get_packed_tables(cfg, cuda_device)
