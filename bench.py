@@ -224,7 +224,12 @@ def measured_ceiling(kt, cells_launch: float, fwd_ms: float, bwd_ms: float, dev)
         ghz, n = clk["ghz"], per_cell.get(name)
         res = {"kernel": name, "kernel_ghz": round(ghz, 4) if ghz else None, "issued_valu_per_cell": n,
                "replay_mix": mix, "replay_instr_per_cu_cycle": round(probes[mix]["instr_per_cu_cycle"], 4),
-               "avg_launch_ms": round(avg_ms, 4)}
+               "avg_launch_ms": round(avg_ms, 4),
+               # a block's first wave from entry to exit, averaged over every block of the timed
+               # launches: against avg_launch_ms it shows how much of a one-round launch (small
+               # calls) lies outside its blocks, in the dispatch of their start and the drain
+               "mean_block_lifetime_ms": round(clk["block_seconds"] / clk["blocks"] * 1e3, 5)
+               if clk["blocks"] else None}
         if ghz and n and avg_ms:
             wave_instr = n * cells_launch / 64.0
             ceiling_ms = wave_instr / (probes[mix]["instr_per_cu_cycle"] * cus * ghz * 1e9) * 1e3
@@ -240,7 +245,7 @@ def measured_ceiling(kt, cells_launch: float, fwd_ms: float, bwd_ms: float, dev)
         "replay_ghz": {m: round(p.get("ghz", 0.0), 4) for m, p in probes.items()},
         "source": "issued_valu_per_cell: profiles/counters_gptl_ffn_bench.md (rocprofv3 SQ_INSTS_VALU, not this "
                   "run); kernel_ghz: clock64 / wall_clock64 of every block of the kernel during the timed steps "
-                  "(isa_ekv_profile_clock); replay: isa_ekv_probe_valu_issue after the timed steps (the kernel's "
+                  "(isa_ekv_profile_clock), mean_block_lifetime_ms: the same blocks' wall time each; replay: isa_ekv_probe_valu_issue after the timed steps (the kernel's "
                   "VALU mix on registers only, at its occupancy; the one- and two-copy backwards are priced "
                   "with the ranked backward's mix)",
     }

@@ -57,6 +57,8 @@ def test_bench_json_line(cuda_device, capsys, monkeypatch):
         assert 0.5 < r["kernel_ghz"] < 3.5, r  # the clock the kernel's own blocks ran at
         assert r["issued_valu_per_cell"] > 0 and r["replay_instr_per_cu_cycle"] > 0.25, r
         assert 0 < r["frac"] <= 1.05, r  # a ceiling: the kernel cannot issue faster than its replay
+        # its blocks live within the launch (one round of blocks at config 1's size)
+        assert 0 < r["mean_block_lifetime_ms"] <= r["avg_launch_ms"], r
     assert mc["backward"]["kernel"] == "bwd_kernel"  # config 1 is below the copy threshold: one copy
     assert mc["fma_issue_instr_per_cu_cycle"] > 0.25
 
